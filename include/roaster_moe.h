@@ -1,0 +1,137 @@
+/*
+ * roaster_moe.h -- MI355X-native entry points of the MoE-FFN hot path that have
+ * no one-to-one counterpart in the reference's kernels.h.  They replace the
+ * reference's per-layer host loop around the kernels (model.c:1059-1146 decode,
+ * model.c:1671-1791 prefill) and its SSD expert cache (weights.c:420-652,
+ * 952-1112) with an HBM-resident expert table and whole-layer GPU launches.
+ *
+ * Conventions: all tensors are row-major f32 unless stated; every pointer
+ * argument of the decode / prefill calls is a DEVICE pointer (allocate with
+ * roaster_dev_alloc, or pass any HIP device allocation); calls are ordered on
+ * the library's stream (roaster_stream) and return after launch, except where
+ * noted.  Return codes: ROASTER_OK or a negative ROASTER_E* (message in
+ * roaster_last_error()).  Calls that overlap from several host threads are
+ * serialised by an internal lock.
+ */
+#ifndef ROASTER_MOE_H
+#define ROASTER_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ROASTER_OK        0
+#define ROASTER_EINVAL   (-1)   /* bad argument / shape */
+#define ROASTER_EDEVICE  (-2)   /* HIP runtime or launch failure */
+#define ROASTER_EROUTE   (-3)   /* fewer than 8 finite router logits (model.c:1074-1075, 1688) */
+#define ROASTER_ENOMEM   (-4)
+
+/* Matrix kinds of an expert. */
+#define ROASTER_GATE 0
+#define ROASTER_UP   1
+#define ROASTER_DOWN 2
+
+/* Prefill arithmetic. */
+#define ROASTER_PREC_BF16  0   /* bf16 MFMA operands, fp32 accumulate (tolerance 2e-3 of |y|inf) */
+#define ROASTER_PREC_SPLIT 1   /* hi+lo bf16 split of both operands, 3 MFMAs (tolerance 2e-4) */
+
+/* ---- runtime ------------------------------------------------------------ */
+const char *roaster_last_error(void);
+int   roaster_init(void);               /* idempotent; every entry point calls it */
+void *roaster_stream(void);             /* the hipStream_t all launches use */
+int   roaster_sync(void);               /* wait for the stream; reports kernel-side errors */
+int   roaster_device_info(int *n_cu, int *n_xcd, size_t *hbm_bytes);
+void *roaster_dev_alloc(size_t bytes);
+void  roaster_dev_free(void *p);
+int   roaster_h2d(void *dst, const void *src, size_t bytes);   /* synchronous */
+int   roaster_d2h(void *dst, const void *src, size_t bytes);   /* synchronous */
+int   roaster_memset(void *dst, int value, size_t bytes);      /* stream-ordered */
+
+/* ---- HBM-resident expert table (replaces weights.c's per-layer LRU cache) -- */
+typedef struct {
+    int    n_layers;      /* 40 */
+    int    n_experts;     /* routed experts per layer, 256 */
+    size_t hidden;        /* 2048, multiple of 256 */
+    size_t inter;         /* 512, multiple of 256 */
+    int    q6[3];         /* routed gate / up / down type: 0 = Q4_K, 1 = Q6_K */
+    int    sh_q6[3];      /* shared expert gate / up / down type */
+} RoasterTableDesc;
+
+typedef struct RoasterTable RoasterTable;
+
+RoasterTable *roaster_table_create(const RoasterTableDesc *desc);
+void   roaster_table_destroy(RoasterTable *t);
+size_t roaster_table_bytes(const RoasterTable *t);
+/* Upload one expert's three matrices from host memory (expert == n_experts is
+ * the shared expert).  Synchronous.  weights.c:380-419 slices the same bytes
+ * out of the GGUF *_exps tensors. */
+int roaster_table_set_expert(RoasterTable *t, int layer, int expert,
+                             const void *gate, const void *up, const void *down);
+/* Upload one whole [n_experts][rows][row_bytes] GGUF tensor of `kind`. */
+int roaster_table_set_exps(RoasterTable *t, int layer, int kind, const void *data, size_t bytes);
+/* Router [n_experts x hidden] and shared-expert gate vector [hidden], host f32. */
+int roaster_table_set_router(RoasterTable *t, int layer, const float *router, const float *shexp_gate_inp);
+/* Device addresses of an expert's matrices (usable as kernels.h weight pointers). */
+int roaster_table_expert_ptrs(const RoasterTable *t, int layer, int expert,
+                              const void **gate, const void **up, const void **down);
+
+/* ---- synthetic inputs (deterministic; identical on host and device) ------ */
+typedef struct {
+    float q4k_lo, q4k_hi;     /* Q4_K d and dmin ~ f16(U(lo, hi)); default 1e-3, 2e-2 */
+    float q6k_lo, q6k_hi;     /* Q6_K d ~ f16(U(lo, hi)); default 1e-3, 1e-2 */
+    float router_sigma;       /* router ~ N(0, sigma^2); default 0.02 */
+    float gate_inp_sigma;     /* shared gate vector ~ N(0, sigma^2); default 0.02 */
+} RoasterSynthSpec;
+
+/* Stream id of (layer, expert, kind); kind 0..2 = matrices, 3 = router, 4 = gate vector. */
+uint64_t roaster_synth_stream(int layer, int expert, int kind);
+void roaster_synth_q4k(uint64_t seed, uint64_t stream, size_t nblocks, float lo, float hi, void *out);
+void roaster_synth_q6k(uint64_t seed, uint64_t stream, size_t nblocks, float lo, float hi, void *out);
+void roaster_synth_normal(uint64_t seed, uint64_t stream, size_t n, float sigma, float *out);
+/* Fill every matrix of the table on the device and upload host-generated
+ * routers / gate vectors.  spec may be NULL (defaults).  Synchronous. */
+int roaster_table_synth(RoasterTable *t, uint64_t seed, const RoasterSynthSpec *spec);
+
+/* ---- decode: one launch per call ---------------------------------------- */
+typedef struct {
+    const float *logits_in;   /* [B x E]: replaces the router matvec, or NULL */
+    float *logits_out;        /* [B x E] or NULL */
+    int   *ids_out;           /* [B x 8] selected experts, descending logit, or NULL */
+    float *w_out;             /* [B x 8] renormalised weights, or NULL */
+} RoasterDecodeIO;
+
+/* y[b] = sum_k w[b,k] * expert_{id[b,k]}(x[b]) + sigmoid(gate_inp . x[b]) * shared(x[b])
+ * for B (1..8) independent tokens: model.c:1059-1146 per token. */
+int roaster_moe_decode(RoasterTable *t, int layer, const float *x, int B, float *y,
+                       const RoasterDecodeIO *io);
+
+/* The layer stack with the hidden state on the GPU:
+ *   for l in [layer0, layer0 + n_layers): h += MoE_l(RMSNorm(h; norm_w[l - layer0], eps))
+ * (model.c:1352-1358 without the mixer).  norm_w is [n_layers x hidden] or NULL
+ * (all ones).  ids_out / w_out: [n_layers x B x 8] or NULL.  One launch. */
+int roaster_moe_decode_stack(RoasterTable *t, float *h, int B, int layer0, int n_layers,
+                             const float *norm_w, float eps, int *ids_out, float *w_out);
+
+/* ---- prefill ------------------------------------------------------------ */
+typedef struct {
+    int precision;             /* ROASTER_PREC_BF16 (default) or ROASTER_PREC_SPLIT */
+    const float *logits_in;    /* [T x E] replaces the router matmul, or NULL */
+    const float *logit_bias;   /* [E] added to every token's logits, or NULL */
+    float *logits_out;         /* [T x E] or NULL */
+    int   *ids_out;            /* [T x 8] or NULL */
+    float *w_out;              /* [T x 8] or NULL */
+    int   *counts_out;         /* [E] tokens per expert, or NULL */
+} RoasterPrefillOpts;
+
+/* Y[t] = sigmoid(gate_inp . X[t]) * shared(X[t]) + sum over t's experts in
+ * ascending id of w * expert(X[t]) -- model.c:1671-1791.  X, Y: [T x hidden]. */
+int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, int T, float *Y,
+                        const RoasterPrefillOpts *opts);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

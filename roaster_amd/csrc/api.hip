@@ -1,0 +1,540 @@
+/*
+ * api.hip -- the C-ABI: kernels.h entry points on host buffers and the
+ * table-based decode entry points of roaster_moe.h.
+ *
+ * Host-buffer entry points follow the reference's contract (kernels.c): they
+ * are synchronous, the caller owns every buffer, and weight pointers are
+ * translated to their HBM copy.  Unlike the reference there is no CPU
+ * fallback: a device failure is printed and reported through the return value
+ * (or NaN outputs for signatures without one).
+ */
+#include "internal.h"
+#include "decode.h"
+#include "matvec.h"
+#include "table.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <vector>
+
+typedef std::lock_guard<std::recursive_mutex> Guard;
+
+static void fill_nan(float *p, size_t n)
+{
+    for (size_t i = 0; i < n; i++) p[i] = NAN;
+}
+
+/* ---- quantised matvec batch (split-phase) ---------------------------------- */
+struct Pending {
+    int open;
+    const KernelMatvecJob *jobs;
+    int n;
+    std::vector<size_t> out_off;
+    float *stage;            /* pinned copy of all outputs */
+    int failed;
+};
+static Pending g_pend;
+
+static int mv_upload_and_launch(const KernelMatvecJob *jobs, int n)
+{
+    RtState &R = rt();
+    /* device layout: [vectors (deduplicated by pointer+cols)] [outputs] */
+    std::vector<size_t> voff(n), ooff(n);
+    std::vector<int> owner(n);
+    size_t vtot = 0, otot = 0;
+    for (int i = 0; i < n; i++) {
+        const KernelMatvecJob &j = jobs[i];
+        if (!j.matrix || !j.vector || !j.output || !j.rows || !j.cols || j.cols % RQK || j.rows > 0x7FFFFFFF)
+            return rt_fail(ROASTER_EINVAL, "kernel_matvec_quant: invalid job %d (cols must be a multiple of 256)", i);
+        owner[i] = i;
+        for (int p = 0; p < i; p++)
+            if (owner[p] == p && jobs[p].vector == j.vector && jobs[p].cols == j.cols) { owner[i] = p; break; }
+        if (owner[i] == i) { voff[i] = vtot; vtot += (j.cols * 4 + 255) & ~(size_t)255; }
+        else voff[i] = voff[owner[i]];
+        ooff[i] = otot;
+        otot += (j.rows * 4 + 255) & ~(size_t)255;
+    }
+    uint8_t *dv = (uint8_t *)rt_scratch(SCR_IN, vtot);
+    uint8_t *dout = (uint8_t *)rt_scratch(SCR_OUT, otot);
+    MvJob *djobs = (MvJob *)rt_scratch(SCR_A, sizeof(MvJob) * n);
+    uint8_t *pin = (uint8_t *)rt_pinned(0, vtot + sizeof(MvJob) * n);
+    float *stage = (float *)rt_pinned(1, otot);
+    if (!dv || !dout || !djobs || !pin || !stage) return ROASTER_ENOMEM;
+    std::vector<MvJob> hj(n);
+    int tasks = 0;
+    for (int i = 0; i < n; i++) {
+        const KernelMatvecJob &j = jobs[i];
+        const size_t bytes = rq_mat_bytes(j.is_q6, j.rows, j.cols);
+        const uint8_t *W = (const uint8_t *)rt_weight_dev(j.matrix, bytes);
+        if (!W) return ROASTER_EDEVICE;
+        if (owner[i] == i) memcpy(pin + voff[i], j.vector, j.cols * 4);
+        hj[i].W = W;
+        hj[i].X = (const float *)(dv + voff[i]);
+        hj[i].Y = (float *)(dout + ooff[i]);
+        hj[i].rows = (int)j.rows;
+        hj[i].cols = (int)j.cols;
+        hj[i].T = 1;
+        hj[i].q6 = j.is_q6 ? 1 : 0;
+        hj[i].task0 = tasks;
+        tasks += mv_tasks_for((int)j.rows, j.cols);
+    }
+    memcpy(pin + vtot, hj.data(), sizeof(MvJob) * n);
+    if (rt_check(hipMemcpyAsync(dv, pin, vtot, hipMemcpyHostToDevice, R.stream), "vector upload") ||
+        rt_check(hipMemcpyAsync(djobs, pin + vtot, sizeof(MvJob) * n, hipMemcpyHostToDevice, R.stream), "job upload"))
+        return ROASTER_EDEVICE;
+    int rc = mv_launch(djobs, n, tasks);
+    if (rc) return rc;
+    if (rt_check(hipMemcpyAsync(stage, dout, otot, hipMemcpyDeviceToHost, R.stream), "output download"))
+        return ROASTER_EDEVICE;
+    g_pend.out_off = ooff;
+    g_pend.stage = stage;
+    return 0;
+}
+
+extern "C" void kernel_matvec_quant_end(void)
+{
+    Guard g(rt_lock());
+    if (!g_pend.open) return;
+    g_pend.open = 0;
+    int rc = g_pend.failed ? ROASTER_EDEVICE : rt_check(hipStreamSynchronize(rt().stream), "matvec sync");
+    for (int i = 0; i < g_pend.n; i++) {
+        const KernelMatvecJob &j = g_pend.jobs[i];
+        if (rc) fill_nan(j.output, j.rows);
+        else memcpy(j.output, (const uint8_t *)g_pend.stage + g_pend.out_off[i], j.rows * 4);
+    }
+}
+
+extern "C" int kernel_matvec_quant_begin(const KernelMatvecJob *jobs, int n)
+{
+    Guard g(rt_lock());
+    if (n <= 0 || !jobs) return 0;
+    kernel_matvec_quant_end();
+    if (rt_init_locked()) {
+        for (int i = 0; i < n; i++) if (jobs[i].output) fill_nan(jobs[i].output, jobs[i].rows);
+        return 0;
+    }
+    int rc = mv_upload_and_launch(jobs, n);
+    g_pend.open = 1;
+    g_pend.jobs = jobs;
+    g_pend.n = n;
+    g_pend.failed = rc != 0;
+    return rc == 0;
+}
+
+extern "C" void kernel_matvec_quant_batch(const KernelMatvecJob *jobs, int n)
+{
+    Guard g(rt_lock());
+    if (n <= 0) return;
+    kernel_matvec_quant_begin(jobs, n);
+    kernel_matvec_quant_end();
+}
+
+extern "C" void kernel_matvec_q4_k(const void *matrix, const float *vector, float *output, size_t rows, size_t cols)
+{
+    KernelMatvecJob j = { 0, matrix, vector, output, rows, cols };
+    kernel_matvec_quant_batch(&j, 1);
+}
+
+extern "C" void kernel_matvec_q6_k(const void *matrix, const float *vector, float *output, size_t rows, size_t cols)
+{
+    KernelMatvecJob j = { 1, matrix, vector, output, rows, cols };
+    kernel_matvec_quant_batch(&j, 1);
+}
+
+static float dot_quant(int q6, const void *w, const float *x, size_t n)
+{
+    if (n == 0) return 0.0f;
+    if (n % RQK) {
+        rt_fail(ROASTER_EINVAL, "kernel_dot_q%d_k: n = %zu is not a multiple of 256", q6 ? 6 : 4, n);
+        return NAN;
+    }
+    float y = NAN;
+    KernelMatvecJob j = { q6, w, x, &y, 1, n };
+    kernel_matvec_quant_batch(&j, 1);
+    return y;
+}
+
+extern "C" float kernel_dot_q4_k(const void *weights, const float *x, size_t n) { return dot_quant(0, weights, x, n); }
+extern "C" float kernel_dot_q6_k(const void *weights, const float *x, size_t n) { return dot_quant(1, weights, x, n); }
+
+/* ---- multi-token matmul ---------------------------------------------------- */
+static int mm_valid(const KernelMatmulJob *j)
+{
+    return j->matrix && j->X && j->Y && j->rows && j->cols && j->T && (j->cols % RQK) == 0 &&
+           j->rows <= 0x7FFFFFFF && j->cols <= 0x7FFFFFFF && j->T <= 0x7FFFFFFF;
+}
+
+extern "C" int kernel_matmul_quant_batch(const KernelMatmulJob *jobs, int n)
+{
+    Guard g(rt_lock());
+    if (!jobs || n < 0) return -1;
+    for (int i = 0; i < n; i++)
+        if (!mm_valid(&jobs[i])) return -1;
+    if (n == 0) return 0;
+    kernel_matvec_quant_end();
+    if (rt_init_locked()) return -1;
+    RtState &R = rt();
+    std::vector<size_t> xoff(n), yoff(n);
+    std::vector<int> owner(n);
+    size_t xt = 0, yt = 0;
+    for (int i = 0; i < n; i++) {
+        const KernelMatmulJob &j = jobs[i];
+        owner[i] = i;
+        for (int p = 0; p < i; p++)
+            if (owner[p] == p && jobs[p].X == j.X && jobs[p].cols == j.cols && jobs[p].T == j.T) { owner[i] = p; break; }
+        if (owner[i] == i) { xoff[i] = xt; xt += (j.T * j.cols * 4 + 255) & ~(size_t)255; }
+        else xoff[i] = xoff[owner[i]];
+        yoff[i] = yt;
+        yt += (j.T * j.rows * 4 + 255) & ~(size_t)255;
+    }
+    uint8_t *dx = (uint8_t *)rt_scratch(SCR_IN, xt);
+    uint8_t *dy = (uint8_t *)rt_scratch(SCR_OUT, yt);
+    MvJob *dj = (MvJob *)rt_scratch(SCR_A, sizeof(MvJob) * n);
+    if (!dx || !dy || !dj) return -1;
+    std::vector<MvJob> hj(n);
+    int tasks = 0;
+    for (int i = 0; i < n; i++) {
+        const KernelMatmulJob &j = jobs[i];
+        const uint8_t *W = (const uint8_t *)rt_weight_dev(j.matrix, rq_mat_bytes(j.is_q6, j.rows, j.cols));
+        if (!W) return -1;
+        if (owner[i] == i &&
+            rt_check(hipMemcpyAsync(dx + xoff[i], j.X, j.T * j.cols * 4, hipMemcpyHostToDevice, R.stream), "X upload"))
+            return -1;
+        hj[i] = MvJob{ W, (const float *)(dx + xoff[i]), (float *)(dy + yoff[i]), (int)j.rows, (int)j.cols, (int)j.T,
+                       j.is_q6 ? 1 : 0, tasks };
+        tasks += mv_tasks_for((int)j.rows, j.cols);
+    }
+    if (rt_check(hipMemcpyAsync(dj, hj.data(), sizeof(MvJob) * n, hipMemcpyHostToDevice, R.stream), "job upload"))
+        return -1;
+    if (mv_launch(dj, n, tasks)) return -1;
+    for (int i = 0; i < n; i++)
+        if (rt_check(hipMemcpyAsync(jobs[i].Y, dy + yoff[i], jobs[i].T * jobs[i].rows * 4, hipMemcpyDeviceToHost,
+                                    R.stream), "Y download"))
+            return -1;
+    return rt_check(hipStreamSynchronize(R.stream), "matmul sync") ? -1 : 0;
+}
+
+/* ---- prefill MoE on host buffers (kernels.c:2198-2214) -------------------- */
+int prefill_groups_device(const KernelMoeExpert *ex, int na, const float *X, float *D, size_t inter, size_t hidden,
+                          size_t total);
+
+extern "C" int kernel_moe_prefill(const KernelMoeExpert *ex, int count, const float *X, float *D, size_t inter,
+                                  size_t hidden)
+{
+    Guard g(rt_lock());
+    if (!ex || count < 0 || !X || !D || !inter || !hidden || (inter % RQK) || (hidden % RQK)) return -1;
+    std::vector<KernelMoeExpert> act;
+    size_t total = 0;
+    for (int i = 0; i < count; i++) {
+        if (!ex[i].gate || !ex[i].up || !ex[i].down) return -1;
+        if (ex[i].n) { act.push_back(ex[i]); total += ex[i].n; }
+    }
+    if (!total) return 0;
+    kernel_matvec_quant_end();
+    if (rt_init_locked()) return -1;
+    RtState &R = rt();
+    float *dx = (float *)rt_scratch(SCR_IN, total * hidden * 4);
+    float *dd = (float *)rt_scratch(SCR_OUT, total * hidden * 4);
+    if (!dx || !dd) return -1;
+    if (rt_check(hipMemcpyAsync(dx, X, total * hidden * 4, hipMemcpyHostToDevice, R.stream), "X upload")) return -1;
+    if (prefill_groups_device(act.data(), (int)act.size(), dx, dd, inter, hidden, total)) return -1;
+    if (rt_check(hipMemcpyAsync(D, dd, total * hidden * 4, hipMemcpyDeviceToHost, R.stream), "D download")) return -1;
+    return rt_check(hipStreamSynchronize(R.stream), "prefill sync") ? -1 : 0;
+}
+
+/* Expert row groups on device buffers with the matvec kernel: gate and up of
+ * every group in one launch, SiLU*up, then every down in one launch. */
+int prefill_groups_device(const KernelMoeExpert *ex, int na, const float *dx, float *dd, size_t inter, size_t hidden,
+                          size_t total)
+{
+    RtState &R = rt();
+    float *gu = (float *)rt_scratch(SCR_B, 2 * total * inter * 4);
+    MvJob *dj = (MvJob *)rt_scratch(SCR_A, sizeof(MvJob) * 2 * na);
+    if (!gu || !dj) return ROASTER_ENOMEM;
+    float *G = gu, *U = gu + total * inter;
+    std::vector<MvJob> hj;
+    int tasks = 0;
+    size_t row = 0;
+    for (int i = 0; i < na; i++) {
+        const KernelMoeExpert &e = ex[i];
+        const uint8_t *gw = (const uint8_t *)rt_weight_dev(e.gate, rq_mat_bytes(e.gate_q6, inter, hidden));
+        const uint8_t *uw = (const uint8_t *)rt_weight_dev(e.up, rq_mat_bytes(e.up_q6, inter, hidden));
+        if (!gw || !uw) return ROASTER_EDEVICE;
+        hj.push_back(MvJob{ gw, dx + row * hidden, G + row * inter, (int)inter, (int)hidden, (int)e.n, e.gate_q6 ? 1 : 0, tasks });
+        tasks += mv_tasks_for((int)inter, hidden);
+        hj.push_back(MvJob{ uw, dx + row * hidden, U + row * inter, (int)inter, (int)hidden, (int)e.n, e.up_q6 ? 1 : 0, tasks });
+        tasks += mv_tasks_for((int)inter, hidden);
+        row += e.n;
+    }
+    std::vector<MvJob> hd;
+    int dtasks = 0;
+    row = 0;
+    for (int i = 0; i < na; i++) {
+        const KernelMoeExpert &e = ex[i];
+        const uint8_t *dw = (const uint8_t *)rt_weight_dev(e.down, rq_mat_bytes(e.down_q6, hidden, inter));
+        if (!dw) return ROASTER_EDEVICE;
+        hd.push_back(MvJob{ dw, G + row * inter, dd + row * hidden, (int)hidden, (int)inter, (int)e.n, e.down_q6 ? 1 : 0, dtasks });
+        dtasks += mv_tasks_for((int)hidden, inter);
+        row += e.n;
+    }
+    MvJob *djd = (MvJob *)rt_scratch(SCR_C, sizeof(MvJob) * na);
+    if (!djd) return ROASTER_ENOMEM;
+    if (rt_check(hipMemcpyAsync(dj, hj.data(), sizeof(MvJob) * hj.size(), hipMemcpyHostToDevice, R.stream), "jobs") ||
+        rt_check(hipMemcpyAsync(djd, hd.data(), sizeof(MvJob) * hd.size(), hipMemcpyHostToDevice, R.stream), "jobs"))
+        return ROASTER_EDEVICE;
+    int rc = mv_launch(dj, (int)hj.size(), tasks);
+    if (!rc) rc = silu_mul_launch(G, U, total * inter);
+    if (!rc) rc = mv_launch(djd, (int)hd.size(), dtasks);
+    if (!rc) rc = rt_check(hipStreamSynchronize(R.stream), "groups sync");   /* host job vectors go out of scope */
+    return rc;
+}
+
+/* ---- fused decode experts (kernels.c:1703-1830) ---------------------------- */
+extern "C" int kernel_ffn_fused(const KernelFfnExpert *ex, int n, const float *x, size_t inter, size_t hidden)
+{
+    Guard g(rt_lock());
+    if (!ex || !x || n <= 0 || n > 9) return 0;
+    if (!inter || !hidden || (inter & 255u) || (hidden & 255u)) return 0;
+    if (inter > 2048 || hidden > 2048) return 0;     /* one wave pass per row: <= 8 super-blocks */
+    kernel_matvec_quant_end();
+    if (rt_init_locked()) return 0;
+    if (((hidden + rt().n_cu - 1) / rt().n_cu + 3) / 4 * 4 > 64) return 0;
+    RtState &R = rt();
+    DecActive hx[9];
+    memset(hx, 0, sizeof(hx));
+    for (int i = 0; i < n; i++) {
+        if (!ex[i].gate || !ex[i].up || !ex[i].down || !ex[i].out) return 0;
+        hx[i].g = (const uint8_t *)rt_weight_dev(ex[i].gate, rq_mat_bytes(ex[i].gate_q6, inter, hidden));
+        hx[i].u = (const uint8_t *)rt_weight_dev(ex[i].up, rq_mat_bytes(ex[i].up_q6, inter, hidden));
+        hx[i].d = (const uint8_t *)rt_weight_dev(ex[i].down, rq_mat_bytes(ex[i].down_q6, hidden, inter));
+        if (!hx[i].g || !hx[i].u || !hx[i].d) return 0;
+        hx[i].gq6 = ex[i].gate_q6 ? 1 : 0;
+        hx[i].uq6 = ex[i].up_q6 ? 1 : 0;
+        hx[i].dq6 = ex[i].down_q6 ? 1 : 0;
+    }
+    float *dx = (float *)rt_scratch(SCR_IN, hidden * 4);
+    float *dout = (float *)rt_scratch(SCR_OUT, (size_t)n * hidden * 4);
+    float *eh = (float *)rt_scratch(SCR_B, 9 * inter * 4);
+    DecActive *dex = (DecActive *)rt_scratch(SCR_A, sizeof(hx));
+    if (!dx || !dout || !eh || !dex) return 0;
+    if (rt_check(hipMemcpyAsync(dx, x, hidden * 4, hipMemcpyHostToDevice, R.stream), "x upload") ||
+        rt_check(hipMemcpyAsync(dex, hx, sizeof(hx), hipMemcpyHostToDevice, R.stream), "expert upload"))
+        return 0;
+    DecArgs A;
+    memset(&A, 0, sizeof(A));
+    A.H = (int)hidden;
+    A.I = (int)inter;
+    A.B = 1;
+    A.nlayers = 1;
+    A.h = dx;
+    A.eh = eh;
+    A.ffn_ex = dex;
+    A.ffn_n = n;
+    A.ffn_out = dout;
+    if (dec_ffn_launch(A)) return 0;
+    for (int i = 0; i < n; i++)
+        if (rt_check(hipMemcpyAsync(ex[i].out, dout + (size_t)i * hidden, hidden * 4, hipMemcpyDeviceToHost, R.stream),
+                     "out download"))
+            return 0;
+    return rt_take_err() == 0 ? 1 : 0;
+}
+
+/* ---- table-based decode ---------------------------------------------------- */
+static void fill_table_args(DecArgs &A, const RoasterTable *t)
+{
+    memset(&A, 0, sizeof(A));
+    A.layers = t->layers_d;
+    A.E = t->d.n_experts;
+    A.H = (int)t->d.hidden;
+    A.I = (int)t->d.inter;
+    A.q6g = t->d.q6[0]; A.q6u = t->d.q6[1]; A.q6d = t->d.q6[2];
+    A.sq6g = t->d.sh_q6[0]; A.sq6u = t->d.sh_q6[1]; A.sq6d = t->d.sh_q6[2];
+    A.bytes_g = t->eb[0]; A.bytes_u = t->eb[1]; A.bytes_d = t->eb[2];
+}
+
+static int dec_scratch(DecArgs &A)
+{
+    const size_t E = (size_t)A.E, B = (size_t)A.B;
+    A.logits = (float *)rt_scratch(SCR_D, B * E * 4);
+    A.sgate_raw = (float *)rt_scratch(SCR_E, B * 4);
+    A.eh = (float *)rt_scratch(SCR_F, B * 9 * (size_t)A.I * 4);
+    return A.logits && A.sgate_raw && A.eh ? 0 : ROASTER_ENOMEM;
+}
+
+static int g_decode_split = -1;   /* ROASTER_DECODE_SPLIT=1: one launch per phase */
+
+static int decode_fused()
+{
+    if (g_decode_split < 0) {
+        const char *s = getenv("ROASTER_DECODE_SPLIT");
+        g_decode_split = s && s[0] == '1';
+    }
+    return !g_decode_split;
+}
+
+extern "C" int roaster_moe_decode(RoasterTable *t, int layer, const float *x, int B, float *y,
+                                  const RoasterDecodeIO *io)
+{
+    Guard g(rt_lock());
+    if (rt_init_locked()) return ROASTER_EDEVICE;
+    if (!t || !x || !y || B < 1 || B > RMAX_B || layer < 0 || layer >= t->d.n_layers)
+        return rt_fail(ROASTER_EINVAL, "roaster_moe_decode: bad arguments");
+    DecArgs A;
+    fill_table_args(A, t);
+    A.layer0 = layer;
+    A.nlayers = 1;
+    A.B = B;
+    A.h = (float *)x;
+    A.y = y;
+    A.do_norm = 0;
+    if (io) {
+        A.logits_in = io->logits_in;
+        A.ids_out = io->ids_out;
+        A.w_out = io->w_out;
+    }
+    if (dec_scratch(A)) return ROASTER_ENOMEM;
+    int rc = dec_launch(A, decode_fused());
+    if (rc) return rc;
+    if (io && io->logits_out) {
+        const float *src = A.logits_in ? A.logits_in : A.logits;
+        if (rt_check(hipMemcpyAsync(io->logits_out, src, (size_t)B * A.E * 4, hipMemcpyDeviceToDevice, rt().stream),
+                     "logits copy"))
+            return ROASTER_EDEVICE;
+    }
+    return 0;
+}
+
+extern "C" int roaster_moe_decode_stack(RoasterTable *t, float *h, int B, int layer0, int n_layers,
+                                        const float *norm_w, float eps, int *ids_out, float *w_out)
+{
+    Guard g(rt_lock());
+    if (rt_init_locked()) return ROASTER_EDEVICE;
+    if (!t || !h || B < 1 || B > RMAX_B || layer0 < 0 || n_layers < 1 || layer0 + n_layers > t->d.n_layers)
+        return rt_fail(ROASTER_EINVAL, "roaster_moe_decode_stack: bad arguments");
+    DecArgs A;
+    fill_table_args(A, t);
+    A.layer0 = layer0;
+    A.nlayers = n_layers;
+    A.B = B;
+    A.h = h;
+    A.y = NULL;
+    A.norm_w = norm_w;
+    A.eps = eps;
+    A.do_norm = 1;
+    A.ids_out = ids_out;
+    A.w_out = w_out;
+    if (dec_scratch(A)) return ROASTER_ENOMEM;
+    return dec_launch(A, decode_fused());
+}
+
+/* ---- small vector kernels (off the MoE path, kept for link compatibility) -- */
+static int up(void *d, const void *s, size_t n)
+{
+    return rt_check(hipMemcpyAsync(d, s, n, hipMemcpyHostToDevice, rt().stream), "upload");
+}
+
+static int down_sync(void *d, const void *s, size_t n)
+{
+    if (rt_check(hipMemcpyAsync(d, s, n, hipMemcpyDeviceToHost, rt().stream), "download")) return -1;
+    return rt_check(hipStreamSynchronize(rt().stream), "sync");
+}
+
+extern "C" void kernel_matvec_f32(const float *matrix, const float *vector, float *output, size_t rows, size_t cols)
+{
+    Guard g(rt_lock());
+    if (!rows) return;
+    kernel_matvec_quant_end();
+    const float *W = rt_init_locked() ? NULL : (const float *)rt_weight_dev(matrix, rows * cols * 4);
+    float *dx = (float *)rt_scratch(SCR_IN, cols * 4 + 16);
+    float *dy = (float *)rt_scratch(SCR_OUT, rows * 4 + 16);
+    if (!W || !dx || !dy || up(dx, vector, cols * 4) || matvec_f32_launch(W, dx, dy, rows, cols) ||
+        down_sync(output, dy, rows * 4))
+        fill_nan(output, rows);
+}
+
+extern "C" float kernel_dot_f32(const float *a, const float *b, size_t n)
+{
+    Guard g(rt_lock());
+    if (!n) return 0.0f;
+    kernel_matvec_quant_end();
+    if (rt_init_locked()) return NAN;
+    float *da = (float *)rt_scratch(SCR_IN, 2 * n * 4 + 64);
+    float *dy = (float *)rt_scratch(SCR_OUT, 64);
+    float y = NAN;
+    if (!da || !dy || up(da, a, n * 4) || up(da + n, b, n * 4) || matvec_f32_launch(da, da + n, dy, 1, n) ||
+        down_sync(&y, dy, 4))
+        return NAN;
+    return y;
+}
+
+static void norm_common(float *out, const float *in, const float *w, size_t n, float eps, int mode)
+{
+    Guard g(rt_lock());
+    if (!n) return;
+    kernel_matvec_quant_end();
+    float *d = rt_init_locked() ? NULL : (float *)rt_scratch(SCR_IN, 3 * n * 4 + 64);
+    if (!d || up(d, in, n * 4) || (mode == 0 && up(d + n, w, n * 4)) ||
+        norm_launch(d + 2 * n, d, d + n, n, eps, mode) || down_sync(out, d + 2 * n, n * 4))
+        fill_nan(out, n);
+}
+
+extern "C" void kernel_rmsnorm(float *output, const float *input, const float *weight, size_t n, float epsilon)
+{
+    norm_common(output, input, weight, n, epsilon, 0);
+}
+
+extern "C" void kernel_l2norm(float *output, const float *input, size_t n, float epsilon)
+{
+    norm_common(output, input, NULL, n, epsilon, 1);
+}
+
+/* Scalar activations: one float in, one float out; a device round trip would
+ * add nothing, so these are plain host math with the reference's formulas
+ * (kernels.c:628-642). */
+extern "C" float kernel_sigmoid(float x)
+{
+    if (x >= 0.0f) { float z = expf(-x); return 1.0f / (1.0f + z); }
+    float z = expf(x);
+    return z / (1.0f + z);
+}
+
+extern "C" float kernel_silu(float x) { return x * kernel_sigmoid(x); }
+
+extern "C" void kernel_silu_array(float *x, size_t n)
+{
+    Guard g(rt_lock());
+    if (!n) return;
+    kernel_matvec_quant_end();
+    float *d = rt_init_locked() ? NULL : (float *)rt_scratch(SCR_IN, n * 4 + 64);
+    if (!d || up(d, x, n * 4) || silu_array_launch(d, n) || down_sync(x, d, n * 4)) fill_nan(x, n);
+}
+
+extern "C" void kernel_embedding_row_q4_k(const void *weights, size_t token_id, float *output, size_t hidden_size)
+{
+    Guard g(rt_lock());
+    if (!hidden_size) return;
+    kernel_matvec_quant_end();
+    if (hidden_size % RQK) { rt_fail(ROASTER_EINVAL, "embedding row: hidden not a multiple of 256"); fill_nan(output, hidden_size); return; }
+    const uint8_t *row = (const uint8_t *)weights + token_id * (hidden_size / RQK) * RQ4K_BYTES;
+    const uint8_t *dw = rt_init_locked() ? NULL : (const uint8_t *)rt_weight_dev(row, hidden_size / RQK * RQ4K_BYTES);
+    float *d = (float *)rt_scratch(SCR_OUT, hidden_size * 4 + 64);
+    if (!dw || !d || q4k_row_launch(dw, d, hidden_size) || down_sync(output, d, hidden_size * 4))
+        fill_nan(output, hidden_size);
+}
+
+extern "C" void kernel_conv1d_causal_f32(const float *input, const float *history, const float *kernel, float *output,
+                                         size_t channels, size_t kernel_size)
+{
+    Guard g(rt_lock());
+    if (kernel_size == 0 || channels == 0) return;
+    kernel_matvec_quant_end();
+    const size_t C = channels, K = kernel_size;
+    float *d = rt_init_locked() ? NULL : (float *)rt_scratch(SCR_IN, (C + (K - 1) * C + C * K + C) * 4 + 64);
+    if (!d) { fill_nan(output, C); return; }
+    float *di = d, *dh = d + C, *dk = dh + (K - 1) * C, *dout = dk + C * K;
+    if (up(di, input, C * 4) || (K > 1 && up(dh, history, (K - 1) * C * 4)) || up(dk, kernel, C * K * 4) ||
+        conv1d_launch(di, dh, dk, dout, C, K) || down_sync(output, dout, C * 4))
+        fill_nan(output, C);
+}

@@ -1,0 +1,67 @@
+/*
+ * decode.h -- argument structures of the decode kernel (decode.hip), shared
+ * with the host code that fills them (api.hip).
+ */
+#ifndef ROASTER_DECODE_H
+#define ROASTER_DECODE_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#define RMAX_ACT (8 * 8 + 1)        /* distinct routed experts of 8 tokens + shared */
+
+/* Device addresses of one layer's tensors in the expert table. */
+struct DecLayer {
+    const uint8_t *gate, *up, *down;      /* [E][rows][row_bytes], GGUF *_exps layout */
+    const uint8_t *sgate, *sup, *sdown;   /* shared expert */
+    const float *router;                  /* [E x H] */
+    const float *gate_inp;                /* [H] */
+};
+
+/* One active expert of a decode plan: its matrices and the (token, slot)
+ * pairs that use it (pair p = t*9 + k, k = 8 for the shared expert). */
+struct DecActive {
+    const uint8_t *g, *u, *d;
+    int gq6, uq6, dq6;
+    int ntok;
+    int tk[8];
+};
+
+struct DecPlan {
+    int nact;
+    int err;
+    DecActive a[RMAX_ACT];
+    int ids[8][8];
+    float w[8][9];          /* routing weights, [8] = sigmoid(shared gate logit) */
+};
+
+struct DecArgs {
+    const DecLayer *layers;     /* device array indexed by layer */
+    int layer0, nlayers;
+    int E, H, I, B;
+    int q6g, q6u, q6d, sq6g, sq6u, sq6d;
+    size_t bytes_g, bytes_u, bytes_d;     /* per-expert matrix bytes */
+    float *h;                   /* [B x H]: stack state (in/out), or the layer input */
+    float *y;                   /* [B x H] layer output, or NULL in stack mode */
+    const float *norm_w;        /* [nlayers x H] or NULL */
+    float eps;
+    int do_norm;
+    const float *logits_in;     /* [B x E] or NULL */
+    float *logits;              /* [B x E] */
+    float *sgate_raw;           /* [B] */
+    float *eh;                  /* [B*9 x I] */
+    int *ids_out;               /* [nlayers x B x 8] or NULL */
+    float *w_out;
+    unsigned *bar;
+    int *err;
+    /* kernel_ffn_fused mode */
+    const DecActive *ffn_ex;    /* [n] device */
+    int ffn_n;
+    float *ffn_out;             /* [n x H] or NULL */
+};
+
+size_t dec_lds_bytes(int B, int H);
+int dec_launch(DecArgs &A, int fused);
+int dec_ffn_launch(DecArgs &A);
+
+#endif

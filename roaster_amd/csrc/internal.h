@@ -1,0 +1,62 @@
+/*
+ * internal.h -- host-side internals shared by the translation units of
+ * libroaster_moe.so (runtime, expert table, decode, prefill, kernels.h API).
+ */
+#ifndef ROASTER_INTERNAL_H
+#define ROASTER_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <mutex>
+
+#include "../../include/kernels.h"
+#include "../../include/roaster_moe.h"
+
+#define RQK 256
+#define RQ4K_BYTES 144
+#define RQ6K_BYTES 210
+#define RTOPK 8
+#define RMAX_B 8                 /* decode tokens per call */
+
+static inline size_t rq_block_bytes(int q6) { return q6 ? RQ6K_BYTES : RQ4K_BYTES; }
+static inline size_t rq_row_bytes(int q6, size_t cols) { return cols / RQK * rq_block_bytes(q6); }
+static inline size_t rq_mat_bytes(int q6, size_t rows, size_t cols) { return rows * rq_row_bytes(q6, cols); }
+
+/* ---- runtime (runtime.hip) ---- */
+struct RtState {
+    int inited;
+    int device;
+    int n_cu;
+    int n_xcd;
+    size_t hbm_bytes;
+    hipStream_t stream;
+};
+RtState &rt();
+std::recursive_mutex &rt_lock();          /* serialises every public entry point */
+int  rt_init_locked();                      /* 0 ok, else ROASTER_EDEVICE */
+int  rt_fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int  rt_check(hipError_t e, const char *what);  /* 0 or ROASTER_EDEVICE with message */
+/* Grow-only device scratch slots (kept until trim/shutdown). */
+enum { SCR_IN = 0, SCR_OUT, SCR_A, SCR_B, SCR_C, SCR_D, SCR_E, SCR_F, SCR_CTRL, SCR_N };
+void *rt_scratch(int slot, size_t bytes);
+void  rt_scratch_trim();
+/* Pinned host staging (grow-only). */
+void *rt_pinned(int slot, size_t bytes);
+
+/* Weight pointer translation: host address of `bytes` weight bytes -> device
+ * address holding the same bytes (uploads on first use).  Device addresses are
+ * returned unchanged.  NULL on failure (message set). */
+const void *rt_weight_dev(const void *ptr, size_t bytes);
+/* Same for f32 weight matrices used by kernel_matvec_f32. */
+void rt_registry_clear();
+void rt_register_device_range(const void *dev, size_t bytes);   /* table allocations */
+void rt_unregister_device_range(const void *dev);
+
+unsigned *rt_ctrl();        /* persistent-kernel control words (device) */
+int rt_take_err();           /* sync the stream, report and clear kernel error bits */
+
+/* Launch helpers */
+int rt_coop_grid(const void *kernel, int threads, size_t lds, int *blocks_out);
+
+#endif

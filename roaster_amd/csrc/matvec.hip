@@ -1,0 +1,209 @@
+/*
+ * matvec.hip -- multi-job quantised matvec / small-T matmul and the small
+ * vector kernels behind kernels.h.
+ *
+ * Reference: kernel_matvec_quant_batch (kernels.c:1582-1646: all jobs of a call
+ * in one submit), kernel_matmul_quant_batch (kernels.c:1916-2069,
+ * Y[t*rows + r] = dot(W[r], X[t])), and the CPU vector kernels
+ * (kernels.c:102-148, 584-719).
+ *
+ * One wave serves a task = (job, group of rows).  Lane layout per row:
+ * lpr = min(64, 8 * blocks_per_row) lanes, 8 lanes per 256-weight super-block
+ * (qdot.h); each lane's quant chunk is loaded once and applied to all T tokens.
+ */
+#include "internal.h"
+#include "qdot.h"
+#include "matvec.h"
+
+#define MV_THREADS 256
+
+template <bool Q6>
+__device__ __forceinline__ void matvec_task(const MvJob &J, int task, int lane)
+{
+    const int nb = J.cols / RQK;
+    const int lpr = nb >= 8 ? 64 : 8 * nb, rpw = 64 / lpr;
+    const int rw = lane / lpr, lr = lane % lpr, c = lr & 7, lb = lr >> 3;
+    const int row = (task - J.task0) * rpw + rw;
+    const bool live = row < J.rows;
+    const size_t bs = Q6 ? RQ6K_BYTES : RQ4K_BYTES;
+    const uint8_t *wrow = J.W + (size_t)(live ? row : 0) * nb * bs;
+    for (int t = 0; t < J.T; t++) {
+        const float *x = J.X + (size_t)t * J.cols;
+        float part = 0.0f;
+        for (int b = lb; live && b < nb; b += 8) {
+            QChunk ch = q_load<Q6>(wrow + (size_t)b * bs, c);
+            const int ca = b * RQK + q_run_a<Q6>(c), cb = ca + q_run_b_off<Q6>();
+            part += q_chunk_dot<Q6>(ch, c, x + ca, x + cb, sum16(x + ca), sum16(x + cb));
+        }
+        part = group_sum(part, lpr);
+        if (live && lr == 0) J.Y[(size_t)t * J.rows + row] = part;
+    }
+}
+
+__global__ void __launch_bounds__(MV_THREADS) matvec_jobs_kernel(const MvJob *jobs, int njobs, int ntasks)
+{
+    const int lane = threadIdx.x & 63;
+    const int gw = blockIdx.x * (MV_THREADS / 64) + (threadIdx.x >> 6), nw = gridDim.x * (MV_THREADS / 64);
+    for (int task = gw; task < ntasks; task += nw) {
+        int j = 0;
+        while (j + 1 < njobs && jobs[j + 1].task0 <= task) j++;
+        const MvJob J = jobs[j];
+        if (J.q6) matvec_task<true>(J, task, lane);
+        else matvec_task<false>(J, task, lane);
+    }
+}
+
+/* eh = (g / (1 + exp(-g))) * u over n elements (kernels.c:2191, model.c:1124). */
+__global__ void silu_mul_kernel(float *g, const float *u, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const float a = g[i];
+        g[i] = (a / (1.0f + expf(-a))) * u[i];
+    }
+}
+
+/* f32 matvec rows (kernel_matvec_f32 / kernel_dot_f32): one wave per row. */
+__global__ void __launch_bounds__(MV_THREADS) matvec_f32_kernel(const float *W, const float *x, float *y, size_t rows,
+                                                                size_t cols)
+{
+    const int lane = threadIdx.x & 63;
+    const size_t gw = (size_t)blockIdx.x * (MV_THREADS / 64) + (threadIdx.x >> 6);
+    const size_t nw = (size_t)gridDim.x * (MV_THREADS / 64);
+    for (size_t r = gw; r < rows; r += nw) {
+        const float *row = W + r * cols;
+        float acc = 0.0f;
+        for (size_t i = lane; i < cols; i += 64) acc = fmaf(row[i], x[i], acc);
+        acc = group_sum(acc, 64);
+        if (lane == 0) y[r] = acc;
+    }
+}
+
+/* mode 0: rmsnorm  y = x * (1/sqrt(mean(x^2) + eps)) * w   (kernels.c:584-605)
+ * mode 1: l2norm   y = x * (1/sqrt(sum(x^2) + eps))        (kernels.c:607-622)
+ * One workgroup. */
+__global__ void __launch_bounds__(1024) norm_kernel(float *y, const float *x, const float *w, size_t n, float eps,
+                                                   int mode)
+{
+    __shared__ float red[16];
+    float ss = 0.0f;
+    for (size_t i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
+    ss = group_sum(ss, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) tot += red[i];
+    const float inv = mode == 0 ? 1.0f / sqrtf(tot / (float)n + eps) : 1.0f / sqrtf(tot + eps);
+    for (size_t i = threadIdx.x; i < n; i += blockDim.x) y[i] = mode == 0 ? x[i] * inv * w[i] : x[i] * inv;
+}
+
+/* kernel_silu_array: x * sigmoid(x) with the two-branch sigmoid (kernels.c:628-652). */
+__global__ void silu_array_kernel(float *x, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const float v = x[i];
+        float s;
+        if (v >= 0.0f) s = 1.0f / (1.0f + expf(-v));
+        else { const float z = expf(v); s = z / (1.0f + z); }
+        x[i] = v * s;
+    }
+}
+
+/* Dequantise one Q4_K row (kernel_embedding_row_q4_k, kernels.c:660-687):
+ * one thread per output element. */
+__global__ void q4k_row_kernel(const uint8_t *blocks, float *out, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const uint8_t *blk = blocks + (i / RQK) * RQ4K_BYTES;
+        const int w = (int)(i % RQK), g = w / 64, hi = (w % 64) >= 32, k = w % 32;
+        const float d = f16_bits_to_f32(blk[0] | (blk[1] << 8)), dmin = f16_bits_to_f32(blk[2] | (blk[3] << 8));
+        const uint8_t *s = blk + 4;
+        const int j = 2 * g + hi;
+        int sc, m;
+        if (j < 4) { sc = s[j] & 63; m = s[j + 4] & 63; }
+        else { sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4); m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
+        const uint8_t q = blk[16 + 32 * g + k];
+        const int qv = hi ? (q >> 4) : (q & 15);
+        out[i] = fmaf(d * (float)sc, (float)qv, -(dmin * (float)m));
+    }
+}
+
+/* kernel_conv1d_causal_f32 (kernels.c:693-719): one thread per channel. */
+__global__ void conv1d_kernel(const float *input, const float *history, const float *kern, float *out, size_t C,
+                              size_t K)
+{
+    for (size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x; c < C; c += (size_t)gridDim.x * blockDim.x) {
+        float sum = 0.0f;
+        for (size_t k = 0; k + 1 < K; k++) sum = fmaf(history[k * C + c], kern[c * K + k], sum);
+        sum = fmaf(input[c], kern[c * K + K - 1], sum);
+        out[c] = sum;
+    }
+}
+
+/* ---- host launchers ------------------------------------------------------- */
+int mv_launch(const MvJob *jobs_dev, int njobs, int ntasks)
+{
+    if (ntasks <= 0) return 0;
+    const int wpb = MV_THREADS / 64;
+    int blocks = (ntasks + wpb - 1) / wpb;
+    if (blocks > 8 * rt().n_cu) blocks = 8 * rt().n_cu;
+    hipLaunchKernelGGL(matvec_jobs_kernel, dim3(blocks), dim3(MV_THREADS), 0, rt().stream, jobs_dev, njobs, ntasks);
+    return rt_check(hipGetLastError(), "matvec launch") ? ROASTER_EDEVICE : 0;
+}
+
+int mv_tasks_for(int rows, size_t cols)
+{
+    const int nb = (int)(cols / RQK);
+    const int lpr = nb >= 8 ? 64 : 8 * nb;
+    const int rpw = 64 / lpr;
+    return (rows + rpw - 1) / rpw;
+}
+
+int silu_mul_launch(float *g, const float *u, size_t n)
+{
+    int blocks = (int)((n + 255) / 256);
+    if (blocks > 4096) blocks = 4096;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks), dim3(256), 0, rt().stream, g, u, n);
+    return rt_check(hipGetLastError(), "silu launch") ? ROASTER_EDEVICE : 0;
+}
+
+int matvec_f32_launch(const float *W, const float *x, float *y, size_t rows, size_t cols)
+{
+    size_t blocks = (rows + 3) / 4;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(matvec_f32_kernel, dim3((unsigned)blocks), dim3(MV_THREADS), 0, rt().stream, W, x, y, rows,
+                       cols);
+    return rt_check(hipGetLastError(), "matvec_f32 launch") ? ROASTER_EDEVICE : 0;
+}
+
+int norm_launch(float *y, const float *x, const float *w, size_t n, float eps, int mode)
+{
+    hipLaunchKernelGGL(norm_kernel, dim3(1), dim3(1024), 0, rt().stream, y, x, w, n, eps, mode);
+    return rt_check(hipGetLastError(), "norm launch") ? ROASTER_EDEVICE : 0;
+}
+
+int silu_array_launch(float *x, size_t n)
+{
+    int blocks = (int)((n + 255) / 256);
+    if (blocks > 4096) blocks = 4096;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(silu_array_kernel, dim3(blocks), dim3(256), 0, rt().stream, x, n);
+    return rt_check(hipGetLastError(), "silu_array launch") ? ROASTER_EDEVICE : 0;
+}
+
+int q4k_row_launch(const uint8_t *blocks, float *out, size_t n)
+{
+    int b = (int)((n + 255) / 256);
+    if (b < 1) b = 1;
+    hipLaunchKernelGGL(q4k_row_kernel, dim3(b), dim3(256), 0, rt().stream, blocks, out, n);
+    return rt_check(hipGetLastError(), "q4k_row launch") ? ROASTER_EDEVICE : 0;
+}
+
+int conv1d_launch(const float *in, const float *hist, const float *kern, float *out, size_t C, size_t K)
+{
+    int b = (int)((C + 255) / 256);
+    if (b < 1) b = 1;
+    hipLaunchKernelGGL(conv1d_kernel, dim3(b), dim3(256), 0, rt().stream, in, hist, kern, out, C, K);
+    return rt_check(hipGetLastError(), "conv1d launch") ? ROASTER_EDEVICE : 0;
+}

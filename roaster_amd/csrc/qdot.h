@@ -1,0 +1,174 @@
+/*
+ * qdot.h -- device helpers: Q4_K / Q6_K super-block chunks for wave-wide
+ * dequantising dot products (decode / matvec kernels).
+ *
+ * One 256-weight super-block is served by 8 lanes.  Lane chunk c (0..7) owns
+ * 32 weights in two runs of 16 consecutive columns, A and B, and the 16 quant
+ * bytes at block offset 16*c (+16 for Q4_K's header):
+ *
+ *   Q4_K (144 B: d, dmin, scales[12], qs[128]; kernels.c:29-34, 1839-1853):
+ *     g = c/2; run A = 64g + 16(c&1) (low nibbles, sub-block 2g),
+ *              run B = A + 32        (high nibbles, sub-block 2g+1).
+ *     w = d*sc*q - dmin*m.
+ *   Q6_K (210 B: ql[128], qh[64], scales[16], d; kernels.c:35-40, 1855-1874):
+ *     n = c/4, p = c&3; run A = 128n + 32(p>>1) + 16(p&1) (low nibbles of ql,
+ *     qh bits 2(p>>1)..+1), run B = A + 64 (high nibbles, qh bits 4+2(p>>1)..+1).
+ *     w = d*sc*(q - 32), q unsigned 6-bit.
+ *
+ * Folded dot for a lane (kernels.c:242-245 uses the same identity):
+ *   sum_i w_i x_i = sA * sum(qA x) - mA * sum(xA) + sB * sum(qB x) - mB * sum(xB)
+ * with mA = dmin*m (Q4_K) or 32*d*sc (Q6_K).  Quant bytes are unpacked four at
+ * a time in 32-bit registers and converted with the byte-select f32 converts.
+ */
+#ifndef ROASTER_QDOT_H
+#define ROASTER_QDOT_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+struct __attribute__((packed, aligned(2))) u32x4_a2 { uint32_t x, y, z, w; };
+struct __attribute__((packed, aligned(2))) u32x2_a2 { uint32_t x, y; };
+
+/* Raw bytes of one lane's share of a super-block. */
+struct QChunk {
+    uint4 q;       /* Q4_K: qs bytes;  Q6_K: ql bytes */
+    uint4 h;       /* Q4_K: header (d, dmin, scales); Q6_K: qh bytes */
+    uint2 s;       /* Q6_K: scales[8n .. 8n+8) */
+    uint32_t dd;   /* Q6_K: d (low 16 bits) */
+};
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+template <bool q6>
+__device__ __forceinline__ QChunk q_load(const uint8_t *blk, int c)
+{
+    QChunk ch;
+    if (!q6) {
+        ch.h = *(const uint4 *)blk;                     /* 144-byte blocks are 16-byte aligned */
+        ch.q = *(const uint4 *)(blk + 16 + 16 * c);
+        ch.s = make_uint2(0, 0);
+        ch.dd = 0;
+    } else {
+        const int n = c >> 2, p = c & 3;
+        u32x4_a2 ql = *(const u32x4_a2 *)(blk + 16 * c);
+        u32x4_a2 qh = *(const u32x4_a2 *)(blk + 128 + 32 * n + 16 * (p & 1));
+        u32x2_a2 sc = *(const u32x2_a2 *)(blk + 192 + 8 * n);
+        ch.q = make_uint4(ql.x, ql.y, ql.z, ql.w);
+        ch.h = make_uint4(qh.x, qh.y, qh.z, qh.w);
+        ch.s = make_uint2(sc.x, sc.y);
+        ch.dd = *(const uint16_t *)(blk + 208);
+    }
+    return ch;
+}
+
+/* Column offsets (within the block) of runs A and B for chunk c. */
+template <bool q6>
+__device__ __forceinline__ int q_run_a(int c)
+{
+    return q6 ? (128 * (c >> 2) + 32 * ((c & 3) >> 1) + 16 * (c & 1)) : (64 * (c >> 1) + 16 * (c & 1));
+}
+template <bool q6>
+__device__ __forceinline__ int q_run_b_off() { return q6 ? 64 : 32; }
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
+
+/* Scale factors for the lane: sA, mA, sB, mB. */
+template <bool q6>
+__device__ __forceinline__ void q_scales(const QChunk &ch, int c, float &sA, float &mA, float &sB, float &mB)
+{
+    if (!q6) {
+        const float d = f16_bits_to_f32(ch.h.x & 0xFFFFu), dmin = f16_bits_to_f32(ch.h.x >> 16);
+        /* scales bytes s[0..11] = h.y (0-3), h.z (4-7), h.w (8-11) */
+        const int g = c >> 1;
+        const int j0 = 2 * g, j1 = 2 * g + 1;
+        uint32_t s03 = ch.h.y, s47 = ch.h.z, s811 = ch.h.w;
+        int sc0, m0, sc1, m1;
+        if (g < 2) {           /* j0, j1 < 4 */
+            sc0 = byte_of(s03, j0) & 63; m0 = byte_of(s47, j0) & 63;
+            sc1 = byte_of(s03, j1) & 63; m1 = byte_of(s47, j1) & 63;
+        } else {               /* j >= 4: low nibble / high nibble of s[j+4], top bits of s[j-4] / s[j] */
+            const int i0 = j0 - 4, i1 = j1 - 4;
+            sc0 = (byte_of(s811, i0) & 15) | ((byte_of(s03, i0) >> 6) << 4);
+            m0  = (byte_of(s811, i0) >> 4) | ((byte_of(s47, i0) >> 6) << 4);
+            sc1 = (byte_of(s811, i1) & 15) | ((byte_of(s03, i1) >> 6) << 4);
+            m1  = (byte_of(s811, i1) >> 4) | ((byte_of(s47, i1) >> 6) << 4);
+        }
+        sA = d * (float)sc0; mA = dmin * (float)m0;
+        sB = d * (float)sc1; mB = dmin * (float)m1;
+    } else {
+        const float d = f16_bits_to_f32(ch.dd);
+        const int p = c & 3;
+        const int ia = (p & 1) + 2 * (p >> 1);     /* index within the 8 scales of this half */
+        const int ib = ia + 4;
+        const int sa = (int)(int8_t)byte_of(ia < 4 ? ch.s.x : ch.s.y, ia & 3);
+        const int sb = (int)(int8_t)byte_of(ch.s.y, ib & 3);
+        sA = d * (float)sa; mA = 32.0f * sA;
+        sB = d * (float)sb; mB = 32.0f * sB;
+    }
+}
+
+/* Quant values of word i (4 consecutive columns) of runs A and B, as 4 bytes each. */
+template <bool q6>
+__device__ __forceinline__ void q_word(const QChunk &ch, int i, int c, uint32_t &a, uint32_t &b)
+{
+    const uint32_t v = i == 0 ? ch.q.x : i == 1 ? ch.q.y : i == 2 ? ch.q.z : ch.q.w;
+    a = v & 0x0F0F0F0Fu;
+    b = (v >> 4) & 0x0F0F0F0Fu;
+    if (q6) {
+        const uint32_t hv = i == 0 ? ch.h.x : i == 1 ? ch.h.y : i == 2 ? ch.h.z : ch.h.w;
+        const int sh = 2 * ((c & 3) >> 1);
+        a |= ((hv >> sh) & 0x03030303u) << 4;
+        b |= ((hv >> (sh + 4)) & 0x03030303u) << 4;
+    }
+}
+
+__device__ __forceinline__ float dot4u8(uint32_t q, const float4 x, float acc)
+{
+    acc = fmaf((float)(q & 0xFFu), x.x, acc);
+    acc = fmaf((float)((q >> 8) & 0xFFu), x.y, acc);
+    acc = fmaf((float)((q >> 16) & 0xFFu), x.z, acc);
+    acc = fmaf((float)(q >> 24), x.w, acc);
+    return acc;
+}
+
+/* Lane partial of sum_i w_i x_i over its 32 weights.  xa / xb point at the
+ * 16 floats of runs A / B (16-byte aligned, global or LDS); sxa / sxb are
+ * their sums. */
+template <bool q6>
+__device__ __forceinline__ float q_chunk_dot(const QChunk &ch, int c, const float *xa, const float *xb,
+                                             float sxa, float sxb)
+{
+    float sA, mA, sB, mB;
+    q_scales<q6>(ch, c, sA, mA, sB, mB);
+    float accA = 0.0f, accB = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t qa, qb;
+        q_word<q6>(ch, i, c, qa, qb);
+        accA = dot4u8(qa, *(const float4 *)(xa + 4 * i), accA);
+        accB = dot4u8(qb, *(const float4 *)(xb + 4 * i), accB);
+    }
+    float r = sA * accA;
+    r = fmaf(-mA, sxa, r);
+    r = fmaf(sB, accB, r);
+    r = fmaf(-mB, sxb, r);
+    return r;
+}
+
+__device__ __forceinline__ float sum16(const float *x)
+{
+    float4 a = *(const float4 *)x, b = *(const float4 *)(x + 4), c = *(const float4 *)(x + 8), d = *(const float4 *)(x + 12);
+    return ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)) + (((c.x + c.y) + (c.z + c.w)) + ((d.x + d.y) + (d.z + d.w)));
+}
+
+/* Sum over aligned lane groups of `width` lanes (power of two <= 64). */
+__device__ __forceinline__ float group_sum(float v, int width)
+{
+    for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+#endif

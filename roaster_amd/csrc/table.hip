@@ -1,0 +1,250 @@
+/*
+ * table.hip -- the HBM-resident expert table and synthetic inputs.
+ *
+ * Replaces the reference's per-layer LRU expert cache (weights.c:420-652,
+ * 952-1112): every expert of every layer is uploaded once.  Per layer the
+ * routed experts of one matrix kind are contiguous, [E][rows][row_bytes], which
+ * is exactly the GGUF 3-D *_exps tensor (weights.c:380-419 slices expert e at
+ * e * size / E), followed by the shared expert's three matrices.  Routers
+ * ([E x H] f32) and shared-gate vectors ([H] f32) sit in a second allocation.
+ */
+#include "internal.h"
+#include "decode.h"
+#include "table.h"
+#include "synth.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#include <vector>
+
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+extern "C" RoasterTable *roaster_table_create(const RoasterTableDesc *d)
+{
+    std::lock_guard<std::recursive_mutex> g(rt_lock());
+    if (rt_init_locked()) return NULL;
+    if (!d || d->n_layers <= 0 || d->n_experts < RTOPK || d->n_experts > 4096 || !d->hidden || !d->inter ||
+        d->hidden % RQK || d->inter % RQK || d->hidden > 2048 || d->inter > 2048) {
+        rt_fail(ROASTER_EINVAL, "invalid table description");
+        return NULL;
+    }
+    RoasterTable *t = new RoasterTable();
+    t->d = *d;
+    const size_t H = d->hidden, I = d->inter, E = (size_t)d->n_experts;
+    t->eb[0] = rq_mat_bytes(d->q6[0], I, H);
+    t->eb[1] = rq_mat_bytes(d->q6[1], I, H);
+    t->eb[2] = rq_mat_bytes(d->q6[2], H, I);
+    t->sb[0] = rq_mat_bytes(d->sh_q6[0], I, H);
+    t->sb[1] = rq_mat_bytes(d->sh_q6[1], I, H);
+    t->sb[2] = rq_mat_bytes(d->sh_q6[2], H, I);
+    size_t off = 0;
+    for (int k = 0; k < 3; k++) { t->off_exps[k] = off; off += align256(E * t->eb[k]); }
+    for (int k = 0; k < 3; k++) { t->off_sh[k] = off; off += align256(t->sb[k]); }
+    t->layer_bytes = off;
+    t->qbytes = off * (size_t)d->n_layers;
+    t->fbytes = (size_t)d->n_layers * (E * H + H) * sizeof(float);
+    if (hipMalloc((void **)&t->qmem, t->qbytes) != hipSuccess ||
+        hipMalloc((void **)&t->fmem, t->fbytes) != hipSuccess ||
+        hipMalloc((void **)&t->layers_d, sizeof(DecLayer) * d->n_layers) != hipSuccess) {
+        (void)hipGetLastError();
+        rt_fail(ROASTER_ENOMEM, "expert table of %zu bytes does not fit in HBM", t->qbytes + t->fbytes);
+        if (t->qmem) (void)hipFree(t->qmem);
+        if (t->fmem) (void)hipFree(t->fmem);
+        delete t;
+        return NULL;
+    }
+    rt_register_device_range(t->qmem, t->qbytes);
+    rt_register_device_range(t->fmem, t->fbytes);
+    t->layers_h.resize(d->n_layers);
+    for (int l = 0; l < d->n_layers; l++) {
+        DecLayer &L = t->layers_h[l];
+        uint8_t *base = t->qmem + (size_t)l * t->layer_bytes;
+        L.gate = base + t->off_exps[0];
+        L.up = base + t->off_exps[1];
+        L.down = base + t->off_exps[2];
+        L.sgate = base + t->off_sh[0];
+        L.sup = base + t->off_sh[1];
+        L.sdown = base + t->off_sh[2];
+        L.router = t->fmem + (size_t)l * (E * H + H);
+        L.gate_inp = L.router + E * H;
+    }
+    if (rt_check(hipMemcpy(t->layers_d, t->layers_h.data(), sizeof(DecLayer) * d->n_layers, hipMemcpyHostToDevice),
+                 "layer table upload")) {
+        roaster_table_destroy(t);
+        return NULL;
+    }
+    return t;
+}
+
+extern "C" void roaster_table_destroy(RoasterTable *t)
+{
+    std::lock_guard<std::recursive_mutex> g(rt_lock());
+    if (!t) return;
+    (void)hipStreamSynchronize(rt().stream);
+    rt_unregister_device_range(t->qmem);
+    rt_unregister_device_range(t->fmem);
+    (void)hipFree(t->qmem);
+    (void)hipFree(t->fmem);
+    (void)hipFree(t->layers_d);
+    delete t;
+}
+
+extern "C" size_t roaster_table_bytes(const RoasterTable *t) { return t ? t->qbytes + t->fbytes : 0; }
+
+static uint8_t *mat_ptr(const RoasterTable *t, int layer, int expert, int kind)
+{
+    uint8_t *base = t->qmem + (size_t)layer * t->layer_bytes;
+    if (expert == t->d.n_experts) return base + t->off_sh[kind];
+    return base + t->off_exps[kind] + (size_t)expert * t->eb[kind];
+}
+
+static size_t mat_bytes(const RoasterTable *t, int expert, int kind)
+{
+    return expert == t->d.n_experts ? t->sb[kind] : t->eb[kind];
+}
+
+extern "C" int roaster_table_set_expert(RoasterTable *t, int layer, int expert, const void *gate, const void *up,
+                                        const void *down)
+{
+    std::lock_guard<std::recursive_mutex> g(rt_lock());
+    if (!t || layer < 0 || layer >= t->d.n_layers || expert < 0 || expert > t->d.n_experts || !gate || !up || !down)
+        return rt_fail(ROASTER_EINVAL, "roaster_table_set_expert: bad arguments");
+    const void *src[3] = { gate, up, down };
+    for (int k = 0; k < 3; k++)
+        if (rt_check(hipMemcpy(mat_ptr(t, layer, expert, k), src[k], mat_bytes(t, expert, k), hipMemcpyHostToDevice),
+                     "expert upload"))
+            return ROASTER_EDEVICE;
+    return 0;
+}
+
+extern "C" int roaster_table_set_exps(RoasterTable *t, int layer, int kind, const void *data, size_t bytes)
+{
+    std::lock_guard<std::recursive_mutex> g(rt_lock());
+    if (!t || layer < 0 || layer >= t->d.n_layers || kind < 0 || kind > 2 || !data ||
+        bytes != (size_t)t->d.n_experts * t->eb[kind])
+        return rt_fail(ROASTER_EINVAL, "roaster_table_set_exps: bad arguments (expected %zu bytes)",
+                       t ? (size_t)t->d.n_experts * t->eb[kind < 0 || kind > 2 ? 0 : kind] : 0);
+    return rt_check(hipMemcpy(mat_ptr(t, layer, 0, kind), data, bytes, hipMemcpyHostToDevice), "exps upload")
+               ? ROASTER_EDEVICE : 0;
+}
+
+extern "C" int roaster_table_set_router(RoasterTable *t, int layer, const float *router, const float *gate_inp)
+{
+    std::lock_guard<std::recursive_mutex> g(rt_lock());
+    if (!t || layer < 0 || layer >= t->d.n_layers || !router || !gate_inp)
+        return rt_fail(ROASTER_EINVAL, "roaster_table_set_router: bad arguments");
+    const DecLayer &L = t->layers_h[layer];
+    const size_t EH = (size_t)t->d.n_experts * t->d.hidden;
+    if (rt_check(hipMemcpy((void *)L.router, router, EH * 4, hipMemcpyHostToDevice), "router upload") ||
+        rt_check(hipMemcpy((void *)L.gate_inp, gate_inp, t->d.hidden * 4, hipMemcpyHostToDevice), "gate upload"))
+        return ROASTER_EDEVICE;
+    return 0;
+}
+
+extern "C" int roaster_table_expert_ptrs(const RoasterTable *t, int layer, int expert, const void **gate,
+                                         const void **up, const void **down)
+{
+    if (!t || layer < 0 || layer >= t->d.n_layers || expert < 0 || expert > t->d.n_experts)
+        return rt_fail(ROASTER_EINVAL, "roaster_table_expert_ptrs: bad arguments");
+    if (gate) *gate = mat_ptr(t, layer, expert, 0);
+    if (up) *up = mat_ptr(t, layer, expert, 1);
+    if (down) *down = mat_ptr(t, layer, expert, 2);
+    return 0;
+}
+
+/* ---- synthetic inputs ----------------------------------------------------- */
+extern "C" uint64_t roaster_synth_stream(int layer, int expert, int kind) { return rs_stream(layer, expert, kind); }
+
+extern "C" void roaster_synth_q4k(uint64_t seed, uint64_t stream, size_t nblocks, float lo, float hi, void *out)
+{
+    const uint64_t key = rs_key(seed, stream);
+    for (size_t b = 0; b < nblocks; b++) rs_q4k_block(key, b, lo, hi, (uint8_t *)out + b * RQ4K_BYTES);
+}
+
+extern "C" void roaster_synth_q6k(uint64_t seed, uint64_t stream, size_t nblocks, float lo, float hi, void *out)
+{
+    const uint64_t key = rs_key(seed, stream);
+    for (size_t b = 0; b < nblocks; b++) rs_q6k_block(key, b, lo, hi, (uint8_t *)out + b * RQ6K_BYTES);
+}
+
+/* Box-Muller, one normal per counter pair, computed in double. */
+extern "C" void roaster_synth_normal(uint64_t seed, uint64_t stream, size_t n, float sigma, float *out)
+{
+    const uint64_t key = rs_key(seed, stream);
+    for (size_t i = 0; i < n; i++) {
+        const uint64_t r1 = rs_at(key, 2 * i), r2 = rs_at(key, 2 * i + 1);
+        const double u1 = ((double)(r1 >> 11) + 1.0) * 0x1p-53;
+        const double u2 = (double)(r2 >> 11) * 0x1p-53;
+        const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+        out[i] = (float)(z * (double)sigma);
+    }
+}
+
+/* One thread per super-block of a set of consecutive matrices (one kind of
+ * one layer: E routed experts, matrix m at dst + m * mat_bytes). */
+__global__ void synth_blocks_kernel(uint8_t *dst, size_t mat_bytes, size_t blocks_per_mat, int nmat,
+                                    uint64_t seed, int layer, int expert0, int kind, int q6, float lo, float hi)
+{
+    const size_t total = blocks_per_mat * (size_t)nmat;
+    for (size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x; gid < total;
+         gid += (size_t)gridDim.x * blockDim.x) {
+        const int m = (int)(gid / blocks_per_mat);
+        const size_t b = gid % blocks_per_mat;
+        const uint64_t key = rs_key(seed, rs_stream(layer, expert0 + m, kind));
+        uint8_t *o = dst + (size_t)m * mat_bytes;
+        if (!q6) {
+            uint8_t blk[RQ4K_BYTES];
+            rs_q4k_block(key, b, lo, hi, blk);
+            uint32_t *w = (uint32_t *)(o + b * RQ4K_BYTES);
+            for (int i = 0; i < RQ4K_BYTES / 4; i++)
+                w[i] = blk[4 * i] | (blk[4 * i + 1] << 8) | (blk[4 * i + 2] << 16) | ((uint32_t)blk[4 * i + 3] << 24);
+        } else {
+            uint8_t blk[RQ6K_BYTES];
+            rs_q6k_block(key, b, lo, hi, blk);
+            uint16_t *w = (uint16_t *)(o + b * RQ6K_BYTES);
+            for (int i = 0; i < RQ6K_BYTES / 2; i++) w[i] = (uint16_t)(blk[2 * i] | (blk[2 * i + 1] << 8));
+        }
+    }
+}
+
+extern "C" int roaster_table_synth(RoasterTable *t, uint64_t seed, const RoasterSynthSpec *spec)
+{
+    std::lock_guard<std::recursive_mutex> g(rt_lock());
+    if (!t) return rt_fail(ROASTER_EINVAL, "roaster_table_synth: NULL table");
+    RoasterSynthSpec s = { 1e-3f, 2e-2f, 1e-3f, 1e-2f, 0.02f, 0.02f };
+    if (spec) s = *spec;
+    const RoasterTableDesc &d = t->d;
+    const size_t H = d.hidden, I = d.inter, E = (size_t)d.n_experts;
+    hipStream_t st = rt().stream;
+    for (int l = 0; l < d.n_layers; l++) {
+        for (int k = 0; k < 3; k++) {
+            const size_t rows = k == 2 ? H : I, cols = k == 2 ? I : H;
+            const size_t bpm = rows * (cols / RQK);
+            for (int shared = 0; shared < 2; shared++) {
+                const int q6 = shared ? d.sh_q6[k] : d.q6[k];
+                const int nmat = shared ? 1 : (int)E;
+                const int e0 = shared ? (int)E : 0;
+                uint8_t *dst = mat_ptr(t, l, e0, k);
+                const size_t mb = mat_bytes(t, e0, k);
+                const float lo = q6 ? s.q6k_lo : s.q4k_lo, hi = q6 ? s.q6k_hi : s.q4k_hi;
+                const size_t total = bpm * (size_t)nmat;
+                const int blocks = (int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
+                hipLaunchKernelGGL(synth_blocks_kernel, dim3(blocks), dim3(256), 0, st, dst, mb, bpm, nmat, seed, l,
+                                   e0, k, q6, lo, hi);
+                if (rt_check(hipGetLastError(), "synth launch")) return ROASTER_EDEVICE;
+            }
+        }
+    }
+    std::vector<float> router(E * H), gi(H);
+    for (int l = 0; l < d.n_layers; l++) {
+        roaster_synth_normal(seed, roaster_synth_stream(l, 0, 3), E * H, s.router_sigma, router.data());
+        roaster_synth_normal(seed, roaster_synth_stream(l, 0, 4), H, s.gate_inp_sigma, gi.data());
+        const DecLayer &L = t->layers_h[l];
+        if (rt_check(hipMemcpyAsync((void *)L.router, router.data(), E * H * 4, hipMemcpyHostToDevice, st), "router") ||
+            rt_check(hipMemcpyAsync((void *)L.gate_inp, gi.data(), H * 4, hipMemcpyHostToDevice, st), "gate_inp") ||
+            rt_check(hipStreamSynchronize(st), "synth sync"))
+            return ROASTER_EDEVICE;
+    }
+    return 0;
+}
