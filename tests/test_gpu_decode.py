@@ -1,0 +1,154 @@
+"""GPU parity of the table-based decode path (roaster_moe_decode and
+roaster_moe_decode_stack) against the oracle (model.c:1059-1146 and the
+model.c:1349-1358 layer carry).
+
+Bars: top-8 ids are bit-exact given identical router logits (ties to the lower
+index); FFN outputs are within max|d| / max|y| <= 2e-3 (fp32 accumulation),
+and in practice far inside it, so a tighter 1e-4 regression bound is also held.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import roaster_amd as R
+from oracle import oracle as O
+from gpu_util import Dev, SynthTable, log, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+TIGHT = 1e-4
+
+
+@pytest.fixture(scope="module")
+def cfg2():
+    log("building config-2 table (seed 1)")
+    t = SynthTable(1)
+    yield t
+    t.destroy()
+
+
+def test_table_synth_matches_host_generator(cfg2):
+    for e in (0, 77, 255, 256):
+        g = C.c_void_p()
+        u = C.c_void_p()
+        d = C.c_void_p()
+        R.check(R.lib().roaster_table_expert_ptrs(cfg2.t, 0, e, C.byref(g), C.byref(u), C.byref(d)))
+        for ptr, host in zip((g, u, d), cfg2.expert(0, e)):
+            got = np.empty(host.nbytes, np.uint8)
+            R.check(R.lib().roaster_d2h(got.ctypes.data, ptr.value, host.nbytes))
+            assert np.array_equal(got, host), e
+
+
+def decode(table, x, B, logits_in=None, layer=0):
+    E = table.desc.n_experts
+    dx = Dev(x)
+    dy = Dev(nbytes=B * 2048 * 4, shape=(B, 2048))
+    dl = Dev(nbytes=B * E * 4, shape=(B, E))
+    di = Dev(nbytes=B * 8 * 4, dtype=np.int32, shape=(B, 8))
+    dw = Dev(nbytes=B * 8 * 4, shape=(B, 8))
+    dli = Dev(logits_in) if logits_in is not None else None
+    io = R.RoasterDecodeIO(dli.p if dli else None, dl.p, di.p, dw.p)
+    R.check(R.lib().roaster_moe_decode(table.t, layer, dx.p, B, dy.p, C.byref(io)), "decode")
+    R.check(R.lib().roaster_sync(), "sync")
+    return dy.get(), dl.get(), di.get(), dw.get()
+
+
+def test_cfg2_decode_single_token(cfg2):
+    log("config 2 decode B=1")
+    x = R.synth_normal(1, R.synth_stream(0, 0, 5), 2048)
+    y, lg, ids, w = decode(cfg2, x[None, :], 1)
+    router, _ = cfg2.router(0)
+    lg_ref = O.matvec_f32(router, x)
+    assert rel_err(lg[0], lg_ref) <= 1e-5
+    ids_ref, w_ref = O.select_top8(lg[0])                  # identical logits -> identical ids
+    assert ids[0].tolist() == ids_ref.tolist()
+    np.testing.assert_allclose(w[0], w_ref, rtol=1e-6, atol=1e-7)
+    L = cfg2.oracle_layer(0, set(ids_ref.tolist()))
+    rc, y_ref, _, _, _ = L.decode(x, logits_in=lg[0])
+    assert rc == 0
+    err = rel_err(y[0], y_ref)
+    log(f"config 2: max|d|/max|y| = {err:.3e}")
+    assert err <= TOL and err <= TIGHT
+
+
+def test_decode_given_logits_ties_and_batch(cfg2):
+    """Identical logits with ties: ids bit-exact (lower index first); B = 8
+    tokens give each token's B = 1 result."""
+    B = 8
+    X = np.stack([R.synth_normal(11, R.synth_stream(0, t, 5), 2048) for t in range(B)])
+    lg = np.stack([R.synth_normal(12, R.synth_stream(0, t, 7), 256) for t in range(B)])
+    lg[1, [5, 9, 13, 40]] = 4.0              # four-way tie
+    lg[2, :] = 0.0                           # all equal: ids 0..7
+    lg[3, [0, 255]] = np.inf
+    lg[3, [1, 2]] = np.nan
+    yb, _, idb, wb = decode(cfg2, X, B, logits_in=lg)
+    need = set()
+    for t in range(B):
+        ids_ref, w_ref = O.select_top8(lg[t])
+        assert idb[t].tolist() == ids_ref.tolist(), t
+        need |= set(ids_ref.tolist())
+    L = cfg2.oracle_layer(0, need)
+    for t in range(B):
+        if t == 3:
+            continue                          # +inf logits: weights are NaN in both paths
+        rc, y_ref, _, _, _ = L.decode(np.ascontiguousarray(X[t]), logits_in=lg[t])
+        assert rc == 0
+        assert rel_err(yb[t], y_ref) <= TIGHT, t
+        y1, _, id1, _ = decode(cfg2, X[t:t + 1], 1, logits_in=lg[t:t + 1])
+        assert id1[0].tolist() == idb[t].tolist()
+        np.testing.assert_array_equal(y1[0], yb[t])
+
+
+def test_decode_reports_routing_failure(cfg2):
+    x = R.synth_normal(1, 3, 2048)[None, :]
+    lg = np.full((1, 256), -np.inf, np.float32)
+    lg[0, :3] = 1.0
+    dx, dy, dl = Dev(x), Dev(nbytes=2048 * 4), Dev(lg)
+    io = R.RoasterDecodeIO(dl.p, None, None, None)
+    R.check(R.lib().roaster_moe_decode(cfg2.t, 0, dx.p, 1, dy.p, C.byref(io)))
+    assert R.lib().roaster_sync() == R.EROUTE
+    assert R.lib().roaster_sync() == 0        # the error is reported once
+
+
+def oracle_stack(table, h0, n_layers, eps=1e-6):
+    """h <- h + MoE_l(RMSNorm(h)) per layer with unit norm weights, per token."""
+    B, H = h0.shape
+    ones = np.ones(H, np.float32)
+    h = h0.copy()
+    ids_all = np.zeros((n_layers, B, 8), np.int32)
+    for l in range(n_layers):
+        router, _ = table.router(l)
+        for t in range(B):
+            xn = np.empty(H, np.float32)
+            O.orc().orc_rmsnorm(xn.ctypes.data, h[t].ctypes.data, ones.ctypes.data, H, C.c_float(eps))
+            lg = O.matvec_f32(router, xn)
+            ids, _ = O.select_top8(lg)
+            L = table.oracle_layer(l, set(ids.tolist()))
+            rc, y, _, ids2, _ = L.decode(xn)
+            assert rc == 0
+            ids_all[l, t] = ids2
+            h[t] = h[t] + y
+    return h, ids_all
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_decode_stack_4_layers(B):
+    log(f"decode stack 4 layers B={B}")
+    t = SynthTable(3, n_layers=4)
+    try:
+        h0 = np.stack([R.synth_normal(3, R.synth_stream(0, i, 5), 2048) for i in range(B)])
+        dh = Dev(h0)
+        di = Dev(nbytes=4 * B * 8 * 4, dtype=np.int32, shape=(4, B, 8))
+        R.check(R.lib().roaster_moe_decode_stack(t.t, dh.p, B, 0, 4, None, C.c_float(1e-6), di.p, None))
+        R.check(R.lib().roaster_sync())
+        h = dh.get()
+        ids = di.get()
+        h_ref, ids_ref = oracle_stack(t, h0, 4)
+        assert np.array_equal(ids, ids_ref)
+        err = rel_err(h - h0, h_ref - h0)
+        log(f"stack B={B}: max|d|/max|ffn| = {err:.3e}")
+        assert err <= TOL and err <= TIGHT
+    finally:
+        t.destroy()
