@@ -300,7 +300,6 @@ extern "C" int kernel_ffn_fused(const KernelFfnExpert *ex, int n, const float *x
     if (inter > 2048 || hidden > 2048) return 0;     /* one wave pass per row: <= 8 super-blocks */
     kernel_matvec_quant_end();
     if (rt_init_locked()) return 0;
-    if (((hidden + rt().n_cu - 1) / rt().n_cu + 3) / 4 * 4 > 64) return 0;
     RtState &R = rt();
     DecActive hx[9];
     memset(hx, 0, sizeof(hx));
@@ -360,18 +359,8 @@ static int dec_scratch(DecArgs &A)
     A.logits = (float *)rt_scratch(SCR_D, B * E * 4);
     A.sgate_raw = (float *)rt_scratch(SCR_E, B * 4);
     A.eh = (float *)rt_scratch(SCR_F, B * 9 * (size_t)A.I * 4);
-    return A.logits && A.sgate_raw && A.eh ? 0 : ROASTER_ENOMEM;
-}
-
-static int g_decode_split = -1;   /* ROASTER_DECODE_SPLIT=1: one launch per phase */
-
-static int decode_fused()
-{
-    if (g_decode_split < 0) {
-        const char *s = getenv("ROASTER_DECODE_SPLIT");
-        g_decode_split = s && s[0] == '1';
-    }
-    return !g_decode_split;
+    A.xn_g = (float *)rt_scratch(SCR_B, B * ((size_t)A.H + A.H / 16) * 4);
+    return A.logits && A.sgate_raw && A.eh && A.xn_g ? 0 : ROASTER_ENOMEM;
 }
 
 extern "C" int roaster_moe_decode(RoasterTable *t, int layer, const float *x, int B, float *y,
@@ -395,7 +384,7 @@ extern "C" int roaster_moe_decode(RoasterTable *t, int layer, const float *x, in
         A.w_out = io->w_out;
     }
     if (dec_scratch(A)) return ROASTER_ENOMEM;
-    int rc = dec_launch(A, decode_fused());
+    int rc = dec_launch(A);
     if (rc) return rc;
     if (io && io->logits_out) {
         const float *src = A.logits_in ? A.logits_in : A.logits;
@@ -426,7 +415,7 @@ extern "C" int roaster_moe_decode_stack(RoasterTable *t, float *h, int B, int la
     A.ids_out = ids_out;
     A.w_out = w_out;
     if (dec_scratch(A)) return ROASTER_ENOMEM;
-    return dec_launch(A, decode_fused());
+    return dec_launch(A);
 }
 
 /* ---- small vector kernels (off the MoE path, kept for link compatibility) -- */

@@ -28,12 +28,16 @@ struct DecActive {
 };
 
 struct DecPlan {
-    int nact;
+    int nact;               /* active experts: [0, nroute) routed, then the shared expert */
+    int nroute;
     int err;
+    int pad0;
     DecActive a[RMAX_ACT];
     int ids[8][8];
     float w[8][9];          /* routing weights, [8] = sigmoid(shared gate logit) */
+    int pad1[2];
 };
+static_assert(sizeof(DecPlan) % 16 == 0, "DecPlan is copied in 16-byte units");
 
 struct DecArgs {
     const DecLayer *layers;     /* device array indexed by layer */
@@ -50,9 +54,10 @@ struct DecArgs {
     float *logits;              /* [B x E] */
     float *sgate_raw;           /* [B] */
     float *eh;                  /* [B*9 x I] */
+    float *xn_g;                /* [B x H] normalised input + [B x H/16] run sums, published by R */
     int *ids_out;               /* [nlayers x B x 8] or NULL */
     float *w_out;
-    unsigned *bar;
+    DecPlan *plan_g;            /* plan written by the gate/up kernel, read by the down kernel */
     int *err;
     /* kernel_ffn_fused mode */
     const DecActive *ffn_ex;    /* [n] device */
@@ -60,8 +65,7 @@ struct DecArgs {
     float *ffn_out;             /* [n x H] or NULL */
 };
 
-size_t dec_lds_bytes(int B, int H);
-int dec_launch(DecArgs &A, int fused);
-int dec_ffn_launch(DecArgs &A);
+int dec_launch(DecArgs &A);          /* all layers of A: 3 kernels per layer */
+int dec_ffn_launch(DecArgs &A);      /* kernel_ffn_fused: gate/up + down kernels */
 
 #endif

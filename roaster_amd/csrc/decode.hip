@@ -4,23 +4,24 @@
  * Reference path: model.c:1059-1146 (moe_forward) and kernels.c:1703-1830
  * (kernel_ffn_fused); the layer carry h += MoE(RMSNorm(h)) is model.c:1349-1358.
  *
- * One kernel body, four phases per layer:
- *   R  RMSNorm of h (stack) into LDS, router logits W_r x (f32) and the
- *      shared-expert gate logit gate_inp . x.
- *   P  top-8 per token (strict '>' insertion order => ties to the lower index,
- *      NaN / -inf never selected; model.c:869-897) and the union of selected
- *      experts into an "active expert" plan, built redundantly in every
- *      workgroup's LDS (deterministic, no extra grid sync).
- *   GU gate and up rows of every active expert for each of its tokens,
- *      eh = silu(g) * u  (model.c:1122-1126).
- *   D  down rows; each workgroup owns a slice of output rows for all active
- *      experts and combines them in the reference order
- *      y = sum_k w_k d_k (k = 0..7) + sigmoid(s) d_shared  (model.c:1139-1144).
- * Fused mode runs all phases of all layers in one cooperative launch with grid
- * barriers between R->GU (logits complete), GU->D (eh complete) and D->R (h
- * complete).  Split mode launches one phase per kernel (same code).
+ * A layer is three kernels on one stream (a kernel boundary is the cheapest
+ * device-wide dependency on MI355X, ~2.5 us, well below a cooperative grid
+ * barrier across 8 XCDs):
+ *   R   RMSNorm of h into LDS (each workgroup, redundantly), router logits
+ *       W_r x (f32), the shared-gate logit gate_inp . x and the shared
+ *       expert's gate/up rows (they need no routing): eh_shared = silu(g)*u.
+ *   GU  top-8 per token from the logits (strict '>' insertion order: ties go
+ *       to the lower index, NaN / -inf never enter; model.c:869-897), the
+ *       union of the tokens' experts as an "active expert" plan (built
+ *       identically in every workgroup; workgroup 0 publishes it), and every
+ *       routed expert's gate/up rows: eh = silu(g) * u  (model.c:1122-1126).
+ *   D   down rows: each workgroup owns 8 output rows for all active experts
+ *       and combines them in the reference order
+ *       y = sum_{k=0..7} w_k d_k + sigmoid(s) d_shared  (model.c:1139-1144).
+ * Every wave issues all loads of its task set before consuming any (one
+ * memory round trip per dependency instead of one per loop iteration).
  *
- * Weights are read in their native GGML layout: every super-block is read once
+ * Weights are read in their native GGML layout: each super-block is read once
  * per call by 8 lanes (16-byte chunks), scales decoded in registers, lane
  * partials reduced with cross-lane shuffles.  A row is at most 8 super-blocks
  * (hidden, inter <= 2048), so one wave pass covers it.
@@ -32,186 +33,315 @@
 #include <stdio.h>
 #include <string.h>
 
-#define DEC_THREADS 512
-#define DEC_WAVES (DEC_THREADS / 64)
-#define PF 2                          /* tasks prefetched per wave in GU */
+#define DT 256                        /* threads per workgroup */
+#define DW (DT / 64)                  /* waves per workgroup */
+#define GU_PF 2                       /* tasks in flight per wave */
+#define D_ROWS 4                      /* output rows per down workgroup */
+#define D_PF 4                        /* down tasks in flight per wave */
 
-/* ---- grid barrier ----------------------------------------------------------
- * Monotonic arrival counter (zeroed before launch).  Barrier number k waits for
- * k * gridDim.x arrivals.  The wait is bounded: after ~2^26 polls the flag
- * err |= 2 is raised and the wave proceeds, so every wave always exits. */
-__device__ __forceinline__ void grid_sync(unsigned *bar, unsigned &epoch, int *err)
+/* Opt-in phase tracing (build with -DROASTER_PHASE_TS): thread 0 of every
+ * workgroup records the 100 MHz real-time counter at phase boundaries;
+ * roaster_phase_ts() copies the [kernel][workgroup][mark] table out. */
+#ifdef ROASTER_PHASE_TS
+__device__ unsigned long long g_phase_ts[3][1024][8];
+#define PHASE_TS(k, i)                                                                      \
+    do {                                                                                    \
+        if (threadIdx.x == 0 && blockIdx.x < 1024)                                          \
+            g_phase_ts[k][blockIdx.x][i] = __builtin_amdgcn_s_memrealtime();                \
+    } while (0)
+extern "C" int roaster_phase_ts(unsigned long long *out)
 {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    epoch += 1;
-    if (threadIdx.x == 0) {
-        const unsigned target = epoch * gridDim.x;
-        __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        unsigned polls = 0;
-        while (__hip_atomic_load(bar, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++polls > (1u << 26)) {
-                __hip_atomic_fetch_or(err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-        }
-    }
-    __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_phase_ts), sizeof(g_phase_ts));
 }
-
-/* ---- LDS layout ---------------------------------------------------------- */
-struct DecShared {
-    DecPlan plan;
-    float red[DEC_WAVES][RMAX_B];
-    float inv_rms[RMAX_B];
-};
+#else
+#define PHASE_TS(k, i) do { } while (0)
+#endif
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
 
-/* xn[t][:] (LDS) and its 16-column run sums.  Stack mode normalises h
- * (kernels.c:584-605 semantics: x * (1/sqrt(mean(x^2)+eps)) * w). */
-__device__ void phase_norm(const DecArgs &A, int l, DecShared &S, float *xn, float *xsum)
+__device__ __forceinline__ int first_of(int begin, int w, int n)
+{
+    return begin + ((w - begin) % n + n) % n;
+}
+
+/* Copy n16 16-byte units global -> LDS, 8 units per thread per round: all
+ * loads of a round are issued before its first store, so a round costs one
+ * memory round trip (one round covers 32 KB). */
+__device__ __forceinline__ void block_copy16(void *dst, const void *src, int n16)
+{
+    for (int base = 0; base < n16; base += 8 * DT) {
+        uint4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = base + threadIdx.x + k * DT;
+            v[k] = i < n16 ? ((const uint4 *)src)[i] : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = base + threadIdx.x + k * DT;
+            if (i < n16) ((uint4 *)dst)[i] = v[k];
+        }
+    }
+}
+
+/* xn[t][:] (LDS) = RMSNorm(h[t]) or a copy of x, and its 16-column run sums.
+ * RMSNorm follows kernels.c:584-605: x * (1/sqrt(mean(x^2) + eps)) * w. */
+__device__ void block_norm(const DecArgs &A, int l, float *xn, float *xsum, float (*red)[RMAX_B], float *inv_rms)
 {
     const int H = A.H, B = A.B;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const float *src = A.h;
+    block_copy16(xn, A.h, B * H / 4);
+    __syncthreads();
     if (A.do_norm) {
         for (int t = 0; t < B; t++) {
             float ss = 0.0f;
-            for (int i = tid; i < H; i += DEC_THREADS) { float v = src[(size_t)t * H + i]; ss = fmaf(v, v, ss); }
-            ss = group_sum(ss, 64);
-            if (lane == 0) S.red[wv][t] = ss;
+            for (int i = tid; i < H; i += DT) { const float v = xn[t * H + i]; ss = fmaf(v, v, ss); }
+            ss = group_sum<64>(ss);
+            if (lane == 0) red[wv][t] = ss;
         }
         __syncthreads();
         if (tid < B) {
             float ss = 0.0f;
-            for (int w = 0; w < DEC_WAVES; w++) ss += S.red[w][tid];
-            S.inv_rms[tid] = 1.0f / sqrtf(ss / (float)H + A.eps);
+            for (int w = 0; w < DW; w++) ss += red[w][tid];
+            inv_rms[tid] = 1.0f / sqrtf(ss / (float)H + A.eps);
         }
         __syncthreads();
         const float *nw = A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * H : NULL;
         for (int t = 0; t < B; t++) {
-            const float inv = S.inv_rms[t];
-            for (int i = tid; i < H; i += DEC_THREADS) {
-                float v = src[(size_t)t * H + i] * inv;
+            const float inv = inv_rms[t];
+            for (int i = tid; i < H; i += DT) {
+                const float v = xn[t * H + i] * inv;
                 xn[t * H + i] = nw ? v * nw[i] : v;
             }
         }
-    } else {
-        for (int t = 0; t < B; t++)
-            for (int i = tid; i < H; i += DEC_THREADS) xn[t * H + i] = src[(size_t)t * H + i];
+        __syncthreads();
     }
-    __syncthreads();
-    for (int r = tid; r < B * (H / 16); r += DEC_THREADS) xsum[r] = sum16(xn + r * 16);
+    for (int r = tid; r < B * (H / 16); r += DT) xsum[r] = sum16(xn + r * 16);
     __syncthreads();
 }
 
-/* Router logits and shared gate logits: row e < E is W_r[e], row E is gate_inp.
- * Rows are spread over all waves of the grid; each row is one wave, lane owns
- * columns 4*lane + 256*m. */
-__device__ void phase_router(const DecArgs &A, const DecLayer &L, const float *xn)
+template <bool G6, bool U6>
+__device__ __forceinline__ QChunk2 load_gu_pair(const uint8_t *g, const uint8_t *u, int j, int nb, int lb, int c)
 {
-    const int H = A.H, B = A.B, E = A.E;
-    const int lane = threadIdx.x & 63;
-    const int gw = blockIdx.x * DEC_WAVES + (threadIdx.x >> 6), nw = gridDim.x * DEC_WAVES;
-    const int first = A.logits_in ? E : 0;
-    for (int e = first + gw; e <= E; e += nw) {
-        const float *row = e < E ? L.router + (size_t)e * H : L.gate_inp;
+    QChunk2 r;
+    r.g = q_load<G6>(g + ((size_t)j * nb + lb) * (G6 ? RQ6K_BYTES : RQ4K_BYTES), c);
+    r.u = q_load<U6>(u + ((size_t)j * nb + lb) * (U6 ? RQ6K_BYTES : RQ4K_BYTES), c);
+    return r;
+}
+
+/* eh[p][j] = silu(gate_j . x_t) * (up_j . x_t) for the (t, slot) pairs p of one
+ * expert, given the lane's chunks of gate row j and up row j. */
+template <bool G6, bool U6>
+__device__ __forceinline__ void gu_row(const DecArgs &A, int j, const QChunk2 &ch, int ntok, const int *tk,
+                                       const float *xn, const float *xsum)
+{
+    const int H = A.H, I = A.I, nb = H / RQK;
+    const int lane = threadIdx.x & 63, c = lane & 7, lb = lane >> 3;
+    const int ga = lb * RQK + q_run_a<G6>(c), gb = ga + q_run_b_off<G6>();
+    const int ua = lb * RQK + q_run_a<U6>(c), ub = ua + q_run_b_off<U6>();
+    for (int i = 0; i < ntok; i++) {
+        const int p = tk[i], t = p / 9;
+        const float *x = xn + t * H, *xs = xsum + t * (H / 16);
+        float pg = 0.0f, pu = 0.0f;
+        if (lb < nb) {
+            pg = q_chunk_dot<G6>(ch.g, c, x + ga, x + gb, xs[ga >> 4], xs[gb >> 4]);
+            pu = q_chunk_dot<U6>(ch.u, c, x + ua, x + ub, xs[ua >> 4], xs[ub >> 4]);
+        }
+        pg = group_sum<64>(pg);
+        pu = group_sum<64>(pu);
+        if (lane == 0) A.eh[(size_t)p * I + j] = silu_mul(pg, pu);
+    }
+}
+
+/* ---- R: router + shared-gate logit + shared expert gate/up ------------------ */
+extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A, int l)
+{
+    extern __shared__ __align__(16) float lds[];
+    __shared__ float red[DW][RMAX_B];
+    __shared__ float inv_rms[RMAX_B];
+    __shared__ int sh_tk[RMAX_B];
+    const int H = A.H, E = A.E, I = A.I, B = A.B, nb = H / RQK;
+    float *xn = lds, *xsum = lds + B * H;
+    const DecLayer L = A.layers[l];
+    const int lane = threadIdx.x & 63, c = lane & 7, lb = lane >> 3;
+    PHASE_TS(0, 0);
+    const int task = blockIdx.x * DW + (threadIdx.x >> 6);
+    const int nrouter = A.logits_in ? 0 : E;
+    /* task < nrouter: router row; == nrouter: gate_inp; then shared-expert row pairs */
+    const bool is_row = task <= nrouter;
+    const int j = task - nrouter - 1;
+    const bool is_sh = !is_row && j < I;
+    const int kind = (A.sq6g ? 2 : 0) | (A.sq6u ? 1 : 0);
+    if (threadIdx.x < B) sh_tk[threadIdx.x] = threadIdx.x * 9 + 8;
+    /* 1. weight loads first (independent of h) */
+    float4 w[8];
+    QChunk2 ch;
+    if (is_row) {
+        const float *row = task < nrouter ? L.router + (size_t)task * H : L.gate_inp;
+#pragma unroll
+        for (int m = 0; m < 8; m++)
+            if (4 * lane + 256 * m < H) w[m] = *(const float4 *)(row + 4 * lane + 256 * m);
+    } else if (is_sh && lb < nb) {
+        if (kind == 0) ch = load_gu_pair<false, false>(L.sgate, L.sup, j, nb, lb, c);
+        else if (kind == 3) ch = load_gu_pair<true, true>(L.sgate, L.sup, j, nb, lb, c);
+        else if (kind == 2) ch = load_gu_pair<true, false>(L.sgate, L.sup, j, nb, lb, c);
+        else ch = load_gu_pair<false, true>(L.sgate, L.sup, j, nb, lb, c);
+    }
+    /* 2. normalised input into LDS; workgroup 0 publishes it for the gate/up kernel */
+    block_norm(A, l, xn, xsum, red, inv_rms);
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < B * (H + H / 16) / 4; i += DT) ((float4 *)A.xn_g)[i] = ((const float4 *)xn)[i];
+    PHASE_TS(0, 1);
+    /* 3. dots */
+    if (is_row) {
         float acc[RMAX_B];
 #pragma unroll
         for (int t = 0; t < RMAX_B; t++) acc[t] = 0.0f;
-        for (int c0 = 4 * lane; c0 < H; c0 += 256) {
-            float4 w = *(const float4 *)(row + c0);
 #pragma unroll
-            for (int t = 0; t < RMAX_B; t++) {
-                if (t < B) {
-                    float4 x = *(const float4 *)(xn + t * H + c0);
-                    acc[t] = fmaf(w.x, x.x, acc[t]);
-                    acc[t] = fmaf(w.y, x.y, acc[t]);
-                    acc[t] = fmaf(w.z, x.z, acc[t]);
-                    acc[t] = fmaf(w.w, x.w, acc[t]);
+        for (int m = 0; m < 8; m++) {
+            const int c0 = 4 * lane + 256 * m;
+            if (c0 < H) {
+#pragma unroll
+                for (int t = 0; t < RMAX_B; t++) {
+                    if (t < B) {
+                        const float4 x = *(const float4 *)(xn + t * H + c0);
+                        acc[t] = fmaf(w[m].x, x.x, acc[t]);
+                        acc[t] = fmaf(w[m].y, x.y, acc[t]);
+                        acc[t] = fmaf(w[m].z, x.z, acc[t]);
+                        acc[t] = fmaf(w[m].w, x.w, acc[t]);
+                    }
                 }
             }
         }
 #pragma unroll
         for (int t = 0; t < RMAX_B; t++) {
             if (t < B) {
-                float s = group_sum(acc[t], 64);
+                const float s = group_sum<64>(acc[t]);
                 if (lane == 0) {
-                    if (e < E) A.logits[(size_t)t * E + e] = s;
+                    if (task < nrouter) A.logits[(size_t)t * E + task] = s;
                     else A.sgate_raw[t] = s;
                 }
             }
         }
+    } else if (is_sh) {
+        if (kind == 0) gu_row<false, false>(A, j, ch, B, sh_tk, xn, xsum);
+        else if (kind == 3) gu_row<true, true>(A, j, ch, B, sh_tk, xn, xsum);
+        else if (kind == 2) gu_row<true, false>(A, j, ch, B, sh_tk, xn, xsum);
+        else gu_row<false, true>(A, j, ch, B, sh_tk, xn, xsum);
     }
+    PHASE_TS(0, 2);
 }
 
-/* Wave-level top-8 of one token (model.c:869-897) into ids / w. */
-__device__ void topk8_wave(const float *lg, int E, int *ids, float *w, int *bad)
+/* ---- GU: routing plan + routed experts' gate/up ----------------------------- */
+
+/* Order-preserving key of a logit: larger float -> larger unsigned key; NaN
+ * and -inf map to 0 and are never selected (model.c:879 enters a value only
+ * if it is > the current slot, which starts at -inf). */
+__device__ __forceinline__ uint32_t logit_key(float v)
+{
+    if (!(v > -INFINITY)) return 0u;
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_logit(uint32_t k)
+{
+    const uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+    return __builtin_bit_cast(float, u);
+}
+
+/* Wave-level top-8 of one token (model.c:869-897).  Each logit becomes a
+ * distinct 40-bit key (logit key << 8 | 255 - expert), so the order is "larger
+ * logit, then lower index" and no two keys tie; NaN / -inf get key 0.  A radix
+ * select over the 40 bits (ballot counts per bit) finds the 8th largest key,
+ * the (at most 8) keys >= it are ranked in 8 lanes, and the softmax over the
+ * selected logits is summed in slot order like the reference.  v4[i] holds the
+ * logit of expert lane + 64*i (E <= 256).  sk: 16 entries of LDS scratch. */
+__device__ void topk8_wave(const float v4in[4], int E, int *ids, float *w, int *bad, unsigned long long *sk)
 {
     const int lane = threadIdx.x & 63;
-    float val[8];
-    int idx[8];
+    unsigned long long key[4];
 #pragma unroll
-    for (int k = 0; k < RTOPK; k++) {
-        /* best candidate of this lane not yet taken: larger value, then lower index */
-        float bv = -INFINITY;
-        int bi = 0x7FFFFFFF;
-        for (int e = lane; e < E; e += 64) {
-            float v = lg[e];
-            bool taken = false;
+    for (int i = 0; i < 4; i++) {
+        const int e = lane + 64 * i;
+        const uint32_t k32 = e < E ? logit_key(v4in[i]) : 0u;
+        key[i] = k32 ? (((unsigned long long)k32 << 8) | (unsigned long long)(255 - e)) : 0ull;
+    }
+    unsigned long long P = 0ull;
+    for (int b = 39; b >= 0; b--) {
+        const unsigned long long C = P | (1ull << b);
+        int cnt = 0;
 #pragma unroll
-            for (int j = 0; j < RTOPK; j++) taken |= (j < k && idx[j] == e);
-            if (taken || !(v > -INFINITY)) continue;       /* NaN and -inf never enter */
-            if (v > bv || (v == bv && e < bi)) { bv = v; bi = e; }
-        }
-        for (int off = 32; off > 0; off >>= 1) {
-            float ov = __shfl_xor(bv, off, 64);
-            int oi = __shfl_xor(bi, off, 64);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
-        val[k] = bv;
-        idx[k] = bi == 0x7FFFFFFF ? -1 : bi;
+        for (int i = 0; i < 4; i++) cnt += __popcll(__ballot(key[i] >= C));
+        if (cnt >= RTOPK) P = C;
     }
-    if (lane == 0) {
-        int ok = 1;
-        for (int k = 0; k < RTOPK; k++) ok &= idx[k] >= 0;
-        float mx = val[0], sum = 0.0f, e8[8];
-        for (int k = 0; k < RTOPK; k++) { e8[k] = expf(val[k] - mx); sum += e8[k]; }
-        float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-        for (int k = 0; k < RTOPK; k++) { ids[k] = idx[k]; w[k] = e8[k] * inv; }
-        if (!ok) *bad = 1;
+    /* the selected keys: >= P and valid; compact them into sk[0..nsel) */
+    int base = 0;
+    const unsigned long long lt = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const bool sel = key[i] != 0ull && key[i] >= P;
+        const unsigned long long m = __ballot(sel);
+        if (sel) {
+            const int pos = base + __popcll(m & lt);
+            if (pos < RTOPK) sk[pos] = key[i];
+        }
+        base += __popcll(m);
     }
+    const int nsel = base < RTOPK ? base : RTOPK;
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    /* rank the selected keys (descending) in lanes 0..7 */
+    if (lane < nsel) {
+        const unsigned long long my = sk[lane];
+        int r = 0;
+        for (int j = 0; j < nsel; j++) r += sk[j] > my;
+        sk[8 + r] = my;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    const unsigned long long kk = lane < nsel ? sk[8 + lane] : 0ull;
+    const int e = kk ? 255 - (int)(kk & 0xFFull) : -1;
+    const float v = kk ? key_logit((uint32_t)(kk >> 8)) : -INFINITY;
+    const float mx = lane_f(v, 0);
+    const float ex = expf(v - mx);
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < RTOPK; k++) sum += lane_f(ex, k);
+    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    if (lane < RTOPK) {
+        ids[lane] = e;
+        w[lane] = ex * inv;
+    }
+    if (lane == 0 && nsel < RTOPK) *bad = 1;
 }
 
-/* Active-expert plan in LDS: union of the tokens' experts in first-appearance
- * order over (t, k), then the shared expert.  pair p = t*9 + k (k = 8: shared). */
-__device__ void phase_plan(const DecArgs &A, const DecLayer &L, int l, DecShared &S)
+/* Active-expert plan: union of the tokens' experts in first-appearance order
+ * over (t, k), then the shared expert.  Pair p = t*9 + k (k = 8: shared).
+ * emask: 256 x 64-bit LDS scratch; sk: 16 x 64-bit per wave. */
+__device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, const float (*lg4)[4], float sg,
+                           unsigned long long *emask, unsigned long long (*sk)[16])
 {
-    DecPlan &P = S.plan;
     const int B = A.B, E = A.E, tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
-    const float *lg = A.logits_in ? A.logits_in : A.logits;
     if (tid == 0) P.err = 0;
     __syncthreads();
-    for (int t = wv; t < B; t += DEC_WAVES) topk8_wave(lg + (size_t)t * E, E, P.ids[t], P.w[t], &P.err);
-    if (tid < B) P.w[tid][8] = 1.0f / (1.0f + expf(-A.sgate_raw[tid]));
+    for (int t = wv, r = 0; t < B; t += DW, r++) topk8_wave(lg4[r], E, P.ids[t], P.w[t], &P.err, sk[wv]);
+    if (tid < B) P.w[tid][8] = 1.0f / (1.0f + expf(-sg));
     __syncthreads();
+    PHASE_TS(1, 4);
     if (wv == 0) {
-        /* lane i = pair (t, k) = (i / 8, i % 8) */
-        const int n = B * RTOPK;
-        int e = lane < n ? P.ids[lane >> 3][lane & 7] : -1;
-        if (e < 0) e = -1;
-        /* lanes with the same expert: compare across the wave */
-        unsigned long long same = 0ull;
-        for (int j = 0; j < n; j++) {
-            int ej = __shfl(e, j, 64);
-            if (ej == e && e >= 0) same |= 1ull << j;
-        }
+        const int n = B * RTOPK;                 /* lane i = pair (i / 8, i % 8) */
+        const int e = lane < n ? P.ids[lane >> 3][lane & 7] : -1;
         const bool valid = e >= 0;
-        const bool leader = valid && ((same & ((1ull << lane) - 1ull)) == 0ull);
-        unsigned long long lead_mask = __ballot(leader);
+        if (valid) emask[e] = 0ull;
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_wave_barrier();
+        if (valid) atomicOr(&emask[e], 1ull << lane);
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_wave_barrier();
+        const unsigned long long m = valid ? emask[e] : 0ull;
+        const bool leader = valid && (__ffsll((long long)m) - 1) == lane;
+        const unsigned long long lead_mask = __ballot(leader);
         const int a = __popcll(lead_mask & ((1ull << lane) - 1ull));
         const int nroute = __popcll(lead_mask);
         if (leader) {
@@ -221,8 +351,10 @@ __device__ void phase_plan(const DecArgs &A, const DecLayer &L, int l, DecShared
             X.d = L.down + (size_t)e * A.bytes_d;
             X.gq6 = A.q6g; X.uq6 = A.q6u; X.dq6 = A.q6d;
             int nt = 0;
-            for (int j = 0; j < n; j++)
-                if (same & (1ull << j)) X.tk[nt++] = (j >> 3) * 9 + (j & 7);
+            for (unsigned long long mm = m; mm; mm &= mm - 1ull) {
+                const int jj = __ffsll((long long)mm) - 1;
+                X.tk[nt++] = (jj >> 3) * 9 + (jj & 7);
+            }
             X.ntok = nt;
         }
         if (lane == 0) {
@@ -231,277 +363,307 @@ __device__ void phase_plan(const DecArgs &A, const DecLayer &L, int l, DecShared
             X.gq6 = A.sq6g; X.uq6 = A.sq6u; X.dq6 = A.sq6d;
             X.ntok = B;
             for (int t = 0; t < B; t++) X.tk[t] = t * 9 + 8;
+            P.nroute = nroute;
             P.nact = nroute + 1;
         }
     }
     __syncthreads();
-    if (blockIdx.x == 0 && tid < B * RTOPK) {
-        const size_t o = ((size_t)(l - A.layer0) * B + (tid >> 3)) * RTOPK + (tid & 7);
-        if (A.ids_out) A.ids_out[o] = P.ids[tid >> 3][tid & 7];
-        if (A.w_out) A.w_out[o] = P.w[tid >> 3][tid & 7];
-    }
-    if (blockIdx.x == 0 && tid == 0 && P.err) atomicOr(A.err, 1);
 }
 
-/* First index >= begin that is congruent to w modulo n. */
-__device__ __forceinline__ int first_of(int begin, int w, int n)
+__device__ void ffn_plan(const DecArgs &A, DecPlan &P)
 {
-    return begin + ((w - begin) % n + n) % n;
+    if (threadIdx.x == 0) {
+        P.nact = A.ffn_n;
+        P.nroute = A.ffn_n;
+        P.err = 0;
+        for (int k = 0; k < A.ffn_n; k++) {
+            P.a[k] = A.ffn_ex[k];
+            P.a[k].ntok = 1;
+            P.a[k].tk[0] = k;
+        }
+    }
+    __syncthreads();
 }
 
-/* Length of the run of active experts starting at a0 that share the given
- * matrix types (all routed experts of a table share them; the shared expert
- * may differ; kernel_ffn_fused experts may each differ). */
-__device__ __forceinline__ int type_run_end(const DecPlan &P, int a0, bool gu)
+__device__ __forceinline__ int type_run_end(const DecPlan &P, int a0, int a_end, bool gu)
 {
     const DecActive &X0 = P.a[a0];
     int a1 = a0 + 1;
-    while (a1 < P.nact && (gu ? (P.a[a1].gq6 == X0.gq6 && P.a[a1].uq6 == X0.uq6) : (P.a[a1].dq6 == X0.dq6))) a1++;
+    while (a1 < a_end && (gu ? (P.a[a1].gq6 == X0.gq6 && P.a[a1].uq6 == X0.uq6) : (P.a[a1].dq6 == X0.dq6))) a1++;
     return a1;
 }
 
-/* Gate/up tasks q = a*I + j for q in [q0, q1), all with types (G6, U6).  The
- * wave loads the chunks of PF tasks first, then computes:
- * eh[p][j] = silu(gate_j . x_t) * (up_j . x_t) for each (t, slot) pair p of a. */
-template <bool G6, bool U6>
+/* Gate/up tasks q = a*I + j for q in [q0, q1), all with types (G6, U6).  Each
+ * wave loads the chunks of GU_PF tasks, then computes them.  With one token
+ * (decode batch 1 and kernel_ffn_fused) the lane's activations are loaded into
+ * registers once and reused by every task. */
+template <bool G6, bool U6, bool ONE>
 __device__ void gu_tasks(const DecArgs &A, const DecPlan &P, int q0, int q1, const float *xn, const float *xsum)
 {
     const int H = A.H, I = A.I, nb = H / RQK;
     const int lane = threadIdx.x & 63, c = lane & 7, lb = lane >> 3;
-    const int gw = blockIdx.x * DEC_WAVES + (threadIdx.x >> 6), nw = gridDim.x * DEC_WAVES;
-    const bool lane_live = lb < nb;
-    const size_t gbs = G6 ? RQ6K_BYTES : RQ4K_BYTES, ubs = U6 ? RQ6K_BYTES : RQ4K_BYTES;
+    const int gw = blockIdx.x * DW + (threadIdx.x >> 6), nw = gridDim.x * DW;
     const int ga = lb * RQK + q_run_a<G6>(c), gb = ga + q_run_b_off<G6>();
     const int ua = lb * RQK + q_run_a<U6>(c), ub = ua + q_run_b_off<U6>();
-    for (int qs = first_of(q0, gw, nw); qs < q1; qs += nw * PF) {
-        QChunk cg[PF], cu[PF];
+    float4 xga[4], xgb[4], xua[4], xub[4];
+    float sga = 0.0f, sgb = 0.0f, sua = 0.0f, sub = 0.0f;
+    if (ONE && lb < nb) {
 #pragma unroll
-        for (int f = 0; f < PF; f++) {
+        for (int i = 0; i < 4; i++) {
+            xga[i] = *(const float4 *)(xn + ga + 4 * i);
+            xgb[i] = *(const float4 *)(xn + gb + 4 * i);
+            xua[i] = *(const float4 *)(xn + ua + 4 * i);
+            xub[i] = *(const float4 *)(xn + ub + 4 * i);
+        }
+        sga = xsum[ga >> 4]; sgb = xsum[gb >> 4]; sua = xsum[ua >> 4]; sub = xsum[ub >> 4];
+    }
+    for (int qs = first_of(q0, gw, nw); qs < q1; qs += nw * GU_PF) {
+        QChunk2 ch[GU_PF];
+#pragma unroll
+        for (int f = 0; f < GU_PF; f++) {
             const int q = qs + f * nw;
-            if (q < q1 && lane_live) {
+            if (q < q1 && lb < nb) {
                 const DecActive &X = P.a[q / I];
-                const int j = q % I;
-                cg[f] = q_load<G6>(X.g + ((size_t)j * nb + lb) * gbs, c);
-                cu[f] = q_load<U6>(X.u + ((size_t)j * nb + lb) * ubs, c);
+                ch[f] = load_gu_pair<G6, U6>(X.g, X.u, q % I, nb, lb, c);
             }
         }
 #pragma unroll
-        for (int f = 0; f < PF; f++) {
+        for (int f = 0; f < GU_PF; f++) {
             const int q = qs + f * nw;
             if (q >= q1) break;
             const DecActive &X = P.a[q / I];
-            const int j = q % I;
-            for (int i = 0; i < X.ntok; i++) {
-                const int p = X.tk[i], t = p / 9;
-                const float *x = xn + t * H;
-                const float *xs = xsum + t * (H / 16);
+            if (ONE) {
                 float pg = 0.0f, pu = 0.0f;
-                if (lane_live) {
-                    pg = q_chunk_dot<G6>(cg[f], c, x + ga, x + gb, xs[ga >> 4], xs[gb >> 4]);
-                    pu = q_chunk_dot<U6>(cu[f], c, x + ua, x + ub, xs[ua >> 4], xs[ub >> 4]);
+                if (lb < nb) {
+                    pg = q_chunk_dot_r<G6>(ch[f].g, c, xga, xgb, sga, sgb);
+                    pu = q_chunk_dot_r<U6>(ch[f].u, c, xua, xub, sua, sub);
                 }
-                pg = group_sum(pg, 64);
-                pu = group_sum(pu, 64);
-                if (lane == 0) A.eh[(size_t)p * I + j] = silu_mul(pg, pu);
+                pg = group_sum<64>(pg);
+                pu = group_sum<64>(pu);
+                if (lane == 0) A.eh[(size_t)X.tk[0] * I + q % I] = silu_mul(pg, pu);
+            } else {
+                gu_row<G6, U6>(A, q % I, ch[f], X.ntok, X.tk, xn, xsum);
             }
         }
     }
 }
 
-__device__ void phase_gu(const DecArgs &A, const DecPlan &P, const float *xn, const float *xsum)
+template <bool G6, bool U6>
+__device__ __forceinline__ void gu_tasks_any(const DecArgs &A, const DecPlan &P, int q0, int q1, const float *xn,
+                                             const float *xsum)
 {
-    const int I = A.I;
-    for (int a0 = 0; a0 < P.nact;) {
-        const int a1 = type_run_end(P, a0, true);
-        const int kind = (P.a[a0].gq6 ? 2 : 0) | (P.a[a0].uq6 ? 1 : 0);
-        if (kind == 0) gu_tasks<false, false>(A, P, a0 * I, a1 * I, xn, xsum);
-        else if (kind == 3) gu_tasks<true, true>(A, P, a0 * I, a1 * I, xn, xsum);
-        else if (kind == 2) gu_tasks<true, false>(A, P, a0 * I, a1 * I, xn, xsum);
-        else gu_tasks<false, true>(A, P, a0 * I, a1 * I, xn, xsum);
-        a0 = a1;
-    }
+    if (A.B == 1) gu_tasks<G6, U6, true>(A, P, q0, q1, xn, xsum);
+    else gu_tasks<G6, U6, false>(A, P, q0, q1, xn, xsum);
 }
 
+extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int l)
+{
+    extern __shared__ __align__(16) float lds[];
+    __shared__ DecPlan P;
+    __shared__ float red[DW][RMAX_B];
+    __shared__ float inv_rms[RMAX_B];
+    __shared__ unsigned long long emask[256];
+    __shared__ unsigned long long sk[DW][16];
+    const int I = A.I, B = A.B, E = A.E;
+    float *xn = lds, *xsum = lds + B * A.H;
+    PHASE_TS(1, 0);
+    if (A.ffn_out) {
+        ffn_plan(A, P);
+        block_norm(A, l, xn, xsum, red, inv_rms);
+    } else {
+        /* logits of this wave's tokens and the shared-gate logits, loaded with h */
+        const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+        const float *lg = A.logits_in ? A.logits_in : A.logits;
+        float lg4[(RMAX_B + DW - 1) / DW][4];
+#pragma unroll
+        for (int r = 0; r < (RMAX_B + DW - 1) / DW; r++) {
+            const int t = wv + r * DW;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                lg4[r][i] = (t < B && lane + 64 * i < E) ? lg[(size_t)t * E + lane + 64 * i] : -INFINITY;
+        }
+        const float sg = threadIdx.x < B ? A.sgate_raw[threadIdx.x] : 0.0f;
+        const DecLayer L = A.layers[l];
+        block_copy16(xn, A.xn_g, B * (A.H + A.H / 16) / 4);
+        __syncthreads();
+        PHASE_TS(1, 1);
+        build_plan(A, L, P, lg4, sg, emask, sk);
+    }
+    PHASE_TS(1, 2);
+    if (blockIdx.x == 0) {
+        const int tid = threadIdx.x;
+        for (int i = tid; i < (int)(sizeof(DecPlan) / 16); i += DT) ((uint4 *)A.plan_g)[i] = ((const uint4 *)&P)[i];
+        if (!A.ffn_out && tid < B * RTOPK) {
+            const size_t o = ((size_t)(l - A.layer0) * B + (tid >> 3)) * RTOPK + (tid & 7);
+            if (A.ids_out) A.ids_out[o] = P.ids[tid >> 3][tid & 7];
+            if (A.w_out) A.w_out[o] = P.w[tid >> 3][tid & 7];
+        }
+        if (tid == 0 && P.err) atomicOr(A.err, 1);
+    }
+    for (int a0 = 0; a0 < P.nroute;) {
+        const int a1 = type_run_end(P, a0, P.nroute, true);
+        const int kind = (P.a[a0].gq6 ? 2 : 0) | (P.a[a0].uq6 ? 1 : 0);
+        if (kind == 0) gu_tasks_any<false, false>(A, P, a0 * I, a1 * I, xn, xsum);
+        else if (kind == 3) gu_tasks_any<true, true>(A, P, a0 * I, a1 * I, xn, xsum);
+        else if (kind == 2) gu_tasks_any<true, false>(A, P, a0 * I, a1 * I, xn, xsum);
+        else gu_tasks_any<false, true>(A, P, a0 * I, a1 * I, xn, xsum);
+        a0 = a1;
+    }
+    PHASE_TS(1, 3);
+}
+
+/* ---- D: down rows + combine ----------------------------------------------- */
+
 /* Down tasks q = a*ngroups + g for q in [q0, q1) (all with type D6): rows
- * r0 + g*rpw + (lane / lpr) of expert a, for each of its (t, slot) pairs, into
- * dbuf[p][row - r0]. */
-template <bool D6>
-__device__ void down_tasks(const DecArgs &A, const DecPlan &P, int q0, int q1, float *dbuf, int R, int ngroups)
+ * r0 + g*rpw + lane/lpr of expert a, for each of its (t, slot) pairs, into
+ * dbuf[p][row - r0].  The SiLU*up inputs come from LDS (ehl, with 16-column
+ * sums ehs) when they fit, else from global memory. */
+template <bool D6, bool EH_LDS>
+__device__ void down_tasks(const DecArgs &A, const DecPlan &P, int q0, int q1, float *dbuf, int ngroups,
+                           const float *ehl, const float *ehs)
 {
     const int H = A.H, I = A.I, nb = I / RQK;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int lpr = nb >= 8 ? 64 : 8 * nb, rpw = 64 / lpr;
     const int rw = lane / lpr, lr = lane % lpr, c = lr & 7, lb = lr >> 3;
     const size_t dbs = D6 ? RQ6K_BYTES : RQ4K_BYTES;
-    const int r0 = blockIdx.x * R;
+    const int r0 = blockIdx.x * D_ROWS;
     const int ca = lb * RQK + q_run_a<D6>(c), cb = ca + q_run_b_off<D6>();
-    for (int q = first_of(q0, wv, DEC_WAVES); q < q1; q += DEC_WAVES) {
-        const int a = q / ngroups, g = q % ngroups;
-        const DecActive &X = P.a[a];
-        const int rl = g * rpw + rw, row = r0 + rl;
-        const bool live = rl < R && row < H;
-        const uint8_t *drow = X.d + (size_t)(live ? row : 0) * nb * dbs;
-        QChunk ch0;
-        if (live && lb < nb) ch0 = q_load<D6>(drow + (size_t)lb * dbs, c);
-        for (int i = 0; i < X.ntok; i++) {
-            const int p = X.tk[i];
-            const float *x = A.eh + (size_t)p * I;
-            float part = 0.0f;
-            if (live && lb < nb) part = q_chunk_dot<D6>(ch0, c, x + ca, x + cb, sum16(x + ca), sum16(x + cb));
-            part = group_sum(part, lpr);
-            if (live && lr == 0) dbuf[p * R + rl] = part;
+    for (int qs = first_of(q0, wv, DW); qs < q1; qs += DW * D_PF) {
+        QChunk ch[D_PF];
+#pragma unroll
+        for (int f = 0; f < D_PF; f++) {
+            const int q = qs + f * DW;
+            if (q < q1) {
+                const int a = q / ngroups, g = q % ngroups;
+                const int rl = g * rpw + rw, row = r0 + rl;
+                if (rl < D_ROWS && row < H && lb < nb)
+                    ch[f] = q_load<D6>(P.a[a].d + ((size_t)row * nb + lb) * dbs, c);
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < D_PF; f++) {
+            const int q = qs + f * DW;
+            if (q >= q1) break;
+            const int a = q / ngroups, g = q % ngroups;
+            const DecActive &X = P.a[a];
+            const int rl = g * rpw + rw, row = r0 + rl;
+            const bool live = rl < D_ROWS && row < H && lb < nb;
+            for (int i = 0; i < X.ntok; i++) {
+                const int p = X.tk[i];
+                float part = 0.0f;
+                if (live) {
+                    if (EH_LDS) {
+                        const float *x = ehl + p * I, *xs = ehs + p * (I / 16);
+                        part = q_chunk_dot<D6>(ch[f], c, x + ca, x + cb, xs[ca >> 4], xs[cb >> 4]);
+                    } else {
+                        const float *x = A.eh + (size_t)p * I;
+                        part = q_chunk_dot<D6>(ch[f], c, x + ca, x + cb, sum16(x + ca), sum16(x + cb));
+                    }
+                }
+                part = group_sum_w(part, lpr);
+                if (live && lr == 0) dbuf[p * D_ROWS + rl] = part;
+            }
         }
     }
 }
 
-/* Down rows [r0, r0 + R) of every active expert, then the combine. */
-__device__ void phase_down(const DecArgs &A, const DecPlan &P, float *dbuf, int R)
+/* SiLU*up inputs of every (t, slot) pair staged in LDS when they fit. */
+#define EH_LDS_FLOATS (18 * 1024)
+
+extern "C" __global__ void __launch_bounds__(DT, 3) dec_down_kernel(DecArgs A, int l)
 {
-    const int H = A.H, I = A.I, B = A.B, nb = I / RQK;
+    extern __shared__ __align__(16) float lds[];
+    __shared__ DecPlan P;
+    __shared__ float dbuf[RMAX_B * 9 * D_ROWS];
+    const int H = A.H, B = A.B, I = A.I, nb = I / RQK;
     const int tid = threadIdx.x;
+    PHASE_TS(2, 0);
+    const int npair = A.ffn_out ? A.ffn_n : B * 9;
+    const bool eh_lds = npair * I <= EH_LDS_FLOATS;
+    float *ehl = lds, *ehs = lds + npair * I;
+    block_copy16(&P, A.plan_g, (int)(sizeof(DecPlan) / 16));
+    if (eh_lds) block_copy16(ehl, A.eh, npair * I / 4);
+    __syncthreads();
+    if (eh_lds) {
+        for (int r = tid; r < npair * (I / 16); r += DT) ehs[r] = sum16(ehl + r * 16);
+        __syncthreads();
+    }
     const int lpr = nb >= 8 ? 64 : 8 * nb, rpw = 64 / lpr;
-    const int ngroups = (R + rpw - 1) / rpw;
-    const int r0 = blockIdx.x * R;
+    const int ngroups = (D_ROWS + rpw - 1) / rpw;
+    const int r0 = blockIdx.x * D_ROWS;
+    PHASE_TS(2, 1);
     for (int a0 = 0; a0 < P.nact;) {
-        const int a1 = type_run_end(P, a0, false);
-        if (P.a[a0].dq6) down_tasks<true>(A, P, a0 * ngroups, a1 * ngroups, dbuf, R, ngroups);
-        else down_tasks<false>(A, P, a0 * ngroups, a1 * ngroups, dbuf, R, ngroups);
+        const int a1 = type_run_end(P, a0, P.nact, false);
+        const int q0 = a0 * ngroups, q1 = a1 * ngroups;
+        if (eh_lds) {
+            if (P.a[a0].dq6) down_tasks<true, true>(A, P, q0, q1, dbuf, ngroups, ehl, ehs);
+            else down_tasks<false, true>(A, P, q0, q1, dbuf, ngroups, ehl, ehs);
+        } else {
+            if (P.a[a0].dq6) down_tasks<true, false>(A, P, q0, q1, dbuf, ngroups, ehl, ehs);
+            else down_tasks<false, false>(A, P, q0, q1, dbuf, ngroups, ehl, ehs);
+        }
         a0 = a1;
     }
     __syncthreads();
+    PHASE_TS(2, 2);
     if (A.ffn_out) {                    /* kernel_ffn_fused: per-expert outputs, token 0 */
-        for (int idx = tid; idx < A.ffn_n * R; idx += DEC_THREADS) {
-            const int k = idx / R, rl = idx % R, row = r0 + rl;
-            if (row < H) A.ffn_out[(size_t)k * H + row] = dbuf[k * R + rl];
+        for (int idx = tid; idx < A.ffn_n * D_ROWS; idx += DT) {
+            const int k = idx / D_ROWS, rl = idx % D_ROWS, row = r0 + rl;
+            if (row < H) A.ffn_out[(size_t)k * H + row] = dbuf[k * D_ROWS + rl];
         }
     } else {
-        for (int idx = tid; idx < B * R; idx += DEC_THREADS) {
-            const int t = idx / R, rl = idx % R, row = r0 + rl;
+        for (int idx = tid; idx < B * D_ROWS; idx += DT) {
+            const int t = idx / D_ROWS, rl = idx % D_ROWS, row = r0 + rl;
             if (row >= H) continue;
             float y = 0.0f;
-            for (int k = 0; k < RTOPK; k++) y = fmaf(P.w[t][k], dbuf[(t * 9 + k) * R + rl], y);
-            y = fmaf(P.w[t][8], dbuf[(t * 9 + 8) * R + rl], y);
+            for (int k = 0; k < RTOPK; k++) y = fmaf(P.w[t][k], dbuf[(t * 9 + k) * D_ROWS + rl], y);
+            y = fmaf(P.w[t][8], dbuf[(t * 9 + 8) * D_ROWS + rl], y);
             if (A.y) A.y[(size_t)t * H + row] = y;
             else A.h[(size_t)t * H + row] = A.h[(size_t)t * H + row] + y;
         }
     }
-}
-
-__device__ void load_ffn_plan(const DecArgs &A, DecShared &S)
-{
-    if (threadIdx.x == 0) {
-        S.plan.nact = A.ffn_n;
-        S.plan.err = 0;
-        for (int k = 0; k < A.ffn_n; k++) {
-            S.plan.a[k] = A.ffn_ex[k];
-            S.plan.a[k].ntok = 1;
-            S.plan.a[k].tk[0] = k;
-        }
-    }
-    __syncthreads();
-}
-
-__device__ __forceinline__ int rows_per_wg(int H)
-{
-    int R = (H + (int)gridDim.x - 1) / (int)gridDim.x;
-    return (R + 3) & ~3;
-}
-
-/* phase_mask bit 0: R, 1: GU (with plan), 2: D (with plan).  fused != 0 runs
- * all phases of all layers with grid barriers. */
-extern "C" __global__ void __launch_bounds__(DEC_THREADS)
-moe_decode_kernel(DecArgs A, int phase_mask, int fused)
-{
-    extern __shared__ __align__(16) float lds[];
-    __shared__ DecShared S;
-    const int H = A.H, B = A.B;
-    float *xn = lds;                           /* [B x H] */
-    float *xsum = xn + B * H;                  /* [B x H/16] */
-    float *dbuf = xsum + B * (H / 16);         /* [B*9 x R] */
-    const int R = rows_per_wg(H);
-    unsigned epoch = 0;
-    if (A.ffn_out) {
-        phase_norm(A, 0, S, xn, xsum);
-        load_ffn_plan(A, S);
-        phase_gu(A, S.plan, xn, xsum);
-        grid_sync(A.bar, epoch, A.err);
-        phase_down(A, S.plan, dbuf, R);
-        return;
-    }
-    for (int l = A.layer0; l < A.layer0 + A.nlayers; l++) {
-        const DecLayer L = A.layers[l];
-        if (fused || (phase_mask & 1)) {
-            phase_norm(A, l, S, xn, xsum);
-            phase_router(A, L, xn);
-        }
-        if (fused) grid_sync(A.bar, epoch, A.err);
-        if (fused || (phase_mask & 2)) {
-            if (!fused) phase_norm(A, l, S, xn, xsum);
-            phase_plan(A, L, l, S);
-            phase_gu(A, S.plan, xn, xsum);
-        }
-        if (fused) grid_sync(A.bar, epoch, A.err);
-        if (fused || (phase_mask & 4)) {
-            if (!fused) phase_plan(A, L, l, S);
-            phase_down(A, S.plan, dbuf, R);
-        }
-        if (fused && l + 1 < A.layer0 + A.nlayers) grid_sync(A.bar, epoch, A.err);
-    }
+    PHASE_TS(2, 3);
+    (void)l;
 }
 
 /* ---- host side ------------------------------------------------------------ */
-size_t dec_lds_bytes(int B, int H)
-{
-    /* xn + xsum + dbuf (R <= H rows of 9*B pairs; R is small, size for 64 rows) */
-    return (size_t)B * H * 4 + (size_t)B * (H / 16) * 4 + (size_t)B * 9 * 64 * 4;
-}
+static size_t norm_lds(int B, int H) { return (size_t)B * H * 4 + (size_t)B * (H / 16) * 4; }
 
-int dec_launch(DecArgs &A, int fused)
+static int launch_layer(const DecArgs &A, int l, bool with_router)
 {
     RtState &R = rt();
-    const size_t lds = dec_lds_bytes(A.B, A.H);
+    const size_t lds = norm_lds(A.B, A.H);
+    if (with_router) {
+        const int ntask = (A.logits_in ? 0 : A.E) + 1 + A.I;
+        hipLaunchKernelGGL(dec_router_kernel, dim3((ntask + DW - 1) / DW), dim3(DT), lds, R.stream, A, l);
+        if (rt_check(hipGetLastError(), "router launch")) return ROASTER_EDEVICE;
+    }
+    hipLaunchKernelGGL(dec_gu_kernel, dim3(2 * R.n_cu), dim3(DT), lds, R.stream, A, l);
+    if (rt_check(hipGetLastError(), "gate/up launch")) return ROASTER_EDEVICE;
+    const int npair = A.ffn_out ? A.ffn_n : A.B * 9;
+    const size_t dlds = npair * A.I <= EH_LDS_FLOATS ? (size_t)npair * A.I * 4 + (size_t)npair * (A.I / 16) * 4 : 0;
+    hipLaunchKernelGGL(dec_down_kernel, dim3((A.H + D_ROWS - 1) / D_ROWS), dim3(DT), dlds, R.stream, A, l);
+    return rt_check(hipGetLastError(), "down launch") ? ROASTER_EDEVICE : 0;
+}
+
+int dec_launch(DecArgs &A)
+{
+    if (A.E > 256) return rt_fail(ROASTER_EINVAL, "decode supports at most 256 routed experts");
     unsigned *ctrl = rt_ctrl();
-    if (!ctrl) return ROASTER_ENOMEM;
-    A.bar = ctrl;
+    A.plan_g = (DecPlan *)rt_scratch(SCR_C, sizeof(DecPlan));
+    if (!ctrl || !A.plan_g) return ROASTER_ENOMEM;
     A.err = (int *)(ctrl + 16);
-    if (fused) {
-        if (rt_check(hipMemsetAsync(ctrl, 0, 4, R.stream), "barrier reset")) return ROASTER_EDEVICE;
-        int blocks = 0;
-        if (rt_coop_grid((const void *)moe_decode_kernel, DEC_THREADS, lds, &blocks)) return ROASTER_EDEVICE;
-        blocks = R.n_cu < blocks ? R.n_cu : blocks;     /* one workgroup per CU */
-        if (((A.H + blocks - 1) / blocks + 3) / 4 * 4 > 64) return rt_fail(ROASTER_EINVAL, "hidden too large");
-        int mask = 7, fz = 1;
-        void *args[] = { &A, &mask, &fz };
-        return rt_check(hipLaunchCooperativeKernel((const void *)moe_decode_kernel, dim3(blocks), dim3(DEC_THREADS),
-                                                   args, lds, R.stream), "cooperative decode launch");
-    }
-    const int blocks = R.n_cu;
-    for (int l = A.layer0; l < A.layer0 + A.nlayers; l++) {
-        DecArgs a1 = A;
-        a1.layer0 = l;
-        a1.nlayers = 1;
-        for (int ph = 0; ph < 3; ph++) {
-            hipLaunchKernelGGL(moe_decode_kernel, dim3(blocks), dim3(DEC_THREADS), lds, R.stream, a1, 1 << ph, 0);
-            if (rt_check(hipGetLastError(), "decode launch")) return ROASTER_EDEVICE;
-        }
-    }
+    for (int l = A.layer0; l < A.layer0 + A.nlayers; l++)
+        if (int rc = launch_layer(A, l, true)) return rc;
     return 0;
 }
 
 int dec_ffn_launch(DecArgs &A)
 {
-    RtState &R = rt();
-    const size_t lds = dec_lds_bytes(1, A.H);
     unsigned *ctrl = rt_ctrl();
-    if (!ctrl) return ROASTER_ENOMEM;
-    A.bar = ctrl;
+    A.plan_g = (DecPlan *)rt_scratch(SCR_C, sizeof(DecPlan));
+    if (!ctrl || !A.plan_g) return ROASTER_ENOMEM;
     A.err = (int *)(ctrl + 16);
-    if (rt_check(hipMemsetAsync(ctrl, 0, 4, R.stream), "barrier reset")) return ROASTER_EDEVICE;
-    int blocks = 0;
-    if (rt_coop_grid((const void *)moe_decode_kernel, DEC_THREADS, lds, &blocks)) return ROASTER_EDEVICE;
-    blocks = R.n_cu < blocks ? R.n_cu : blocks;
-    int mask = 7, fz = 1;
-    void *args[] = { &A, &mask, &fz };
-    return rt_check(hipLaunchCooperativeKernel((const void *)moe_decode_kernel, dim3(blocks), dim3(DEC_THREADS),
-                                               args, lds, R.stream), "cooperative ffn launch");
+    return launch_layer(A, 0, false);
 }

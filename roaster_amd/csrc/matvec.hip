@@ -35,7 +35,7 @@ __device__ __forceinline__ void matvec_task(const MvJob &J, int task, int lane)
             const int ca = b * RQK + q_run_a<Q6>(c), cb = ca + q_run_b_off<Q6>();
             part += q_chunk_dot<Q6>(ch, c, x + ca, x + cb, sum16(x + ca), sum16(x + cb));
         }
-        part = group_sum(part, lpr);
+        part = group_sum_w(part, lpr);
         if (live && lr == 0) J.Y[(size_t)t * J.rows + row] = part;
     }
 }
@@ -73,7 +73,7 @@ __global__ void __launch_bounds__(MV_THREADS) matvec_f32_kernel(const float *W, 
         const float *row = W + r * cols;
         float acc = 0.0f;
         for (size_t i = lane; i < cols; i += 64) acc = fmaf(row[i], x[i], acc);
-        acc = group_sum(acc, 64);
+        acc = group_sum<64>(acc);
         if (lane == 0) y[r] = acc;
     }
 }
@@ -87,7 +87,7 @@ __global__ void __launch_bounds__(1024) norm_kernel(float *y, const float *x, co
     __shared__ float red[16];
     float ss = 0.0f;
     for (size_t i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
-    ss = group_sum(ss, 64);
+    ss = group_sum<64>(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     float tot = 0.0f;

@@ -37,6 +37,9 @@ struct QChunk {
     uint32_t dd;   /* Q6_K: d (low 16 bits) */
 };
 
+/* Chunks of one gate row and one up row. */
+struct QChunk2 { QChunk g, u; };
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h)
 {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
@@ -134,12 +137,11 @@ __device__ __forceinline__ float dot4u8(uint32_t q, const float4 x, float acc)
     return acc;
 }
 
-/* Lane partial of sum_i w_i x_i over its 32 weights.  xa / xb point at the
- * 16 floats of runs A / B (16-byte aligned, global or LDS); sxa / sxb are
- * their sums. */
+/* Lane partial of sum_i w_i x_i over its 32 weights, x already in registers:
+ * xa / xb are the 16 floats of runs A / B, sxa / sxb their sums. */
 template <bool q6>
-__device__ __forceinline__ float q_chunk_dot(const QChunk &ch, int c, const float *xa, const float *xb,
-                                             float sxa, float sxb)
+__device__ __forceinline__ float q_chunk_dot_r(const QChunk &ch, int c, const float4 (&xa)[4], const float4 (&xb)[4],
+                                               float sxa, float sxb)
 {
     float sA, mA, sB, mB;
     q_scales<q6>(ch, c, sA, mA, sB, mB);
@@ -148,8 +150,8 @@ __device__ __forceinline__ float q_chunk_dot(const QChunk &ch, int c, const floa
     for (int i = 0; i < 4; i++) {
         uint32_t qa, qb;
         q_word<q6>(ch, i, c, qa, qb);
-        accA = dot4u8(qa, *(const float4 *)(xa + 4 * i), accA);
-        accB = dot4u8(qb, *(const float4 *)(xb + 4 * i), accB);
+        accA = dot4u8(qa, xa[i], accA);
+        accB = dot4u8(qb, xb[i], accB);
     }
     float r = sA * accA;
     r = fmaf(-mA, sxa, r);
@@ -158,17 +160,71 @@ __device__ __forceinline__ float q_chunk_dot(const QChunk &ch, int c, const floa
     return r;
 }
 
+/* The same with x read from memory (16-byte aligned, global or LDS). */
+template <bool q6>
+__device__ __forceinline__ float q_chunk_dot(const QChunk &ch, int c, const float *xa, const float *xb,
+                                             float sxa, float sxb)
+{
+    float4 a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        a[i] = *(const float4 *)(xa + 4 * i);
+        b[i] = *(const float4 *)(xb + 4 * i);
+    }
+    return q_chunk_dot_r<q6>(ch, c, a, b, sxa, sxb);
+}
+
 __device__ __forceinline__ float sum16(const float *x)
 {
     float4 a = *(const float4 *)x, b = *(const float4 *)(x + 4), c = *(const float4 *)(x + 8), d = *(const float4 *)(x + 12);
     return ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)) + (((c.x + c.y) + (c.z + c.w)) + ((d.x + d.y) + (d.z + d.w)));
 }
 
-/* Sum over aligned lane groups of `width` lanes (power of two <= 64). */
-__device__ __forceinline__ float group_sum(float v, int width)
+/* ---- cross-lane reductions with DPP (no LDS crossbar round trips) ---------- */
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v)
 {
-    for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ float lane_f(float v, int l)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+#define DPP_XOR1 0xB1          /* quad_perm [1,0,3,2] */
+#define DPP_XOR2 0x4E          /* quad_perm [2,3,0,1] */
+#define DPP_HALF_MIRROR 0x141  /* lane i <-> 7-i within 8 */
+#define DPP_MIRROR 0x140       /* lane i <-> 15-i within 16 */
+
+/* Sum over aligned groups of W lanes (W a power of two <= 64); every lane of a
+ * group receives the group's sum (fixed order, so results are deterministic). */
+template <int W>
+__device__ __forceinline__ float group_sum(float v)
+{
+    if (W >= 2) v += dpp_f<DPP_XOR1>(v);
+    if (W >= 4) v += dpp_f<DPP_XOR2>(v);
+    if (W >= 8) v += dpp_f<DPP_HALF_MIRROR>(v);
+    if (W >= 16) v += dpp_f<DPP_MIRROR>(v);
+    if (W == 32) {
+        const float lo = lane_f(v, 0) + lane_f(v, 16), hi = lane_f(v, 32) + lane_f(v, 48);
+        v = (threadIdx.x & 32) ? hi : lo;
+    }
+    if (W == 64) v = (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
     return v;
+}
+
+/* Runtime group width (8, 16, 32 or 64). */
+__device__ __forceinline__ float group_sum_w(float v, int w)
+{
+    if (w == 16) return group_sum<16>(v);
+    if (w == 64) return group_sum<64>(v);
+    if (w == 8) return group_sum<8>(v);
+    return group_sum<32>(v);
 }
 
 #endif
