@@ -35,8 +35,10 @@ extern "C" {
 #define ROASTER_DOWN 2
 
 /* Prefill arithmetic. */
-#define ROASTER_PREC_BF16  0   /* bf16 MFMA operands, fp32 accumulate (tolerance 2e-3 of |y|inf) */
-#define ROASTER_PREC_SPLIT 1   /* hi+lo bf16 split of both operands, 3 MFMAs (tolerance 2e-4) */
+/* Prefill GEMM operand precision (fp32 accumulation in every mode). */
+#define ROASTER_PREC_F16   0   /* fp16 operands, activations scaled per row by a power of two (default) */
+#define ROASTER_PREC_SPLIT 1   /* bf16 hi+lo split of both operands, 3 MFMAs per product block */
+#define ROASTER_PREC_BF16  2   /* bf16 operands: fastest to convert, about 8 significant bits */
 
 /* ---- runtime ------------------------------------------------------------ */
 const char *roaster_last_error(void);
@@ -117,7 +119,7 @@ int roaster_moe_decode_stack(RoasterTable *t, float *h, int B, int layer0, int n
 
 /* ---- prefill ------------------------------------------------------------ */
 typedef struct {
-    int precision;             /* ROASTER_PREC_BF16 (default) or ROASTER_PREC_SPLIT */
+    int precision;             /* ROASTER_PREC_F16 (default), _SPLIT or _BF16 */
     const float *logits_in;    /* [T x E] replaces the router matmul, or NULL */
     const float *logit_bias;   /* [E] added to every token's logits, or NULL */
     float *logits_out;         /* [T x E] or NULL */

@@ -20,7 +20,7 @@ Q6K_BYTES = 210
 
 OK, EINVAL, EDEVICE, EROUTE, ENOMEM = 0, -1, -2, -3, -4
 GATE, UP, DOWN = 0, 1, 2
-PREC_BF16, PREC_SPLIT = 0, 1
+PREC_F16, PREC_SPLIT, PREC_BF16 = 0, 1, 2
 
 
 class KernelMatvecJob(C.Structure):

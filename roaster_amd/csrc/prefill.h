@@ -1,0 +1,45 @@
+/*
+ * prefill.h -- grouped expert GEMMs (prefill.hip), shared with the kernels.h
+ * implementation of kernel_moe_prefill (api.hip).
+ *
+ * A group is one expert's row list: n rows, row a reads activation row
+ * tok[a] (or tok0 + a) of X and owns slot slot0 + a of the intermediate and
+ * output buffers.  A tile is 64 consecutive rows of one group.
+ */
+#ifndef ROASTER_PREFILL_H
+#define ROASTER_PREFILL_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+struct PfGroup {
+    const uint8_t *g, *u, *d;      /* gate [I x H], up [I x H], down [H x I] */
+    int gq6, uq6, dq6;
+    int n;                          /* rows */
+    int slot0;                      /* first slot */
+    int tok0;                       /* rows read X[tok0 + a] when tok is NULL */
+    const int *tok;                 /* [n] activation rows, or NULL */
+    int pad;
+};
+
+struct PfTile {
+    int grp, m0;
+};
+
+struct PfGemmArgs {
+    const PfGroup *groups;
+    const PfTile *tiles;
+    const int *ntiles;              /* device count of valid tiles */
+    const float *X;                 /* [* x H] activations */
+    const float *xinv, *xfwd;       /* per X row power-of-two scales (fp16 mode), or NULL */
+    float *act;                     /* [slots x I]: silu(gate) * up */
+    unsigned *amax;                 /* [slots] max |act| bits (fp16 mode), or NULL */
+    float *out;                     /* [slots x H]: down products */
+    int H, I;
+};
+
+/* Launch the gate/up and down GEMMs over up to max_tiles tiles.  op: PF_F16,
+ * PF_SPLIT or PF_BF16 (gemm.h).  0 or ROASTER_EDEVICE. */
+int pf_gemm_launch(const PfGemmArgs &A, int max_tiles, int op);
+
+#endif

@@ -1,11 +1,606 @@
 /*
- * prefill.hip -- MoE prefill (placeholder until the MFMA path lands).
+ * prefill.hip -- the MoE block over T tokens (model.c:1671-1791) on the GPU.
+ *
+ *   pf_router_kernel   logits = X . W_r^T in f32, split over K into 4 partial
+ *                      sums added in fixed order (model.c:1679)
+ *   pf_token_kernel    one wave per token: logits (+ bias), top-8 and
+ *                      renormalised weights (model.c:1681-1692), the shared
+ *                      expert's sigmoid gate (model.c:1707-1708), the row
+ *                      scale of X for the fp16 GEMM operands
+ *   pf_bucket_kernel   one workgroup per expert: that expert's token list in
+ *                      token order, i.e. the stable counting sort over (t, k)
+ *                      of model.c:1713-1731
+ *   pf_plan_kernel     offsets (prefix sums of the counts), groups and the
+ *                      64-row tile list; the shared expert is one more group
+ *                      over all T tokens (model.c:1694-1711)
+ *   pf_gu_kernel       grouped GEMM gate/up, SiLU(gate) * up epilogue
+ *   pf_down_kernel     grouped GEMM down
+ *   pf_combine_kernel  Y[t] = sigmoid(s_t) * shared(t), then += w * expert
+ *                      output in ascending expert id (model.c:1709-1711,
+ *                      1776-1788), one fused multiply-add per term
+ *
+ * Slots: routed pair (t, k) with expert e owns slot off[e] + rank, where rank
+ * is t's position in e's list; token t's shared-expert row owns slot 8T + t.
  */
 #include "internal.h"
+#include "gemm.h"
+#include "prefill.h"
+#include "table.h"
+#include "topk.h"
+
+#include <string.h>
+
+#define PF_MAX_T (1 << 16)
+#define RT_KSPLIT 4               /* router K split */
+
+__device__ __forceinline__ float pf_silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
+/* Exclusive prefix sum over a 256-thread workgroup; *total gets the sum. */
+__device__ int block_scan_256(int v, int *lds, int *total)
+{
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int inc = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(inc, d);
+        if (lane >= d) inc += o;
+    }
+    if (lane == 63) lds[w] = inc;
+    __syncthreads();
+    int before = 0, all = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = lds[i];
+        before += i < w ? c : 0;
+        all += c;
+    }
+    __syncthreads();
+    *total = all;
+    return before + inc - v;
+}
+
+/* ---- router: part[s][t][e] = sum over k in split s of X[t][k] * W[e][k] ---- */
+#define RT_TM 32
+#define RT_TN 64
+#define RT_KC 32
+
+extern "C" __global__ void __launch_bounds__(256) pf_router_kernel(const float *X, const float *W, float *part, int T,
+                                                                   int E, int H)
+{
+    __shared__ float Xs[RT_KC][RT_TM + 4];
+    __shared__ float Ws[RT_KC][RT_TN + 4];
+    const int t = threadIdx.x;
+    const int n0 = blockIdx.x * RT_TN, m0 = blockIdx.y * RT_TM, s = blockIdx.z;
+    const int klen = H / RT_KSPLIT, kbeg = s * klen;
+    const int ty = t >> 4, tx = t & 15;
+    float acc[2][4] = {};
+    /* loaders: X row t/8 (32 rows), k 4*(t%8); W rows t/8 and 32 + t/8 */
+    const int xr = t >> 3, xk = 4 * (t & 7);
+    const float *xp = (m0 + xr < T) ? X + (size_t)(m0 + xr) * H + kbeg + xk : nullptr;
+    const float *wp0 = (n0 + xr < E) ? W + (size_t)(n0 + xr) * H + kbeg + xk : nullptr;
+    const float *wp1 = (n0 + 32 + xr < E) ? W + (size_t)(n0 + 32 + xr) * H + kbeg + xk : nullptr;
+    for (int k0 = 0; k0 < klen; k0 += RT_KC) {
+        const float4 a = xp ? *(const float4 *)(xp + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 b0 = wp0 ? *(const float4 *)(wp0 + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 b1 = wp1 ? *(const float4 *)(wp1 + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        __syncthreads();
+        Xs[xk + 0][xr] = a.x; Xs[xk + 1][xr] = a.y; Xs[xk + 2][xr] = a.z; Xs[xk + 3][xr] = a.w;
+        Ws[xk + 0][xr] = b0.x; Ws[xk + 1][xr] = b0.y; Ws[xk + 2][xr] = b0.z; Ws[xk + 3][xr] = b0.w;
+        Ws[xk + 0][32 + xr] = b1.x; Ws[xk + 1][32 + xr] = b1.y; Ws[xk + 2][32 + xr] = b1.z; Ws[xk + 3][32 + xr] = b1.w;
+        __syncthreads();
+#pragma unroll 8
+        for (int k = 0; k < RT_KC; k++) {
+            const float2 av = *(const float2 *)&Xs[k][2 * ty];
+            const float4 bv = *(const float4 *)&Ws[k][4 * tx];
+            acc[0][0] = fmaf(av.x, bv.x, acc[0][0]); acc[0][1] = fmaf(av.x, bv.y, acc[0][1]);
+            acc[0][2] = fmaf(av.x, bv.z, acc[0][2]); acc[0][3] = fmaf(av.x, bv.w, acc[0][3]);
+            acc[1][0] = fmaf(av.y, bv.x, acc[1][0]); acc[1][1] = fmaf(av.y, bv.y, acc[1][1]);
+            acc[1][2] = fmaf(av.y, bv.z, acc[1][2]); acc[1][3] = fmaf(av.y, bv.w, acc[1][3]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int m = m0 + 2 * ty + i;
+        if (m >= T) continue;
+        float *dst = part + ((size_t)s * T + m) * E;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int n = n0 + 4 * tx + j;
+            if (n < E) dst[n] = acc[i][j];
+        }
+    }
+}
+
+/* ---- per token: logits, top-8, shared gate, X row scale ------------------ */
+struct PfTokArgs {
+    const float *X;
+    const float *gate_inp;
+    const float *part;          /* router partial sums [KSPLIT][T][E], or NULL */
+    const float *logits_in;     /* [T x E] or NULL */
+    const float *bias;          /* [E] or NULL */
+    float *logits_out;          /* [T x E] or NULL */
+    int *ids;                   /* [T x 8] */
+    float *w;                   /* [T x 8] */
+    int *ids_out;
+    float *w_out;
+    float *sg;                  /* [T] */
+    float *xinv, *xfwd;         /* [T] (fp16 mode) or NULL */
+    unsigned *amax;             /* [9T] zeroed here, or NULL */
+    int *err;
+    int T, E, H;
+};
+
+extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
+{
+    __shared__ unsigned long long sk[4][16];
+    __shared__ int bad[4];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + wv;
+    if (t >= A.T) return;
+    /* X row: max |x| and the shared-expert gate dot */
+    const float *x = A.X + (size_t)t * A.H;
+    float mx = 0.0f, dot = 0.0f;
+    for (int k = 4 * lane; k < A.H; k += 256) {
+        const float4 v = *(const float4 *)(x + k);
+        const float4 g = *(const float4 *)(A.gate_inp + k);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        dot = fmaf(v.x, g.x, dot); dot = fmaf(v.y, g.y, dot);
+        dot = fmaf(v.z, g.z, dot); dot = fmaf(v.w, g.w, dot);
+    }
+    dot = group_sum<64>(dot);
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+    if (lane == 0) {
+        A.sg[t] = 1.0f / (1.0f + expf(-dot));
+        if (A.xinv) {
+            float inv, fwd;
+            row_scale(mx, inv, fwd);
+            A.xinv[t] = inv;
+            A.xfwd[t] = fwd;
+        }
+    }
+    if (A.amax && lane < 9) A.amax[(size_t)t * 9 + lane] = 0u;
+    /* logits */
+    float v4[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int e = lane + 64 * i;
+        float l = -INFINITY;
+        if (e < A.E) {
+            const size_t o = (size_t)t * A.E + e;
+            if (A.logits_in) {
+                l = A.logits_in[o];
+            } else {
+                const size_t TE = (size_t)A.T * A.E;
+                l = ((A.part[o] + A.part[TE + o]) + A.part[2 * TE + o]) + A.part[3 * TE + o];
+            }
+            if (A.bias) l = l + A.bias[e];
+            if (A.logits_out) A.logits_out[o] = l;
+        }
+        v4[i] = l;
+    }
+    if (lane == 0) bad[wv] = 0;
+    __builtin_amdgcn_wave_barrier();
+    topk8_wave(v4, A.E, A.ids + (size_t)t * 8, A.w + (size_t)t * 8, &bad[wv], sk[wv]);
+    if (lane < 8) {
+        if (A.ids_out) A.ids_out[(size_t)t * 8 + lane] = A.ids[(size_t)t * 8 + lane];
+        if (A.w_out) A.w_out[(size_t)t * 8 + lane] = A.w[(size_t)t * 8 + lane];
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0 && bad[wv]) atomicOr(A.err, 1);
+}
+
+/* ---- bucketing: list[e][r] = r-th token (ascending) that selected e ------- */
+extern "C" __global__ void __launch_bounds__(256) pf_bucket_kernel(const int *ids, int T, int *list, int *rank,
+                                                                   int *cnt)
+{
+    __shared__ int wsum[4];
+    const int e = blockIdx.x;
+    int base = 0;
+    for (int c = 0; c < T; c += 256) {
+        const int t = c + threadIdx.x;
+        int k = -1;
+        if (t < T) {
+            const int4 a = *(const int4 *)(ids + (size_t)t * 8);
+            const int4 b = *(const int4 *)(ids + (size_t)t * 8 + 4);
+            k = a.x == e ? 0 : a.y == e ? 1 : a.z == e ? 2 : a.w == e ? 3
+              : b.x == e ? 4 : b.y == e ? 5 : b.z == e ? 6 : b.w == e ? 7 : -1;
+        }
+        int total;
+        const int r = base + block_scan_256(k >= 0 ? 1 : 0, wsum, &total);
+        if (k >= 0) {
+            list[(size_t)e * T + r] = t;
+            rank[(size_t)t * 8 + k] = r;
+        }
+        base += total;
+    }
+    if (threadIdx.x == 0) cnt[e] = base;
+}
+
+/* ---- plan: offsets, groups, tiles ----------------------------------------- */
+struct PfPlanArgs {
+    DecLayer L;
+    size_t eb_g, eb_u, eb_d;    /* per-expert matrix bytes */
+    int q6g, q6u, q6d, sq6g, sq6u, sq6d;
+    const int *cnt;
+    const int *list;
+    int *off;                   /* [E] */
+    int *counts_out;            /* [E] or NULL */
+    PfGroup *groups;            /* [E + 1] */
+    PfTile *tiles;
+    int *ntiles;
+    int T, E;
+};
+
+extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
+{
+    __shared__ int wsum[4];
+    const int e = threadIdx.x;
+    const int c = e < A.E ? A.cnt[e] : 0;
+    const int nt = (c + GM - 1) / GM;
+    int tot_rows, tot_tiles;
+    const int off = block_scan_256(c, wsum, &tot_rows);
+    const int toff = block_scan_256(nt, wsum, &tot_tiles);
+    if (e < A.E) {
+        A.off[e] = off;
+        if (A.counts_out) A.counts_out[e] = c;
+        PfGroup G;
+        G.g = A.L.gate + (size_t)e * A.eb_g;
+        G.u = A.L.up + (size_t)e * A.eb_u;
+        G.d = A.L.down + (size_t)e * A.eb_d;
+        G.gq6 = A.q6g; G.uq6 = A.q6u; G.dq6 = A.q6d;
+        G.n = c;
+        G.slot0 = off;
+        G.tok0 = 0;
+        G.tok = A.list + (size_t)e * A.T;
+        G.pad = 0;
+        A.groups[e] = G;
+        for (int i = 0; i < nt; i++) A.tiles[toff + i] = PfTile{ e, i * GM };
+    }
+    const int nsh = (A.T + GM - 1) / GM;
+    if (e == 0) {
+        PfGroup G;
+        G.g = A.L.sgate; G.u = A.L.sup; G.d = A.L.sdown;
+        G.gq6 = A.sq6g; G.uq6 = A.sq6u; G.dq6 = A.sq6d;
+        G.n = A.T;
+        G.slot0 = 8 * A.T;
+        G.tok0 = 0;
+        G.tok = nullptr;
+        G.pad = 0;
+        A.groups[A.E] = G;
+        *A.ntiles = tot_tiles + nsh;
+    }
+    for (int i = e; i < nsh; i += 256) A.tiles[tot_tiles + i] = PfTile{ A.E, i * GM };
+}
+
+/* ---- grouped GEMMs -------------------------------------------------------- */
+/* Virtual block id: blocks b < R = ntiles * nblk run; on a grid dispatched
+ * round-robin over the 8 XCDs, XCD b % 8 takes the contiguous range of
+ * virtual ids [(b % 8) * R / 8, ...), so the n-blocks of one tile and the
+ * consecutive tiles of one expert share an L2. */
+__device__ __forceinline__ int pf_virtual_block(int b, int R)
+{
+    return (R & 7) ? b : (b & 7) * (R >> 3) + (b >> 3);
+}
+
+struct PfRowMeta {
+    const float *src[GM];
+    int slot[GM];
+    float inv[GM], fwd[GM];
+};
+
+template <int OP>
+__global__ void __launch_bounds__(GT) pf_gu_kernel(PfGemmArgs A)
+{
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    __shared__ PfRowMeta meta;
+    const int nblk = A.I / 32;
+    const int R = *A.ntiles * nblk;
+    const int b = blockIdx.x;
+    if (b >= R) return;
+    const int v = pf_virtual_block(b, R);
+    const PfTile tile = A.tiles[v / nblk];
+    const int j0 = (v % nblk) * 32;
+    const PfGroup &G = A.groups[tile.grp];
+    const int t = threadIdx.x;
+    if (t < GM) {
+        const int a = tile.m0 + t;
+        if (a < G.n) {
+            const int tok = G.tok ? G.tok[a] : G.tok0 + a;
+            meta.src[t] = A.X + (size_t)tok * A.H;
+            meta.slot[t] = G.slot0 + a;
+            meta.inv[t] = A.xinv ? A.xinv[tok] : 1.0f;
+            meta.fwd[t] = A.xfwd ? A.xfwd[tok] : 1.0f;
+        } else {
+            meta.src[t] = nullptr;
+            meta.slot[t] = -1;
+            meta.inv[t] = 1.0f;
+            meta.fwd[t] = 1.0f;
+        }
+    }
+    uint16_t *Xh = smem, *Wh = smem + G_TILE_ELEMS;
+    uint16_t *Xl = smem + 2 * G_TILE_ELEMS, *Wl = smem + 3 * G_TILE_ELEMS;
+    /* weight row of this thread: tile rows 0..31 gate rows j0.., 32..63 up rows j0.. */
+    const int wr = t >> 2;
+    const bool is_up = wr >= 32;
+    const bool q6 = is_up ? G.uq6 : G.gq6;
+    const size_t bb = q6 ? RQ6K_BYTES : RQ4K_BYTES;
+    const int nkb = A.H / GK;
+    const uint8_t *wrow = (is_up ? G.u : G.g) + (size_t)(j0 + (wr & 31)) * nkb * bb;
+    __syncthreads();
+    const float *xsrc = meta.src[wr];
+    const float xinv = meta.inv[wr];
+    const int w = t >> 6, wm = w & 1, wn = w >> 1;
+    f32x16 acc = {};
+    for (int kb = 0; kb < nkb; kb++) {
+        if (kb) __syncthreads();
+        load_w_tile<OP>(wrow + kb * bb, q6, Wh, Wl);
+        load_x_tile<OP>(xsrc ? xsrc + kb * GK : nullptr, xinv, Xh, Xl);
+        __syncthreads();
+        mfma_tile<OP>(acc, Xh, Xl, Wh, Wl, wm, wn);
+    }
+    /* epilogue: gate / up blocks meet in LDS */
+    __syncthreads();
+    float *Cs = (float *)smem;                 /* [64][65] */
+    const int l = t & 63;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int m = 32 * wm + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
+        Cs[m * 65 + 32 * wn + (l & 31)] = acc[i];
+    }
+    __syncthreads();
+    const int m = t >> 2, q = t & 3;
+    const int slot = meta.slot[m];
+    const float fwd = meta.fwd[m];
+    float e8[8];
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float g = Cs[m * 65 + 8 * q + i] * fwd, u = Cs[m * 65 + 32 + 8 * q + i] * fwd;
+        e8[i] = pf_silu_mul(g, u);
+        mx = fmaxf(mx, fabsf(e8[i]));
+    }
+    if (slot >= 0) {
+        float4 *dst = (float4 *)(A.act + (size_t)slot * A.I + j0 + 8 * q);
+        dst[0] = make_float4(e8[0], e8[1], e8[2], e8[3]);
+        dst[1] = make_float4(e8[4], e8[5], e8[6], e8[7]);
+    }
+    if (A.amax) {
+        mx = fmaxf(mx, __shfl_xor(mx, 1));
+        mx = fmaxf(mx, __shfl_xor(mx, 2));
+        if (q == 0 && slot >= 0) atomicMax(A.amax + slot, __builtin_bit_cast(unsigned, mx));
+    }
+}
+
+template <int OP>
+__global__ void __launch_bounds__(GT) pf_down_kernel(PfGemmArgs A)
+{
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    __shared__ PfRowMeta meta;
+    const int nblk = A.H / GN;
+    const int R = *A.ntiles * nblk;
+    const int b = blockIdx.x;
+    if (b >= R) return;
+    const int v = pf_virtual_block(b, R);
+    const PfTile tile = A.tiles[v / nblk];
+    const int n0 = (v % nblk) * GN;
+    const PfGroup &G = A.groups[tile.grp];
+    const int t = threadIdx.x;
+    if (t < GM) {
+        const int a = tile.m0 + t;
+        if (a < G.n) {
+            const int slot = G.slot0 + a;
+            meta.src[t] = A.act + (size_t)slot * A.I;
+            meta.slot[t] = slot;
+            float inv = 1.0f, fwd = 1.0f;
+            if (A.amax) row_scale(__builtin_bit_cast(float, A.amax[slot]), inv, fwd);
+            meta.inv[t] = inv;
+            meta.fwd[t] = fwd;
+        } else {
+            meta.src[t] = nullptr;
+            meta.slot[t] = -1;
+            meta.inv[t] = 1.0f;
+            meta.fwd[t] = 1.0f;
+        }
+    }
+    uint16_t *Xh = smem, *Wh = smem + G_TILE_ELEMS;
+    uint16_t *Xl = smem + 2 * G_TILE_ELEMS, *Wl = smem + 3 * G_TILE_ELEMS;
+    const int wr = t >> 2;
+    const bool q6 = G.dq6;
+    const size_t bb = q6 ? RQ6K_BYTES : RQ4K_BYTES;
+    const int nkb = A.I / GK;
+    const uint8_t *wrow = G.d + (size_t)(n0 + wr) * nkb * bb;
+    __syncthreads();
+    const float *xsrc = meta.src[wr];
+    const float xinv = meta.inv[wr];
+    const int w = t >> 6, wm = w & 1, wn = w >> 1;
+    f32x16 acc = {};
+    for (int kb = 0; kb < nkb; kb++) {
+        if (kb) __syncthreads();
+        load_w_tile<OP>(wrow + kb * bb, q6, Wh, Wl);
+        load_x_tile<OP>(xsrc ? xsrc + kb * GK : nullptr, xinv, Xh, Xl);
+        __syncthreads();
+        mfma_tile<OP>(acc, Xh, Xl, Wh, Wl, wm, wn);
+    }
+    const int l = t & 63;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int m = 32 * wm + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
+        const int slot = meta.slot[m];
+        if (slot >= 0) A.out[(size_t)slot * A.H + n0 + 32 * wn + (l & 31)] = acc[i] * meta.fwd[m];
+    }
+}
+
+/* ---- combine -------------------------------------------------------------- */
+extern "C" __global__ void __launch_bounds__(256) pf_combine_kernel(const float *ed, const int *ids, const float *w,
+                                                                    const int *rank, const int *off, const float *sg,
+                                                                    float *Y, int T, int H)
+{
+    const int t = blockIdx.x;
+    int id[8], sl[8];
+    float wt[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        id[k] = ids[(size_t)t * 8 + k];
+        wt[k] = w[(size_t)t * 8 + k];
+    }
+    /* ascending expert id (ids of one token are distinct; -1 = unrouted) */
+#pragma unroll
+    for (int i = 1; i < 8; i++)
+#pragma unroll
+        for (int j = i; j > 0; j--)
+            if (id[j] < id[j - 1]) {
+                const int ti = id[j]; id[j] = id[j - 1]; id[j - 1] = ti;
+                const float tw = wt[j]; wt[j] = wt[j - 1]; wt[j - 1] = tw;
+            }
+    /* slots need the original k of each id: rank is indexed by (t, k) */
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        sl[k] = -1;
+        if (id[k] >= 0) {
+            int kk = 0;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (ids[(size_t)t * 8 + j] == id[k]) kk = j;
+            sl[k] = off[id[k]] + rank[(size_t)t * 8 + kk];
+        }
+    }
+    const float g = sg[t];
+    const float *sh = ed + ((size_t)8 * T + t) * H;
+    for (int i = threadIdx.x * 4; i < H; i += 1024) {
+        const float4 s = *(const float4 *)(sh + i);
+        float4 y = make_float4(g * s.x, g * s.y, g * s.z, g * s.w);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            if (sl[k] < 0) continue;
+            const float4 d = *(const float4 *)(ed + (size_t)sl[k] * H + i);
+            y.x = fmaf(wt[k], d.x, y.x);
+            y.y = fmaf(wt[k], d.y, y.y);
+            y.z = fmaf(wt[k], d.z, y.z);
+            y.w = fmaf(wt[k], d.w, y.w);
+        }
+        *(float4 *)(Y + (size_t)t * H + i) = y;
+    }
+}
+
+/* ---- host ----------------------------------------------------------------- */
+template <int OP>
+static int launch_gemms(const PfGemmArgs &A, int max_tiles)
+{
+    RtState &R = rt();
+    const size_t lds = gemm_lds_bytes(OP);
+    const int gu_blocks = max_tiles * (A.I / 32), d_blocks = max_tiles * (A.H / GN);
+    hipLaunchKernelGGL(pf_gu_kernel<OP>, dim3(gu_blocks), dim3(GT), lds, R.stream, A);
+    if (rt_check(hipGetLastError(), "prefill gate/up launch")) return ROASTER_EDEVICE;
+    hipLaunchKernelGGL(pf_down_kernel<OP>, dim3(d_blocks), dim3(GT), lds, R.stream, A);
+    return rt_check(hipGetLastError(), "prefill down launch") ? ROASTER_EDEVICE : 0;
+}
+
+int pf_gemm_launch(const PfGemmArgs &A, int max_tiles, int op)
+{
+    if (max_tiles <= 0) return 0;
+    if (op == PF_F16) return launch_gemms<PF_F16>(A, max_tiles);
+    if (op == PF_SPLIT) return launch_gemms<PF_SPLIT>(A, max_tiles);
+    return launch_gemms<PF_BF16>(A, max_tiles);
+}
+
+static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, int T, float *Y,
                                    const RoasterPrefillOpts *o)
 {
-    (void)t; (void)layer; (void)X; (void)T; (void)Y; (void)o;
-    return rt_fail(ROASTER_EINVAL, "roaster_moe_prefill: not built yet");
+    std::lock_guard<std::recursive_mutex> lk(rt_lock());
+    if (rt_init_locked()) return ROASTER_EDEVICE;
+    RoasterPrefillOpts opt;
+    memset(&opt, 0, sizeof(opt));
+    if (o) opt = *o;
+    if (!t || layer < 0 || layer >= t->d.n_layers || !X || !Y || T < 1 || T > PF_MAX_T)
+        return rt_fail(ROASTER_EINVAL, "roaster_moe_prefill: bad arguments (T must be 1..%d)", PF_MAX_T);
+    if (opt.precision != ROASTER_PREC_F16 && opt.precision != ROASTER_PREC_SPLIT && opt.precision != ROASTER_PREC_BF16)
+        return rt_fail(ROASTER_EINVAL, "roaster_moe_prefill: unknown precision %d", opt.precision);
+    const int E = t->d.n_experts, H = (int)t->d.hidden, I = (int)t->d.inter;
+    if (E > 256) return rt_fail(ROASTER_EINVAL, "roaster_moe_prefill: at most 256 routed experts");
+    const int op = opt.precision == ROASTER_PREC_F16 ? PF_F16 : opt.precision == ROASTER_PREC_SPLIT ? PF_SPLIT : PF_BF16;
+    const size_t TT = (size_t)T, slots = 9 * TT;
+    const int max_tiles = (int)((8 * TT + GM - 1) / GM + E + (TT + GM - 1) / GM);
+
+    /* workspace */
+    size_t sz = 0;
+    auto take = [&](size_t n) { const size_t at = sz; sz += align256(n); return at; };
+    const size_t o_part = opt.logits_in ? 0 : take((size_t)RT_KSPLIT * TT * E * 4);
+    const size_t o_ids = take(TT * 8 * 4), o_w = take(TT * 8 * 4), o_rank = take(TT * 8 * 4);
+    const size_t o_sg = take(TT * 4), o_xinv = take(TT * 4), o_xfwd = take(TT * 4);
+    const size_t o_cnt = take((size_t)E * 4), o_off = take((size_t)E * 4), o_list = take((size_t)E * TT * 4);
+    const size_t o_grp = take(sizeof(PfGroup) * (E + 1)), o_tiles = take(sizeof(PfTile) * max_tiles);
+    const size_t o_nt = take(4), o_amax = take(slots * 4);
+    const size_t o_act = take(slots * I * 4), o_ed = take(slots * H * 4);
+    uint8_t *ws = (uint8_t *)rt_scratch(SCR_PF, sz);
+    unsigned *ctrl = rt_ctrl();
+    if (!ws || !ctrl) return ROASTER_ENOMEM;
+    RtState &R = rt();
+    const DecLayer &L = t->layers_h[layer];
+
+    if (!opt.logits_in) {
+        dim3 g((E + RT_TN - 1) / RT_TN, (T + RT_TM - 1) / RT_TM, RT_KSPLIT);
+        hipLaunchKernelGGL(pf_router_kernel, g, dim3(256), 0, R.stream, X, L.router, (float *)(ws + o_part), T, E, H);
+        if (rt_check(hipGetLastError(), "prefill router launch")) return ROASTER_EDEVICE;
+    }
+    PfTokArgs ta;
+    ta.X = X;
+    ta.gate_inp = L.gate_inp;
+    ta.part = opt.logits_in ? nullptr : (const float *)(ws + o_part);
+    ta.logits_in = opt.logits_in;
+    ta.bias = opt.logit_bias;
+    ta.logits_out = opt.logits_out;
+    ta.ids = (int *)(ws + o_ids);
+    ta.w = (float *)(ws + o_w);
+    ta.ids_out = opt.ids_out;
+    ta.w_out = opt.w_out;
+    ta.sg = (float *)(ws + o_sg);
+    ta.xinv = op == PF_F16 ? (float *)(ws + o_xinv) : nullptr;
+    ta.xfwd = op == PF_F16 ? (float *)(ws + o_xfwd) : nullptr;
+    ta.amax = op == PF_F16 ? (unsigned *)(ws + o_amax) : nullptr;
+    ta.err = (int *)(ctrl + 16);
+    ta.T = T; ta.E = E; ta.H = H;
+    hipLaunchKernelGGL(pf_token_kernel, dim3((T + 3) / 4), dim3(256), 0, R.stream, ta);
+    if (rt_check(hipGetLastError(), "prefill token launch")) return ROASTER_EDEVICE;
+
+    hipLaunchKernelGGL(pf_bucket_kernel, dim3(E), dim3(256), 0, R.stream, (const int *)(ws + o_ids), T,
+                       (int *)(ws + o_list), (int *)(ws + o_rank), (int *)(ws + o_cnt));
+    if (rt_check(hipGetLastError(), "prefill bucket launch")) return ROASTER_EDEVICE;
+
+    PfPlanArgs pa;
+    pa.L = L;
+    pa.eb_g = t->eb[0]; pa.eb_u = t->eb[1]; pa.eb_d = t->eb[2];
+    pa.q6g = t->d.q6[0]; pa.q6u = t->d.q6[1]; pa.q6d = t->d.q6[2];
+    pa.sq6g = t->d.sh_q6[0]; pa.sq6u = t->d.sh_q6[1]; pa.sq6d = t->d.sh_q6[2];
+    pa.cnt = (const int *)(ws + o_cnt);
+    pa.list = (const int *)(ws + o_list);
+    pa.off = (int *)(ws + o_off);
+    pa.counts_out = opt.counts_out;
+    pa.groups = (PfGroup *)(ws + o_grp);
+    pa.tiles = (PfTile *)(ws + o_tiles);
+    pa.ntiles = (int *)(ws + o_nt);
+    pa.T = T; pa.E = E;
+    hipLaunchKernelGGL(pf_plan_kernel, dim3(1), dim3(256), 0, R.stream, pa);
+    if (rt_check(hipGetLastError(), "prefill plan launch")) return ROASTER_EDEVICE;
+
+    PfGemmArgs ga;
+    ga.groups = pa.groups;
+    ga.tiles = pa.tiles;
+    ga.ntiles = pa.ntiles;
+    ga.X = X;
+    ga.xinv = ta.xinv;
+    ga.xfwd = ta.xfwd;
+    ga.act = (float *)(ws + o_act);
+    ga.amax = ta.amax;
+    ga.out = (float *)(ws + o_ed);
+    ga.H = H; ga.I = I;
+    if (int rc = pf_gemm_launch(ga, max_tiles, op)) return rc;
+
+    hipLaunchKernelGGL(pf_combine_kernel, dim3(T), dim3(256), 0, R.stream, (const float *)ga.out,
+                       (const int *)ta.ids, (const float *)ta.w, (const int *)(ws + o_rank), (const int *)pa.off,
+                       (const float *)ta.sg, Y, T, H);
+    return rt_check(hipGetLastError(), "prefill combine launch") ? ROASTER_EDEVICE : 0;
 }

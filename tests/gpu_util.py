@@ -105,3 +105,40 @@ class SynthTable:
         if self.t:
             R.lib().roaster_table_destroy(self.t)
             self.t = None
+
+
+def bf16_round(a):
+    """Round f32 values to the nearest bf16 (ties to even), kept as f32."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def zipf_bias(E, seed, s=1.1, tau=0.3):
+    """Per-expert logit bias tau * ln(p_e) with p_e proportional to rank_e^-s
+    (Zipf), ranks assigned to expert ids by a permutation drawn from seed.
+    tau = 0.3 skews T = 512 tokens' expert lists from 0 to about 200 rows."""
+    perm = np.random.default_rng(seed).permutation(E)
+    rank = np.empty(E, np.float64)
+    rank[perm] = np.arange(1, E + 1)
+    p = rank ** -s
+    p /= p.sum()
+    return (tau * np.log(p)).astype(np.float32)
+
+
+def prefill(table, X, layer=0, precision=R.PREC_F16, logits_in=None, bias=None):
+    """roaster_moe_prefill through the C ABI; returns (Y, logits, ids, w, counts)."""
+    T, H = X.shape
+    E = table.desc.n_experts
+    dx = Dev(X)
+    dy = Dev(nbytes=T * H * 4, shape=(T, H))
+    dl = Dev(nbytes=T * E * 4, shape=(T, E))
+    di = Dev(nbytes=T * 8 * 4, dtype=np.int32, shape=(T, 8))
+    dw = Dev(nbytes=T * 8 * 4, shape=(T, 8))
+    dc = Dev(nbytes=E * 4, dtype=np.int32, shape=(E,))
+    dli = Dev(logits_in) if logits_in is not None else None
+    db = Dev(bias) if bias is not None else None
+    o = R.RoasterPrefillOpts(precision, dli.p if dli else None, db.p if db else None, dl.p, di.p, dw.p, dc.p)
+    R.check(R.lib().roaster_moe_prefill(table.t, layer, dx.p, T, dy.p, C.byref(o)), "prefill")
+    R.check(R.lib().roaster_sync(), "sync")
+    return dy.get(), dl.get(), di.get(), dw.get(), dc.get()
