@@ -181,7 +181,7 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A,
         const float *row = task < nrouter ? L.router + (size_t)task * H : L.gate_inp;
 #pragma unroll
         for (int m = 0; m < 8; m++)
-            if (4 * lane + 256 * m < H) w[m] = *(const float4 *)(row + 4 * lane + 256 * m);
+            if (4 * lane + 256 * m < H) w[m] = gld_f4(row + 4 * lane + 256 * m);
     } else if (is_sh && lb < nb) {
         if (kind == 0) ch = load_gu_pair<false, false>(L.sgate, L.sup, j, nb, lb, c);
         else if (kind == 3) ch = load_gu_pair<true, true>(L.sgate, L.sup, j, nb, lb, c);

@@ -71,7 +71,7 @@ __device__ __forceinline__ void dequant_quarter(const uint8_t *blk, int qd, floa
     if (!Q6) {
         /* quarter qd = group g (kernels.c:1844-1852): qs[32g .. 32g+32) low
          * nibbles use sub-block 2g, high nibbles 2g+1 */
-        const uint4 hd = *(const uint4 *)blk;
+        const uint4 hd = gld_u4(blk);
         const float d = f16_bits_to_f32(hd.x & 0xFFFFu), dmin = f16_bits_to_f32(hd.x >> 16);
         const int j0 = 2 * qd, j1 = j0 + 1;
         const uint32_t s03 = hd.y, s47 = hd.z, s811 = hd.w;
@@ -88,8 +88,8 @@ __device__ __forceinline__ void dequant_quarter(const uint8_t *blk, int qd, floa
         }
         const float s0 = d * (float)sc0, mm0 = dmin * (float)m0;
         const float s1 = d * (float)sc1, mm1 = dmin * (float)m1;
-        const uint4 qa = *(const uint4 *)(blk + 16 + 32 * qd);
-        const uint4 qb = *(const uint4 *)(blk + 32 + 32 * qd);
+        const uint4 qa = gld_u4(blk + 16 + 32 * qd);
+        const uint4 qb = gld_u4(blk + 32 + 32 * qd);
         const uint32_t w8[8] = { qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w };
 #pragma unroll
         for (int i = 0; i < 8; i++)
@@ -105,16 +105,17 @@ __device__ __forceinline__ void dequant_quarter(const uint8_t *blk, int qd, floa
          * qh bits 2-3; odd quarter: high nibbles with qh bits 4-5 / 6-7 */
         const int n = qd >> 1, hiq = qd & 1;
         const uint8_t *ql = blk + 64 * n, *qh = blk + 128 + 32 * n;
-        const int8_t *sc = (const int8_t *)(blk + 192 + 8 * n);
-        const float d = f16_bits_to_f32(*(const uint16_t *)(blk + 208));
-        const u32x4_a2 l0 = *(const u32x4_a2 *)ql, l1 = *(const u32x4_a2 *)(ql + 16);
-        const u32x4_a2 l2 = *(const u32x4_a2 *)(ql + 32), l3 = *(const u32x4_a2 *)(ql + 48);
-        const u32x4_a2 h0 = *(const u32x4_a2 *)qh, h1 = *(const u32x4_a2 *)(qh + 16);
+        const uint2 scw = gld_u2a2(blk + 192 + 8 * n);
+        const uint32_t scl = hiq ? scw.y : scw.x;
+        const float d = f16_bits_to_f32(gld_u16(blk + 208));
+        const uint4 l0 = gld_u4a2(ql), l1 = gld_u4a2(ql + 16);
+        const uint4 l2 = gld_u4a2(ql + 32), l3 = gld_u4a2(ql + 48);
+        const uint4 h0 = gld_u4a2(qh), h1 = gld_u4a2(qh + 16);
         const uint32_t L[16] = { l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w,
                                  l2.x, l2.y, l2.z, l2.w, l3.x, l3.y, l3.z, l3.w };
         const uint32_t Hh[8] = { h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w };
-        const float dA0 = d * (float)sc[4 * hiq + 0], dA1 = d * (float)sc[4 * hiq + 1];
-        const float dB0 = d * (float)sc[4 * hiq + 2], dB1 = d * (float)sc[4 * hiq + 3];
+        const float dA0 = d * (float)(int8_t)byte_of(scl, 0), dA1 = d * (float)(int8_t)byte_of(scl, 1);
+        const float dB0 = d * (float)(int8_t)byte_of(scl, 2), dB1 = d * (float)(int8_t)byte_of(scl, 3);
         const int shl = hiq ? 4 : 0, shA = hiq ? 4 : 0, shB = hiq ? 6 : 2;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -163,7 +164,7 @@ __device__ __forceinline__ void load_x_tile(const float *src, float scale, uint1
     const int off = (t >> 2) * GLD + 64 * qd;
     float4 v[16];
 #pragma unroll
-    for (int i = 0; i < 16; i++) v[i] = src ? *(const float4 *)(src + 64 * qd + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < 16; i++) v[i] = src ? gld_f4(src + 64 * qd + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int c = 0; c < 8; c++) {
         f32x8 e = { v[2 * c].x, v[2 * c].y, v[2 * c].z, v[2 * c].w,

@@ -1,0 +1,628 @@
+/*
+ * pf_gemm.hip -- grouped expert GEMMs of the prefill path on MFMA.
+ *
+ * Both launch forms take a device tile list (group, first row) built by the
+ * caller and a group table (prefill.h); a tile is `chunk` consecutive rows of
+ * one group.  Launch grids are sized for the worst case and surplus
+ * workgroups exit at once.
+ *
+ * v2 (PF_F16, the default) -- weight-stationary, 256 threads (one wave per
+ * SIMD, so a wave may hold up to 512 registers):
+ *   A workgroup owns up to 96 rows of one group (MS = 1..3 row blocks of 32)
+ *   and 256 weight rows; every wave owns 64 of those rows as two 32-row MFMA
+ *   column blocks (gate/up: the same 32 gate rows and 32 up rows, so the
+ *   SiLU(gate) * up epilogue pairs accumulators in registers).  Each lane
+ *   dequantises, for one weight row, the half super-block that forms its MFMA
+ *   B operand, straight into registers: weights never pass through LDS.
+ *   Inside a super-block the K order is permuted so that the 8 k-items a lane
+ *   feeds per v_mfma_f32_32x32x16_f16 come from one dword of Q6_K ql / qh (or
+ *   Q4_K qs): items i = 0..3 / 4..7 of k-slice kk in half h are super-block
+ *   positions 128h + 64(kk/8) + 4(kk%8) + i and + 32 + i - 4.  Activations are
+ *   stored in that permuted order (fp16, scaled per row by a power of two), so
+ *   A and B agree and the dot product is unchanged.
+ *   Q6_K: 1024 + q is built as an fp16 bit pattern with v_perm_b32, then
+ *   fma(1024 + q, sc, -1056 sc) = sc (q - 32) exactly and one multiply by d
+ *   rounds once: the fp16 weight is the reference's f32 weight (kernels.c:
+ *   1855-1874) rounded to nearest even.  Q4_K: d sc q - dmin m in f32 with one
+ *   fused multiply-add (kernels.c:1844-1852), then rounded to fp16.
+ *
+ * v1 (PF_SPLIT, PF_BF16) -- 64 x 64 output tiles, 256 threads, operands of
+ * both sides dequantised / converted into LDS (gemm.h).
+ */
+#include "internal.h"
+#include "gemm.h"
+#include "prefill.h"
+
+static __device__ __forceinline__ float pf_silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
+/* Virtual block id: blocks b < R = ntiles * nblk run; on a grid dispatched
+ * round-robin over the 8 XCDs, XCD b % 8 takes the contiguous range of
+ * virtual ids [(b % 8) * R / 8, ...), so the n-blocks of one tile and the
+ * consecutive tiles of one expert share an L2. */
+__device__ __forceinline__ int pf_virtual_block(int b, int R)
+{
+    return (R & 7) ? b : (b & 7) * (R >> 3) + (b >> 3);
+}
+
+struct PfRowMeta {
+    const float *src[GM];
+    int slot[GM];
+    float inv[GM], fwd[GM];
+};
+
+template <int OP>
+__global__ void __launch_bounds__(GT) pf_gu_kernel(PfGemmArgs A)
+{
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    __shared__ PfRowMeta meta;
+    const int nblk = A.I / 32;
+    const int R = *A.ntiles * nblk;
+    const int b = blockIdx.x;
+    if (b >= R) return;
+    const int v = pf_virtual_block(b, R);
+    const PfTile tile = A.tiles[v / nblk];
+    const int j0 = (v % nblk) * 32;
+    const PfGroup &G = A.groups[tile.grp];
+    const int t = threadIdx.x;
+    if (t < GM) {
+        const int a = tile.m0 + t;
+        if (a < G.n) {
+            const int tok = G.tok ? G.tok[a] : G.tok0 + a;
+            meta.src[t] = A.X + (size_t)tok * A.H;
+            meta.slot[t] = G.slot0 + a;
+            meta.inv[t] = A.xinv ? A.xinv[tok] : 1.0f;
+            meta.fwd[t] = A.xfwd ? A.xfwd[tok] : 1.0f;
+        } else {
+            meta.src[t] = nullptr;
+            meta.slot[t] = -1;
+            meta.inv[t] = 1.0f;
+            meta.fwd[t] = 1.0f;
+        }
+    }
+    uint16_t *Xh = smem, *Wh = smem + G_TILE_ELEMS;
+    uint16_t *Xl = smem + 2 * G_TILE_ELEMS, *Wl = smem + 3 * G_TILE_ELEMS;
+    /* weight row of this thread: tile rows 0..31 gate rows j0.., 32..63 up rows j0.. */
+    const int wr = t >> 2;
+    const bool is_up = wr >= 32;
+    const bool q6 = is_up ? G.uq6 : G.gq6;
+    const size_t bb = q6 ? RQ6K_BYTES : RQ4K_BYTES;
+    const int nkb = A.H / GK;
+    const uint8_t *wrow = (is_up ? G.u : G.g) + (size_t)(j0 + (wr & 31)) * nkb * bb;
+    __syncthreads();
+    const float *xsrc = meta.src[wr];
+    const float xinv = meta.inv[wr];
+    const int w = t >> 6, wm = w & 1, wn = w >> 1;
+    f32x16 acc = {};
+    for (int kb = 0; kb < nkb; kb++) {
+        if (kb) __syncthreads();
+        load_w_tile<OP>(wrow + kb * bb, q6, Wh, Wl);
+        load_x_tile<OP>(xsrc ? xsrc + kb * GK : nullptr, xinv, Xh, Xl);
+        __syncthreads();
+        mfma_tile<OP>(acc, Xh, Xl, Wh, Wl, wm, wn);
+    }
+    /* epilogue: gate / up blocks meet in LDS */
+    __syncthreads();
+    float *Cs = (float *)smem;                 /* [64][65] */
+    const int l = t & 63;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int m = 32 * wm + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
+        Cs[m * 65 + 32 * wn + (l & 31)] = acc[i];
+    }
+    __syncthreads();
+    const int m = t >> 2, q = t & 3;
+    const int slot = meta.slot[m];
+    const float fwd = meta.fwd[m];
+    float e8[8];
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float g = Cs[m * 65 + 8 * q + i] * fwd, u = Cs[m * 65 + 32 + 8 * q + i] * fwd;
+        e8[i] = pf_silu_mul(g, u);
+        mx = fmaxf(mx, fabsf(e8[i]));
+    }
+    if (slot >= 0) {
+        float4 *dst = (float4 *)(A.act + (size_t)slot * A.I + j0 + 8 * q);
+        dst[0] = make_float4(e8[0], e8[1], e8[2], e8[3]);
+        dst[1] = make_float4(e8[4], e8[5], e8[6], e8[7]);
+    }
+    if (A.amax) {
+        mx = fmaxf(mx, __shfl_xor(mx, 1));
+        mx = fmaxf(mx, __shfl_xor(mx, 2));
+        if (q == 0 && slot >= 0) atomicMax(A.amax + slot, __builtin_bit_cast(unsigned, mx));
+    }
+}
+
+template <int OP>
+__global__ void __launch_bounds__(GT) pf_down_kernel(PfGemmArgs A)
+{
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    __shared__ PfRowMeta meta;
+    const int nblk = A.H / GN;
+    const int R = *A.ntiles * nblk;
+    const int b = blockIdx.x;
+    if (b >= R) return;
+    const int v = pf_virtual_block(b, R);
+    const PfTile tile = A.tiles[v / nblk];
+    const int n0 = (v % nblk) * GN;
+    const PfGroup &G = A.groups[tile.grp];
+    const int t = threadIdx.x;
+    if (t < GM) {
+        const int a = tile.m0 + t;
+        if (a < G.n) {
+            const int slot = G.slot0 + a;
+            meta.src[t] = A.act + (size_t)slot * A.I;
+            meta.slot[t] = slot;
+            float inv = 1.0f, fwd = 1.0f;
+            if (A.amax) row_scale(__builtin_bit_cast(float, A.amax[slot]), inv, fwd);
+            meta.inv[t] = inv;
+            meta.fwd[t] = fwd;
+        } else {
+            meta.src[t] = nullptr;
+            meta.slot[t] = -1;
+            meta.inv[t] = 1.0f;
+            meta.fwd[t] = 1.0f;
+        }
+    }
+    uint16_t *Xh = smem, *Wh = smem + G_TILE_ELEMS;
+    uint16_t *Xl = smem + 2 * G_TILE_ELEMS, *Wl = smem + 3 * G_TILE_ELEMS;
+    const int wr = t >> 2;
+    const bool q6 = G.dq6;
+    const size_t bb = q6 ? RQ6K_BYTES : RQ4K_BYTES;
+    const int nkb = A.I / GK;
+    const uint8_t *wrow = G.d + (size_t)(n0 + wr) * nkb * bb;
+    __syncthreads();
+    const float *xsrc = meta.src[wr];
+    const float xinv = meta.inv[wr];
+    const int w = t >> 6, wm = w & 1, wn = w >> 1;
+    f32x16 acc = {};
+    for (int kb = 0; kb < nkb; kb++) {
+        if (kb) __syncthreads();
+        load_w_tile<OP>(wrow + kb * bb, q6, Wh, Wl);
+        load_x_tile<OP>(xsrc ? xsrc + kb * GK : nullptr, xinv, Xh, Xl);
+        __syncthreads();
+        mfma_tile<OP>(acc, Xh, Xl, Wh, Wl, wm, wn);
+    }
+    const int l = t & 63;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int m = 32 * wm + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
+        const int slot = meta.slot[m];
+        if (slot >= 0) A.out[(size_t)slot * A.H + n0 + 32 * wn + (l & 31)] = acc[i] * meta.fwd[m];
+    }
+}
+
+
+/* ---- v2 ------------------------------------------------------------------- */
+#define V2_T 256                  /* threads */
+#define V2_W 4                    /* waves */
+#define V2_GU_J (32 * V2_W)       /* gate/up j columns per workgroup */
+#define V2_DN_N (64 * V2_W)       /* down output rows per workgroup */
+#define V2_MC 96                  /* rows per tile */
+#define V2_LD (GK + 8)            /* LDS row stride (fp16 elements) */
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+/* One lane's raw share of a super-block: half h (weights 128h .. 128h+127). */
+struct RawQ6 { uint32_t L[16], Hh[8], S[2], d; };
+struct RawQ4 { uint32_t hd[4], Q[16]; };
+template <bool Q6> struct RawOf;
+template <> struct RawOf<true> { typedef RawQ6 T; };
+template <> struct RawOf<false> { typedef RawQ4 T; };
+
+__device__ __forceinline__ void raw_load(RawQ6 &r, const uint8_t *blk, int h)
+{
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint4 v = gld_u4a2(blk + 64 * h + 16 * i);
+        r.L[4 * i] = v.x; r.L[4 * i + 1] = v.y; r.L[4 * i + 2] = v.z; r.L[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const uint4 v = gld_u4a2(blk + 128 + 32 * h + 16 * i);
+        r.Hh[4 * i] = v.x; r.Hh[4 * i + 1] = v.y; r.Hh[4 * i + 2] = v.z; r.Hh[4 * i + 3] = v.w;
+    }
+    const uint2 s = gld_u2a2(blk + 192 + 8 * h);
+    r.S[0] = s.x; r.S[1] = s.y;
+    r.d = gld_u16(blk + 208);
+}
+
+__device__ __forceinline__ void raw_load(RawQ4 &r, const uint8_t *blk, int h)
+{
+    const uint4 hd = gld_u4(blk);
+    r.hd[0] = hd.x; r.hd[1] = hd.y; r.hd[2] = hd.z; r.hd[3] = hd.w;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint4 v = gld_u4(blk + 16 + 64 * h + 16 * i);
+        r.Q[4 * i] = v.x; r.Q[4 * i + 1] = v.y; r.Q[4 * i + 2] = v.z; r.Q[4 * i + 3] = v.w;
+    }
+}
+
+/* Per super-block constants of one lane's half. */
+struct ConstQ6 { f16x2 sc[8], bias[8], d; };   /* sc[s] = (S[s], S[s]), bias = -1056 sc */
+struct ConstQ4 { float s[4], m[4]; };          /* sub-blocks 4h .. 4h+3: d*sc, dmin*m */
+template <bool Q6> struct ConstOf;
+template <> struct ConstOf<true> { typedef ConstQ6 T; };
+template <> struct ConstOf<false> { typedef ConstQ4 T; };
+
+__device__ __forceinline__ void raw_consts(const RawQ6 &r, int h, ConstQ6 &c)
+{
+    (void)h;
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        const int v = (int)(int8_t)((r.S[s >> 2] >> (8 * (s & 3))) & 0xFFu);
+        const _Float16 f = (_Float16)v;
+        c.sc[s] = (f16x2){ f, f };
+        c.bias[s] = c.sc[s] * (f16x2){ (_Float16)-1056.0f, (_Float16)-1056.0f };   /* exact: 33 * 32 * sc */
+    }
+    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)r.d);
+    c.d = (f16x2){ d, d };
+}
+
+__device__ __forceinline__ void raw_consts(const RawQ4 &r, int h, ConstQ4 &c)
+{
+    const float d = f16_bits_to_f32(r.hd[0] & 0xFFFFu), dmin = f16_bits_to_f32(r.hd[0] >> 16);
+    const uint32_t s03 = r.hd[1], s47 = r.hd[2], s811 = r.hd[3];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int sc, m;
+        if (h == 0) {
+            sc = byte_of(s03, i) & 63;
+            m = byte_of(s47, i) & 63;
+        } else {
+            sc = (byte_of(s811, i) & 15) | ((byte_of(s03, i) >> 6) << 4);
+            m = (byte_of(s811, i) >> 4) | ((byte_of(s47, i) >> 6) << 4);
+        }
+        c.s[i] = d * (float)sc;
+        c.m[i] = dmin * (float)m;
+    }
+}
+
+/* fp16 pairs (1024 + b0, 1024 + b1) and (1024 + b2, 1024 + b3) of the bytes of q. */
+__device__ __forceinline__ f16x2 magic_lo(uint32_t q) { return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(q, 0x64646464u, 0x00050004u)); }
+__device__ __forceinline__ f16x2 magic_hi(uint32_t q) { return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(q, 0x64646464u, 0x00070006u)); }
+
+__device__ __forceinline__ uint32_t q6_pair(f16x2 v, f16x2 sc, f16x2 bias, f16x2 d)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(v, sc, bias) * d);
+}
+
+/* B operands of k-slices j and j + 8 (j = 0..7). */
+__device__ __forceinline__ void dequant_pair(const RawQ6 &r, const ConstQ6 &c, int j, f16x8 &b0, f16x8 &b1)
+{
+    const uint32_t A = r.L[j], B = r.L[8 + j], C = r.Hh[j];
+    const uint32_t qa = (A & 0x0F0F0F0Fu) | ((C << 4) & 0x30303030u);
+    const uint32_t qb = (B & 0x0F0F0F0Fu) | ((C << 2) & 0x30303030u);
+    const uint32_t qc = ((A >> 4) & 0x0F0F0F0Fu) | (C & 0x30303030u);
+    const uint32_t qd = ((B >> 4) & 0x0F0F0F0Fu) | ((C >> 2) & 0x30303030u);
+    const int s = j >> 2;
+    const uint4 u0 = { q6_pair(magic_lo(qa), c.sc[s], c.bias[s], c.d), q6_pair(magic_hi(qa), c.sc[s], c.bias[s], c.d),
+                       q6_pair(magic_lo(qb), c.sc[s + 2], c.bias[s + 2], c.d),
+                       q6_pair(magic_hi(qb), c.sc[s + 2], c.bias[s + 2], c.d) };
+    const uint4 u1 = { q6_pair(magic_lo(qc), c.sc[s + 4], c.bias[s + 4], c.d),
+                       q6_pair(magic_hi(qc), c.sc[s + 4], c.bias[s + 4], c.d),
+                       q6_pair(magic_lo(qd), c.sc[s + 6], c.bias[s + 6], c.d),
+                       q6_pair(magic_hi(qd), c.sc[s + 6], c.bias[s + 6], c.d) };
+    b0 = __builtin_bit_cast(f16x8, u0);
+    b1 = __builtin_bit_cast(f16x8, u1);
+}
+
+__device__ __forceinline__ f16x8 q4_slice(uint32_t a, float s0, float m0, float s1, float m1)
+{
+    const uint32_t lo = a & 0x0F0F0F0Fu, hi = (a >> 4) & 0x0F0F0F0Fu;
+    f32x8 v;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        v[b] = fmaf(s0, (float)((lo >> (8 * b)) & 0xFFu), -m0);
+        v[4 + b] = fmaf(s1, (float)((hi >> (8 * b)) & 0xFFu), -m1);
+    }
+    return __builtin_convertvector(v, f16x8);
+}
+
+__device__ __forceinline__ void dequant_pair(const RawQ4 &r, const ConstQ4 &c, int j, f16x8 &b0, f16x8 &b1)
+{
+    b0 = q4_slice(r.Q[j], c.s[0], c.m[0], c.s[1], c.m[1]);
+    b1 = q4_slice(r.Q[8 + j], c.s[2], c.m[2], c.s[3], c.m[3]);
+}
+
+/* Natural position p (multiple of 4) of a super-block -> its permuted slot. */
+__device__ __forceinline__ int perm_slot4(int p)
+{
+    const int h = p >> 7, q = p & 127, hi = q >> 6, r = q & 63;
+    const int l0 = r < 32 ? r : r - 32, i0 = r < 32 ? 0 : 4;
+    return (8 * hi + (l0 >> 2)) * 16 + 8 * h + i0;
+}
+
+struct V2Meta {
+    int tok[V2_MC];
+    int slot[V2_MC];
+    float inv[V2_MC], fwd[V2_MC];
+};
+
+/* One K step (super-block) of MS row blocks x two 32-row weight blocks. */
+template <int MS, bool Q6A, bool Q6B>
+__device__ __forceinline__ void v2_kstep(f32x16 (&acc)[MS][2], const _Float16 *Xs, int ld,
+                                         const typename RawOf<Q6A>::T &ra, const typename RawOf<Q6B>::T &rb, int h)
+{
+    typename ConstOf<Q6A>::T ca;
+    typename ConstOf<Q6B>::T cb;
+    raw_consts(ra, h, ca);
+    raw_consts(rb, h, cb);
+    const int l = threadIdx.x & 63;
+    const _Float16 *xa = Xs + (l & 31) * ld + 8 * (l >> 5);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        f16x8 a0b0, a0b1, a1b0, a1b1;
+        dequant_pair(ra, ca, j, a0b0, a0b1);
+        dequant_pair(rb, cb, j, a1b0, a1b1);
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++) {
+            const f16x8 x0 = *(const f16x8 *)(xa + ms * 32 * ld + 16 * j);
+            const f16x8 x1 = *(const f16x8 *)(xa + ms * 32 * ld + 16 * (j + 8));
+            acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, a0b0, acc[ms][0], 0, 0, 0);
+            acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, a1b0, acc[ms][1], 0, 0, 0);
+            acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, a0b1, acc[ms][0], 0, 0, 0);
+            acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, a1b1, acc[ms][1], 0, 0, 0);
+        }
+    }
+}
+
+/* gate/up: block = (tile, V2_GU_J j's); wave w: gate and up rows jw .. jw+31. */
+template <int MS, bool G6, bool U6>
+__device__ __forceinline__ void v2_gu_body(const PfGemmArgs &A, const PfGroup &G, const V2Meta &meta, int mlen, int jw,
+                           _Float16 *Xs)
+{
+    typedef typename RawOf<G6>::T RG;
+    typedef typename RawOf<U6>::T RU;
+    const int t = threadIdx.x, l = t & 63, h = l >> 5;
+    const int nkb = A.H / GK;
+    const size_t bg = G6 ? RQ6K_BYTES : RQ4K_BYTES, bu = U6 ? RQ6K_BYTES : RQ4K_BYTES;
+    const uint8_t *gr = G.g + (size_t)(jw + (l & 31)) * nkb * bg;
+    const uint8_t *ur = G.u + (size_t)(jw + (l & 31)) * nkb * bu;
+    /* activation staging: 16-byte pieces, row = idx / 32, piece = idx % 32 */
+    constexpr int NP = (MS * 32 * 32 + V2_T - 1) / V2_T;
+    uint4 xr[NP];
+    const uint16_t *xrow[NP];
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const int idx = t + i * V2_T, row = idx >> 5;
+        xrow[i] = row < mlen ? A.X16 + (size_t)meta.tok[row] * A.H + 8 * (idx & 31) : nullptr;
+    }
+    auto x_load = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < NP; i++) xr[i] = xrow[i] ? gld_u4(xrow[i] + kb * GK) : make_uint4(0u, 0u, 0u, 0u);
+    };
+    auto x_store = [&](_Float16 *dst) {
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int idx = t + i * V2_T, row = idx >> 5;
+            if (row < MS * 32) *(uint4 *)(dst + row * V2_LD + 8 * (idx & 31)) = xr[i];
+        }
+    };
+    f32x16 acc[MS][2];
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++) acc[ms][0] = acc[ms][1] = (f32x16){};
+    RG rg;
+    RU ru;
+    raw_load(rg, gr, h);            /* issued before the staging loads, so that the wait */
+    raw_load(ru, ur, h);            /* for those leaves nothing pending at the loop head */
+    x_load(0);
+    x_store(Xs);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; kb++) {
+        _Float16 *cur = Xs + (kb & 1) * (V2_MC * V2_LD);
+        RG ng;
+        RU nu;
+        const bool more = kb + 1 < nkb;
+        if (more) {
+            x_load(kb + 1);
+            raw_load(ng, gr + (kb + 1) * bg, h);
+            raw_load(nu, ur + (kb + 1) * bu, h);
+        }
+        v2_kstep<MS, G6, U6>(acc, cur, V2_LD, rg, ru, h);
+        if (more) {
+            x_store(Xs + ((kb + 1) & 1) * (V2_MC * V2_LD));
+            rg = ng;
+            ru = nu;
+        }
+        __syncthreads();
+    }
+    /* epilogue: act = silu(gate) * up (f32), and each row's largest |act|
+     * over this workgroup's columns into amax[slot] (the down GEMM's row scale) */
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int m0 = 32 * ms + 8 * (i >> 2) + (i & 3), m = m0 + 4 * h;
+            float e = 0.0f;
+            if (m < mlen) {
+                const float f = meta.fwd[m];
+                e = pf_silu_mul(acc[ms][0][i] * f, acc[ms][1][i] * f);
+                A.act[(size_t)meta.slot[m] * A.I + jw + (l & 31)] = e;
+            }
+            float lo, hi;
+            half_max(fabsf(e), lo, hi);
+            if (l == 0) {
+                if (m0 < mlen) atomicMax(A.amax + meta.slot[m0], __builtin_bit_cast(unsigned, lo));
+                if (m0 + 4 < mlen) atomicMax(A.amax + meta.slot[m0 + 4], __builtin_bit_cast(unsigned, hi));
+            }
+        }
+}
+
+/* down: block = (tile, V2_DN_N output rows); wave w: rows nw .. nw+63.  The
+ * act rows (f32) are staged whole (K = inter) into LDS as scaled fp16 in the
+ * permuted K order, after the first K step's weight loads are in flight. */
+template <int MS, bool D6>
+__device__ __forceinline__ void v2_dn_body(const PfGemmArgs &A, const V2Meta &meta, const PfGroup &G, int mlen,
+                                           int nw, _Float16 *Xs)
+{
+    typedef typename RawOf<D6>::T RD;
+    const int t = threadIdx.x, l = t & 63, h = l >> 5;
+    const int nkb = A.I / GK, ld = A.I + 8;
+    const size_t bd = D6 ? RQ6K_BYTES : RQ4K_BYTES;
+    const uint8_t *r0 = G.d + (size_t)(nw + (l & 31)) * nkb * bd;
+    const uint8_t *r1 = G.d + (size_t)(nw + 32 + (l & 31)) * nkb * bd;
+    RD a0, a1;
+    raw_load(a0, r0, h);
+    raw_load(a1, r1, h);
+    /* staging: float4 pieces, 16 in flight per thread */
+    const int per_row = A.I / 4, total = mlen * per_row;
+    for (int base = 0; base < total; base += 16 * V2_T) {
+        float4 v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int idx = base + t + u * V2_T, row = idx / per_row, c = idx - row * per_row;
+            v[u] = idx < total ? gld_f4(A.act + (size_t)meta.slot[row] * A.I + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int idx = base + t + u * V2_T, row = idx / per_row, c = idx - row * per_row;
+            if (idx < total) {
+                const float s = meta.inv[row];
+                const f32x8 e = { v[u].x * s, v[u].y * s, v[u].z * s, v[u].w * s, 0.f, 0.f, 0.f, 0.f };
+                const uint4 cu = __builtin_bit_cast(uint4, __builtin_convertvector(e, f16x8));
+                const int k = 4 * c;
+                *(uint2 *)(Xs + row * ld + (k & ~255) + perm_slot4(k & 255)) = make_uint2(cu.x, cu.y);
+            }
+        }
+    }
+    __syncthreads();
+    f32x16 acc[MS][2];
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++) acc[ms][0] = acc[ms][1] = (f32x16){};
+    for (int kb = 0; kb < nkb; kb++) {
+        RD n0, n1;
+        const bool more = kb + 1 < nkb;
+        if (more) {
+            raw_load(n0, r0 + (kb + 1) * bd, h);
+            raw_load(n1, r1 + (kb + 1) * bd, h);
+        }
+        v2_kstep<MS, D6, D6>(acc, Xs + kb * GK, ld, a0, a1, h);
+        if (more) {
+            a0 = n0;
+            a1 = n1;
+        }
+    }
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (m < mlen) {
+                const float f = meta.fwd[m];
+                float *o = A.out + (size_t)meta.slot[m] * A.H + nw + (l & 31);
+                o[0] = acc[ms][0][i] * f;
+                o[32] = acc[ms][1][i] * f;
+            }
+        }
+}
+
+__device__ __forceinline__ bool v2_tile(const PfGemmArgs &A, int nblk, int &v, PfTile &tile)
+{
+    const int R = *A.ntiles * nblk;
+    const int b = blockIdx.x;
+    if (b >= R) return false;
+    v = pf_virtual_block(b, R);
+    tile = A.tiles[v / nblk];
+    return true;
+}
+
+extern "C" __global__ void __launch_bounds__(V2_T) pf2_gu_kernel(PfGemmArgs A)
+{
+    extern __shared__ __attribute__((aligned(16))) _Float16 xs2[];
+    __shared__ V2Meta meta;
+    const int nblk = A.I / V2_GU_J;
+    int v;
+    PfTile tile;
+    if (!v2_tile(A, nblk, v, tile)) return;
+    const PfGroup &G = A.groups[tile.grp];
+    const int mlen = min(V2_MC, G.n - tile.m0);
+    const int t = threadIdx.x;
+    if (t < V2_MC) {
+        const int a = tile.m0 + t;
+        if (t < mlen) {
+            const int tok = G.tok ? G.tok[a] : G.tok0 + a;
+            meta.tok[t] = tok;
+            meta.slot[t] = G.slot0 + a;
+            meta.fwd[t] = A.xfwd ? A.xfwd[tok] : 1.0f;
+        }
+    }
+    __syncthreads();
+    const int jw = (v % nblk) * V2_GU_J + 32 * (t >> 6);
+    const int ms = (mlen + 31) >> 5;
+    const int ty = (G.gq6 ? 2 : 0) | (G.uq6 ? 1 : 0);
+#define GU_CASE(M)                                                                   \
+    if (ms == M) {                                                                   \
+        if (ty == 3) v2_gu_body<M, true, true>(A, G, meta, mlen, jw, xs2);          \
+        else if (ty == 2) v2_gu_body<M, true, false>(A, G, meta, mlen, jw, xs2);    \
+        else if (ty == 1) v2_gu_body<M, false, true>(A, G, meta, mlen, jw, xs2);    \
+        else v2_gu_body<M, false, false>(A, G, meta, mlen, jw, xs2);                \
+        return;                                                                      \
+    }
+    GU_CASE(1)
+    GU_CASE(2)
+    GU_CASE(3)
+#undef GU_CASE
+}
+
+extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
+{
+    extern __shared__ __attribute__((aligned(16))) _Float16 xs2[];
+    __shared__ V2Meta meta;
+    const int nblk = A.H / V2_DN_N;
+    int v;
+    PfTile tile;
+    if (!v2_tile(A, nblk, v, tile)) return;
+    const PfGroup &G = A.groups[tile.grp];
+    const int mlen = min(V2_MC, G.n - tile.m0);
+    const int t = threadIdx.x, w = t >> 6;
+    if (t < mlen) {
+        const int slot = G.slot0 + tile.m0 + t;
+        float inv, fwd;
+        row_scale(__builtin_bit_cast(float, A.amax[slot]), inv, fwd);
+        meta.slot[t] = slot;
+        meta.inv[t] = inv;
+        meta.fwd[t] = fwd;
+    }
+    __syncthreads();
+    const int nw = (v % nblk) * V2_DN_N + 64 * w;
+    const int ms = (mlen + 31) >> 5;
+#define DN_CASE(M)                                                                   \
+    if (ms == M) {                                                                   \
+        if (G.dq6) v2_dn_body<M, true>(A, meta, G, mlen, nw, xs2);                  \
+        else v2_dn_body<M, false>(A, meta, G, mlen, nw, xs2);                       \
+        return;                                                                      \
+    }
+    DN_CASE(1)
+    DN_CASE(2)
+    DN_CASE(3)
+#undef DN_CASE
+}
+
+/* ---- host ----------------------------------------------------------------- */
+template <int OP>
+static int launch_v1(const PfGemmArgs &A, int max_tiles)
+{
+    RtState &R = rt();
+    const size_t lds = gemm_lds_bytes(OP);
+    const int gu_blocks = max_tiles * (A.I / 32), d_blocks = max_tiles * (A.H / GN);
+    hipLaunchKernelGGL(pf_gu_kernel<OP>, dim3(gu_blocks), dim3(GT), lds, R.stream, A);
+    if (rt_check(hipGetLastError(), "prefill gate/up launch")) return ROASTER_EDEVICE;
+    hipLaunchKernelGGL(pf_down_kernel<OP>, dim3(d_blocks), dim3(GT), lds, R.stream, A);
+    return rt_check(hipGetLastError(), "prefill down launch") ? ROASTER_EDEVICE : 0;
+}
+
+int pf_gemm_chunk(int op) { return op == PF_F16 ? V2_MC : GM; }
+
+int pf_gemm_launch(const PfGemmArgs &A, int max_tiles, int op)
+{
+    if (max_tiles <= 0) return 0;
+    if (op == PF_SPLIT) return launch_v1<PF_SPLIT>(A, max_tiles);
+    if (op == PF_BF16) return launch_v1<PF_BF16>(A, max_tiles);
+    RtState &R = rt();
+    const size_t lds_gu = 2 * (size_t)V2_MC * V2_LD * 2, lds_dn = (size_t)V2_MC * (A.I + 8) * 2;
+    hipLaunchKernelGGL(pf2_gu_kernel, dim3(max_tiles * (A.I / V2_GU_J)), dim3(V2_T), lds_gu, R.stream, A);
+    if (rt_check(hipGetLastError(), "prefill gate/up launch")) return ROASTER_EDEVICE;
+    hipLaunchKernelGGL(pf2_down_kernel, dim3(max_tiles * (A.H / V2_DN_N)), dim3(V2_T), lds_dn, R.stream, A);
+    return rt_check(hipGetLastError(), "prefill down launch") ? ROASTER_EDEVICE : 0;
+}

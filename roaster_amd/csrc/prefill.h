@@ -30,13 +30,17 @@ struct PfGemmArgs {
     const PfGroup *groups;
     const PfTile *tiles;
     const int *ntiles;              /* device count of valid tiles */
-    const float *X;                 /* [* x H] activations */
+    const float *X;                 /* [* x H] activations (f32, natural order) */
+    const uint16_t *X16;            /* [* x H] fp16 activations, scaled, permuted (v2), or NULL */
     const float *xinv, *xfwd;       /* per X row power-of-two scales (fp16 mode), or NULL */
     float *act;                     /* [slots x I]: silu(gate) * up */
     unsigned *amax;                 /* [slots] max |act| bits (fp16 mode), or NULL */
     float *out;                     /* [slots x H]: down products */
     int H, I;
 };
+
+/* Rows per tile the GEMMs of operand mode op expect in the tile list. */
+int pf_gemm_chunk(int op);
 
 /* Launch the gate/up and down GEMMs over up to max_tiles tiles.  op: PF_F16,
  * PF_SPLIT or PF_BF16 (gemm.h).  0 or ROASTER_EDEVICE. */

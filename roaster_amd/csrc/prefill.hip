@@ -11,10 +11,10 @@
  *                      token order, i.e. the stable counting sort over (t, k)
  *                      of model.c:1713-1731
  *   pf_plan_kernel     offsets (prefix sums of the counts), groups and the
- *                      64-row tile list; the shared expert is one more group
- *                      over all T tokens (model.c:1694-1711)
- *   pf_gu_kernel       grouped GEMM gate/up, SiLU(gate) * up epilogue
- *   pf_down_kernel     grouped GEMM down
+ *                      tile list; the shared expert is one more group over
+ *                      all T tokens (model.c:1694-1711)
+ *   grouped GEMMs      gate/up with the SiLU(gate) * up epilogue, then down
+ *                      (pf_gemm.hip)
  *   pf_combine_kernel  Y[t] = sigmoid(s_t) * shared(t), then += w * expert
  *                      output in ascending expert id (model.c:1709-1711,
  *                      1776-1788), one fused multiply-add per term
@@ -33,7 +33,14 @@
 #define PF_MAX_T (1 << 16)
 #define RT_KSPLIT 4               /* router K split */
 
-__device__ __forceinline__ float pf_silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+/* Natural position p (multiple of 4) inside a super-block -> the slot of its
+ * first element in the fp16 GEMM's permuted K order (pf_gemm.hip). */
+__device__ __forceinline__ int pf_perm_slot4(int p)
+{
+    const int h = p >> 7, q = p & 127, hi = q >> 6, r = q & 63;
+    const int l0 = r < 32 ? r : r - 32, i0 = r < 32 ? 0 : 4;
+    return (8 * hi + (l0 >> 2)) * 16 + 8 * h + i0;
+}
 
 /* Exclusive prefix sum over a 256-thread workgroup; *total gets the sum. */
 __device__ int block_scan_256(int v, int *lds, int *total)
@@ -125,7 +132,8 @@ struct PfTokArgs {
     float *w_out;
     float *sg;                  /* [T] */
     float *xinv, *xfwd;         /* [T] (fp16 mode) or NULL */
-    unsigned *amax;             /* [9T] zeroed here, or NULL */
+    uint16_t *x16;              /* [T x H] fp16 X * xinv in the GEMM's permuted K order, or NULL */
+    unsigned *amax;             /* [9T] per-slot max |act| bits, zeroed here, or NULL */
     int *err;
     int T, E, H;
 };
@@ -150,15 +158,22 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
     dot = group_sum<64>(dot);
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
-    if (lane == 0) {
-        A.sg[t] = 1.0f / (1.0f + expf(-dot));
-        if (A.xinv) {
-            float inv, fwd;
-            row_scale(mx, inv, fwd);
+    if (A.xinv) {
+        float inv, fwd;
+        row_scale(mx, inv, fwd);
+        if (lane == 0) {
             A.xinv[t] = inv;
             A.xfwd[t] = fwd;
         }
+        if (A.x16)
+            for (int k = 4 * lane; k < A.H; k += 256) {
+                const float4 v = *(const float4 *)(x + k);
+                const f32x8 e = { v.x * inv, v.y * inv, v.z * inv, v.w * inv, 0.f, 0.f, 0.f, 0.f };
+                const uint4 c = __builtin_bit_cast(uint4, __builtin_convertvector(e, f16x8));
+                *(uint2 *)(A.x16 + (size_t)t * A.H + (k & ~255) + pf_perm_slot4(k & 255)) = make_uint2(c.x, c.y);
+            }
     }
+    if (lane == 0) A.sg[t] = 1.0f / (1.0f + expf(-dot));
     if (A.amax && lane < 9) A.amax[(size_t)t * 9 + lane] = 0u;
     /* logits */
     float v4[4];
@@ -231,6 +246,7 @@ struct PfPlanArgs {
     PfTile *tiles;
     int *ntiles;
     int T, E;
+    int chunk;                  /* rows per tile */
 };
 
 extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
@@ -238,7 +254,7 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
     __shared__ int wsum[4];
     const int e = threadIdx.x;
     const int c = e < A.E ? A.cnt[e] : 0;
-    const int nt = (c + GM - 1) / GM;
+    const int nt = (c + A.chunk - 1) / A.chunk;
     int tot_rows, tot_tiles;
     const int off = block_scan_256(c, wsum, &tot_rows);
     const int toff = block_scan_256(nt, wsum, &tot_tiles);
@@ -256,9 +272,9 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
         G.tok = A.list + (size_t)e * A.T;
         G.pad = 0;
         A.groups[e] = G;
-        for (int i = 0; i < nt; i++) A.tiles[toff + i] = PfTile{ e, i * GM };
+        for (int i = 0; i < nt; i++) A.tiles[toff + i] = PfTile{ e, i * A.chunk };
     }
-    const int nsh = (A.T + GM - 1) / GM;
+    const int nsh = (A.T + A.chunk - 1) / A.chunk;
     if (e == 0) {
         PfGroup G;
         G.g = A.L.sgate; G.u = A.L.sup; G.d = A.L.sdown;
@@ -271,165 +287,7 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
         A.groups[A.E] = G;
         *A.ntiles = tot_tiles + nsh;
     }
-    for (int i = e; i < nsh; i += 256) A.tiles[tot_tiles + i] = PfTile{ A.E, i * GM };
-}
-
-/* ---- grouped GEMMs -------------------------------------------------------- */
-/* Virtual block id: blocks b < R = ntiles * nblk run; on a grid dispatched
- * round-robin over the 8 XCDs, XCD b % 8 takes the contiguous range of
- * virtual ids [(b % 8) * R / 8, ...), so the n-blocks of one tile and the
- * consecutive tiles of one expert share an L2. */
-__device__ __forceinline__ int pf_virtual_block(int b, int R)
-{
-    return (R & 7) ? b : (b & 7) * (R >> 3) + (b >> 3);
-}
-
-struct PfRowMeta {
-    const float *src[GM];
-    int slot[GM];
-    float inv[GM], fwd[GM];
-};
-
-template <int OP>
-__global__ void __launch_bounds__(GT) pf_gu_kernel(PfGemmArgs A)
-{
-    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-    __shared__ PfRowMeta meta;
-    const int nblk = A.I / 32;
-    const int R = *A.ntiles * nblk;
-    const int b = blockIdx.x;
-    if (b >= R) return;
-    const int v = pf_virtual_block(b, R);
-    const PfTile tile = A.tiles[v / nblk];
-    const int j0 = (v % nblk) * 32;
-    const PfGroup &G = A.groups[tile.grp];
-    const int t = threadIdx.x;
-    if (t < GM) {
-        const int a = tile.m0 + t;
-        if (a < G.n) {
-            const int tok = G.tok ? G.tok[a] : G.tok0 + a;
-            meta.src[t] = A.X + (size_t)tok * A.H;
-            meta.slot[t] = G.slot0 + a;
-            meta.inv[t] = A.xinv ? A.xinv[tok] : 1.0f;
-            meta.fwd[t] = A.xfwd ? A.xfwd[tok] : 1.0f;
-        } else {
-            meta.src[t] = nullptr;
-            meta.slot[t] = -1;
-            meta.inv[t] = 1.0f;
-            meta.fwd[t] = 1.0f;
-        }
-    }
-    uint16_t *Xh = smem, *Wh = smem + G_TILE_ELEMS;
-    uint16_t *Xl = smem + 2 * G_TILE_ELEMS, *Wl = smem + 3 * G_TILE_ELEMS;
-    /* weight row of this thread: tile rows 0..31 gate rows j0.., 32..63 up rows j0.. */
-    const int wr = t >> 2;
-    const bool is_up = wr >= 32;
-    const bool q6 = is_up ? G.uq6 : G.gq6;
-    const size_t bb = q6 ? RQ6K_BYTES : RQ4K_BYTES;
-    const int nkb = A.H / GK;
-    const uint8_t *wrow = (is_up ? G.u : G.g) + (size_t)(j0 + (wr & 31)) * nkb * bb;
-    __syncthreads();
-    const float *xsrc = meta.src[wr];
-    const float xinv = meta.inv[wr];
-    const int w = t >> 6, wm = w & 1, wn = w >> 1;
-    f32x16 acc = {};
-    for (int kb = 0; kb < nkb; kb++) {
-        if (kb) __syncthreads();
-        load_w_tile<OP>(wrow + kb * bb, q6, Wh, Wl);
-        load_x_tile<OP>(xsrc ? xsrc + kb * GK : nullptr, xinv, Xh, Xl);
-        __syncthreads();
-        mfma_tile<OP>(acc, Xh, Xl, Wh, Wl, wm, wn);
-    }
-    /* epilogue: gate / up blocks meet in LDS */
-    __syncthreads();
-    float *Cs = (float *)smem;                 /* [64][65] */
-    const int l = t & 63;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int m = 32 * wm + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
-        Cs[m * 65 + 32 * wn + (l & 31)] = acc[i];
-    }
-    __syncthreads();
-    const int m = t >> 2, q = t & 3;
-    const int slot = meta.slot[m];
-    const float fwd = meta.fwd[m];
-    float e8[8];
-    float mx = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float g = Cs[m * 65 + 8 * q + i] * fwd, u = Cs[m * 65 + 32 + 8 * q + i] * fwd;
-        e8[i] = pf_silu_mul(g, u);
-        mx = fmaxf(mx, fabsf(e8[i]));
-    }
-    if (slot >= 0) {
-        float4 *dst = (float4 *)(A.act + (size_t)slot * A.I + j0 + 8 * q);
-        dst[0] = make_float4(e8[0], e8[1], e8[2], e8[3]);
-        dst[1] = make_float4(e8[4], e8[5], e8[6], e8[7]);
-    }
-    if (A.amax) {
-        mx = fmaxf(mx, __shfl_xor(mx, 1));
-        mx = fmaxf(mx, __shfl_xor(mx, 2));
-        if (q == 0 && slot >= 0) atomicMax(A.amax + slot, __builtin_bit_cast(unsigned, mx));
-    }
-}
-
-template <int OP>
-__global__ void __launch_bounds__(GT) pf_down_kernel(PfGemmArgs A)
-{
-    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-    __shared__ PfRowMeta meta;
-    const int nblk = A.H / GN;
-    const int R = *A.ntiles * nblk;
-    const int b = blockIdx.x;
-    if (b >= R) return;
-    const int v = pf_virtual_block(b, R);
-    const PfTile tile = A.tiles[v / nblk];
-    const int n0 = (v % nblk) * GN;
-    const PfGroup &G = A.groups[tile.grp];
-    const int t = threadIdx.x;
-    if (t < GM) {
-        const int a = tile.m0 + t;
-        if (a < G.n) {
-            const int slot = G.slot0 + a;
-            meta.src[t] = A.act + (size_t)slot * A.I;
-            meta.slot[t] = slot;
-            float inv = 1.0f, fwd = 1.0f;
-            if (A.amax) row_scale(__builtin_bit_cast(float, A.amax[slot]), inv, fwd);
-            meta.inv[t] = inv;
-            meta.fwd[t] = fwd;
-        } else {
-            meta.src[t] = nullptr;
-            meta.slot[t] = -1;
-            meta.inv[t] = 1.0f;
-            meta.fwd[t] = 1.0f;
-        }
-    }
-    uint16_t *Xh = smem, *Wh = smem + G_TILE_ELEMS;
-    uint16_t *Xl = smem + 2 * G_TILE_ELEMS, *Wl = smem + 3 * G_TILE_ELEMS;
-    const int wr = t >> 2;
-    const bool q6 = G.dq6;
-    const size_t bb = q6 ? RQ6K_BYTES : RQ4K_BYTES;
-    const int nkb = A.I / GK;
-    const uint8_t *wrow = G.d + (size_t)(n0 + wr) * nkb * bb;
-    __syncthreads();
-    const float *xsrc = meta.src[wr];
-    const float xinv = meta.inv[wr];
-    const int w = t >> 6, wm = w & 1, wn = w >> 1;
-    f32x16 acc = {};
-    for (int kb = 0; kb < nkb; kb++) {
-        if (kb) __syncthreads();
-        load_w_tile<OP>(wrow + kb * bb, q6, Wh, Wl);
-        load_x_tile<OP>(xsrc ? xsrc + kb * GK : nullptr, xinv, Xh, Xl);
-        __syncthreads();
-        mfma_tile<OP>(acc, Xh, Xl, Wh, Wl, wm, wn);
-    }
-    const int l = t & 63;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int m = 32 * wm + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
-        const int slot = meta.slot[m];
-        if (slot >= 0) A.out[(size_t)slot * A.H + n0 + 32 * wn + (l & 31)] = acc[i] * meta.fwd[m];
-    }
+    for (int i = e; i < nsh; i += 256) A.tiles[tot_tiles + i] = PfTile{ A.E, i * A.chunk };
 }
 
 /* ---- combine -------------------------------------------------------------- */
@@ -484,27 +342,7 @@ extern "C" __global__ void __launch_bounds__(256) pf_combine_kernel(const float 
     }
 }
 
-/* ---- host ----------------------------------------------------------------- */
-template <int OP>
-static int launch_gemms(const PfGemmArgs &A, int max_tiles)
-{
-    RtState &R = rt();
-    const size_t lds = gemm_lds_bytes(OP);
-    const int gu_blocks = max_tiles * (A.I / 32), d_blocks = max_tiles * (A.H / GN);
-    hipLaunchKernelGGL(pf_gu_kernel<OP>, dim3(gu_blocks), dim3(GT), lds, R.stream, A);
-    if (rt_check(hipGetLastError(), "prefill gate/up launch")) return ROASTER_EDEVICE;
-    hipLaunchKernelGGL(pf_down_kernel<OP>, dim3(d_blocks), dim3(GT), lds, R.stream, A);
-    return rt_check(hipGetLastError(), "prefill down launch") ? ROASTER_EDEVICE : 0;
-}
-
-int pf_gemm_launch(const PfGemmArgs &A, int max_tiles, int op)
-{
-    if (max_tiles <= 0) return 0;
-    if (op == PF_F16) return launch_gemms<PF_F16>(A, max_tiles);
-    if (op == PF_SPLIT) return launch_gemms<PF_SPLIT>(A, max_tiles);
-    return launch_gemms<PF_BF16>(A, max_tiles);
-}
-
+/* ---- host ---------------------------------------------------------------- */
 static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, int T, float *Y,
@@ -523,7 +361,8 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     if (E > 256) return rt_fail(ROASTER_EINVAL, "roaster_moe_prefill: at most 256 routed experts");
     const int op = opt.precision == ROASTER_PREC_F16 ? PF_F16 : opt.precision == ROASTER_PREC_SPLIT ? PF_SPLIT : PF_BF16;
     const size_t TT = (size_t)T, slots = 9 * TT;
-    const int max_tiles = (int)((8 * TT + GM - 1) / GM + E + (TT + GM - 1) / GM);
+    const int chunk = pf_gemm_chunk(op);
+    const int max_tiles = (int)((8 * TT + chunk - 1) / chunk + E + (TT + chunk - 1) / chunk);
 
     /* workspace */
     size_t sz = 0;
@@ -531,6 +370,7 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     const size_t o_part = opt.logits_in ? 0 : take((size_t)RT_KSPLIT * TT * E * 4);
     const size_t o_ids = take(TT * 8 * 4), o_w = take(TT * 8 * 4), o_rank = take(TT * 8 * 4);
     const size_t o_sg = take(TT * 4), o_xinv = take(TT * 4), o_xfwd = take(TT * 4);
+    const size_t o_x16 = op == PF_F16 ? take(TT * H * 2) : 0;
     const size_t o_cnt = take((size_t)E * 4), o_off = take((size_t)E * 4), o_list = take((size_t)E * TT * 4);
     const size_t o_grp = take(sizeof(PfGroup) * (E + 1)), o_tiles = take(sizeof(PfTile) * max_tiles);
     const size_t o_nt = take(4), o_amax = take(slots * 4);
@@ -560,6 +400,7 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     ta.sg = (float *)(ws + o_sg);
     ta.xinv = op == PF_F16 ? (float *)(ws + o_xinv) : nullptr;
     ta.xfwd = op == PF_F16 ? (float *)(ws + o_xfwd) : nullptr;
+    ta.x16 = op == PF_F16 ? (uint16_t *)(ws + o_x16) : nullptr;
     ta.amax = op == PF_F16 ? (unsigned *)(ws + o_amax) : nullptr;
     ta.err = (int *)(ctrl + 16);
     ta.T = T; ta.E = E; ta.H = H;
@@ -583,6 +424,7 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     pa.tiles = (PfTile *)(ws + o_tiles);
     pa.ntiles = (int *)(ws + o_nt);
     pa.T = T; pa.E = E;
+    pa.chunk = chunk;
     hipLaunchKernelGGL(pf_plan_kernel, dim3(1), dim3(256), 0, R.stream, pa);
     if (rt_check(hipGetLastError(), "prefill plan launch")) return ROASTER_EDEVICE;
 
@@ -591,6 +433,7 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     ga.tiles = pa.tiles;
     ga.ntiles = pa.ntiles;
     ga.X = X;
+    ga.X16 = ta.x16;
     ga.xinv = ta.xinv;
     ga.xfwd = ta.xfwd;
     ga.act = (float *)(ws + o_act);

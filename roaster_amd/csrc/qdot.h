@@ -29,6 +29,40 @@
 struct __attribute__((packed, aligned(2))) u32x4_a2 { uint32_t x, y, z, w; };
 struct __attribute__((packed, aligned(2))) u32x2_a2 { uint32_t x, y; };
 
+/* Global-memory loads.  Weight pointers read out of device-side tables have no
+ * provable address space, so plain dereferences compile to flat loads, and a
+ * flat load also holds the LDS wait counter: every later LDS wait would then
+ * wait for the weight fetch too.  These helpers load through address space 1
+ * (global) explicitly; the pointer must point into device memory. */
+#define GAS __attribute__((address_space(1)))
+typedef uint32_t gu32x4 __attribute__((ext_vector_type(4)));
+typedef gu32x4 __attribute__((aligned(2))) gu32x4_a2;
+typedef uint32_t gu32x2 __attribute__((ext_vector_type(2)));
+typedef gu32x2 __attribute__((aligned(2))) gu32x2_a2;
+typedef float gf32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 gld_u4(const void *p)          /* 16-byte aligned */
+{
+    const gu32x4 v = *(const GAS gu32x4 *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 gld_u4a2(const void *p)        /* 2-byte aligned */
+{
+    const gu32x4 v = *(const GAS gu32x4_a2 *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 gld_u2a2(const void *p)
+{
+    const gu32x2 v = *(const GAS gu32x2_a2 *)p;
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t gld_u16(const void *p) { return *(const GAS uint16_t *)p; }
+__device__ __forceinline__ float4 gld_f4(const void *p)
+{
+    const gf32x4 v = *(const GAS gf32x4 *)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 /* Raw bytes of one lane's share of a super-block. */
 struct QChunk {
     uint4 q;       /* Q4_K: qs bytes;  Q6_K: ql bytes */
@@ -50,19 +84,16 @@ __device__ __forceinline__ QChunk q_load(const uint8_t *blk, int c)
 {
     QChunk ch;
     if (!q6) {
-        ch.h = *(const uint4 *)blk;                     /* 144-byte blocks are 16-byte aligned */
-        ch.q = *(const uint4 *)(blk + 16 + 16 * c);
+        ch.h = gld_u4(blk);                             /* 144-byte blocks are 16-byte aligned */
+        ch.q = gld_u4(blk + 16 + 16 * c);
         ch.s = make_uint2(0, 0);
         ch.dd = 0;
     } else {
         const int n = c >> 2, p = c & 3;
-        u32x4_a2 ql = *(const u32x4_a2 *)(blk + 16 * c);
-        u32x4_a2 qh = *(const u32x4_a2 *)(blk + 128 + 32 * n + 16 * (p & 1));
-        u32x2_a2 sc = *(const u32x2_a2 *)(blk + 192 + 8 * n);
-        ch.q = make_uint4(ql.x, ql.y, ql.z, ql.w);
-        ch.h = make_uint4(qh.x, qh.y, qh.z, qh.w);
-        ch.s = make_uint2(sc.x, sc.y);
-        ch.dd = *(const uint16_t *)(blk + 208);
+        ch.q = gld_u4a2(blk + 16 * c);
+        ch.h = gld_u4a2(blk + 128 + 32 * n + 16 * (p & 1));
+        ch.s = gld_u2a2(blk + 192 + 8 * n);
+        ch.dd = gld_u16(blk + 208);
     }
     return ch;
 }
@@ -216,6 +247,18 @@ __device__ __forceinline__ float group_sum(float v)
     }
     if (W == 64) v = (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
     return v;
+}
+
+/* Maximum of v over each 32-lane half of the wave: lo = lanes 0..31, hi =
+ * lanes 32..63 (wave-uniform results). */
+__device__ __forceinline__ void half_max(float v, float &lo, float &hi)
+{
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    lo = fmaxf(lane_f(v, 0), lane_f(v, 16));
+    hi = fmaxf(lane_f(v, 32), lane_f(v, 48));
 }
 
 /* Runtime group width (8, 16, 32 or 64). */
