@@ -4,13 +4,19 @@ Headline (value): batch-1 decode through the 40-layer MoE-FFN stack -- hidden
 2048, 256 routed experts (top-8) + 1 shared expert per layer, gate/up Q4_K
 [512 x 2048], down Q6_K [2048 x 512], F32 router, RMSNorm (eps 1e-6) carried
 between layers -- with every expert resident in HBM (21.05 GB).  A step is one
-token through all 40 layers (one launch).  Inputs and weights are synthetic
-(seeded) and already in HBM when timing starts.
+token through all 40 layers (one library call, 3 kernels per layer).  Inputs
+and weights are synthetic (seeded) and already in HBM when timing starts.
 
-Also reported: batch-8 decode (8 slots, one token each) and the roofline of the
-decode kernel (algorithmic bytes / average kernel time from HIP events on the
-library's stream), plus the reference's CPU path (its own AVX2 kernels,
-compiled from the reference tree into oracle/_ref) timed on this host.
+Also reported in the same JSON line:
+  batch8   -- 8 slots, one token each, through the same stack;
+  prefill  -- the MoE block over T tokens: 2048 tokens through 4 all-Q6_K
+              layers with N(0,1) logits given (the MFMA roofline line), and 512
+              tokens through one Q4_K/Q6_K layer with the router and a
+              Zipf(1.1) per-expert logit bias;
+  roofline / cpu_baseline -- see below.
+Kernel times come from HIP events recorded on the library's stream.  The CPU
+baselines run the reference's own C kernels (compiled from the reference tree
+into oracle/_ref) on a bounded sample of the same workloads on this host.
 """
 import argparse
 import ctypes as C
@@ -25,11 +31,15 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0          # dense fp16 / bf16
 N_LAYERS, E, H, I = 40, 256, 2048, 512
 Q4_MAT = I * (H // 256) * 144          # 589,824
 Q6_MAT = H * (I // 256) * 210          # 860,160
+Q6_GU = I * (H // 256) * 210           # 860,160 (all-Q6_K gate / up)
 EXPERT_BYTES = 2 * Q4_MAT + Q6_MAT     # 2,039,808
+EXPERT_BYTES_Q6 = 3 * Q6_GU            # 2,580,480
 ROUTER_BYTES = E * H * 4 + H * 4       # router + shared-gate vector
+FFN_FLOPS_PER_ROW = 6 * H * I          # gate + up + down per (token, expert) row
 
 
 def decode_bytes(ids):
@@ -48,9 +58,27 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--batch", type=int, default=1)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-tokens", type=int, default=40)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill legs")
+    ap.add_argument("--cpu-tokens", type=int, default=160)
+    ap.add_argument("--prefill-reps", type=int, default=10)
     return ap.parse_args()
+
+
+def bf16_round(a):
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def zipf_bias(n, seed, s=1.1, tau=0.3):
+    """tau * ln(p_e), p_e proportional to rank_e^-s, ranks permuted by seed."""
+    perm = np.random.default_rng(seed).permutation(n)
+    rank = np.empty(n, np.float64)
+    rank[perm] = np.arange(1, n + 1)
+    p = rank ** -s
+    p /= p.sum()
+    return (tau * np.log(p)).astype(np.float32)
 
 
 def fetch_expert(R, table, seed, layer, e, desc):
@@ -59,29 +87,34 @@ def fetch_expert(R, table, seed, layer, e, desc):
     L = R.lib()
     ptrs = [C.c_void_p() for _ in range(3)]
     R.check(L.roaster_table_expert_ptrs(table, layer, e, *[C.byref(p) for p in ptrs]))
+    sizes = [R.matrix_bytes(desc.q6[0] if e < desc.n_experts else desc.sh_q6[0], desc.inter, desc.hidden),
+             R.matrix_bytes(desc.q6[1] if e < desc.n_experts else desc.sh_q6[1], desc.inter, desc.hidden),
+             R.matrix_bytes(desc.q6[2] if e < desc.n_experts else desc.sh_q6[2], desc.hidden, desc.inter)]
     out = []
-    for p, n in zip(ptrs, (Q4_MAT, Q4_MAT, Q6_MAT)):
+    for p, n in zip(ptrs, sizes):
         a = np.empty(n, np.uint8)
         R.check(L.roaster_d2h(a.ctypes.data, p.value, n))
         out.append(a)
     return out
 
 
-def cpu_baseline(table_seed, n_tokens, table=None):
+def omp_threads():
+    try:
+        return int(C.CDLL("libgomp.so.1").omp_get_max_threads())
+    except OSError:
+        return int(os.environ.get("OMP_NUM_THREADS", "1"))
+
+
+def cpu_baseline_decode(table_seed, n_tokens, table=None):
     """The reference's CPU decode path (kernels.c AVX2 kernels via oracle/_ref,
     composed as model.c:1059-1146 does, one thread as the reference's OpenMP
     thresholds keep it) on a bounded sample: n_tokens tokens through all 40
-    layers.  Expert bytes are copied from the device table (or regenerated on
-    the host) outside the timed region."""
+    layers.  Expert bytes are copied from the device table outside the timed
+    region."""
     import roaster_amd as R
     from oracle import oracle as O
-    kind = "reference"
-    if not O.ref_available():
-        kind = "port"
+    kind = "reference" if O.ref_available() else "port"
     desc = R.table_desc(N_LAYERS)
-    libm = C.CDLL("libm.so.6")
-    libm.expf.restype = C.c_float
-    libm.expf.argtypes = [C.c_float]
     ones = np.ones(H, np.float32)
     routers = {}
     total = 0.0
@@ -135,11 +168,149 @@ def cpu_baseline(table_seed, n_tokens, table=None):
                       f"8+1 experts, combine; {total:.2f} s of CPU work), same table seed"}
 
 
+def cpu_baseline_prefill(table, desc, seed, X, bias, ids, reps=2):
+    """The reference's CPU prefill block (model.c:1671-1791 composition over
+    its kernels.c routines via oracle/_ref: router matvec per token, moe_cpu
+    over the expert row groups -- OpenMP-parallel as kernels.c:1882 is -- and
+    moe_cpu for the shared expert) on the 512-token Zipf layer, with the
+    GPU's routing.  Gathers and the combine are outside the timed region."""
+    import roaster_amd as R
+    from oracle import oracle as O
+    if not O.ref_available():
+        return None
+    Rf = O.ref()
+    T = X.shape[0]
+    router, gi = R.host_router(seed, 0, desc)
+    mats = {e: fetch_expert(R, table, seed, 0, e, desc) for e in range(E + 1)}
+    groups = []
+    for e in range(E):
+        rows = np.nonzero((ids == e).any(axis=1))[0]
+        if len(rows):
+            groups.append((e, rows))
+    n_tot = sum(len(r) for _, r in groups)
+    Xg = np.ascontiguousarray(np.concatenate([X[r] for _, r in groups]))
+    Dg = np.empty((n_tot, H), np.float32)
+    exs = (R.KernelMoeExpert * len(groups))()
+    for i, (e, rows) in enumerate(groups):
+        g, u, d = mats[e]
+        exs[i] = R.KernelMoeExpert(g.ctypes.data, u.ctypes.data, d.ctypes.data, desc.q6[0], desc.q6[1], desc.q6[2], len(rows))
+    sh = (R.KernelMoeExpert * 1)()
+    g, u, d = mats[E]
+    sh[0] = R.KernelMoeExpert(g.ctypes.data, u.ctypes.data, d.ctypes.data, desc.sh_q6[0], desc.sh_q6[1], desc.sh_q6[2], T)
+    Ds = np.empty((T, H), np.float32)
+    lg = np.empty(E, np.float32)
+    best = None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for t in range(T):
+            Rf.kernel_matvec_f32(router.ctypes.data, X[t].ctypes.data, lg.ctypes.data, E, H)
+        Rf.ref_moe_cpu(C.cast(sh, C.c_void_p), 1, X.ctypes.data, Ds.ctypes.data, I, H)
+        Rf.ref_moe_cpu(C.cast(exs, C.c_void_p), len(groups), Xg.ctypes.data, Dg.ctypes.data, I, H)
+        dt = time.perf_counter() - t0
+        best = dt if best is None else min(best, dt)
+    return {"value": round(T / best, 1), "unit": "tokens/s", "cores": omp_threads(), "kind": "reference",
+            "sample": f"one {T}-token Zipf-routed Q4_K/Q6_K layer (router + {len(groups)} expert groups + shared "
+                      f"expert via the reference moe_cpu), best of {reps}: {best:.3f} s"}
+
+
+def event_ms(torch, stream, fn, reps):
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        fn()
+    b.record(stream)
+    b.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def prefill_legs(torch, L, R, dev, stream, reps, with_cpu):
+    out = {}
+    # all-Q6_K, T = 2048, 4 layers, N(0,1) logits given (no router)
+    T, NL, seed = 2048, 4, 4
+    desc = R.table_desc(NL, q6=(1, 1, 1), sh_q6=(1, 1, 1))
+    t = L.roaster_table_create(C.byref(desc))
+    assert t, R.last_error()
+    try:
+        R.check(L.roaster_table_synth(t, seed, None), "table_synth")
+        X = torch.from_numpy(bf16_round(np.stack([R.synth_normal(seed, R.synth_stream(0, i, 5), H)
+                                                  for i in range(T)]))).to(dev)
+        lg = [torch.from_numpy(np.stack([R.synth_normal(seed, R.synth_stream(l, i, 7), E) for i in range(T)])).to(dev)
+              for l in range(NL)]
+        Y = torch.empty_like(X)
+        cnt = torch.empty((NL, E), dtype=torch.int32, device=dev)
+        torch.cuda.synchronize()
+        opts = [R.RoasterPrefillOpts(R.PREC_F16, lg[l].data_ptr(), None, None, None, None, cnt[l].data_ptr())
+                for l in range(NL)]
+
+        def run():
+            for l in range(NL):
+                rc = L.roaster_moe_prefill(t, l, X.data_ptr(), T, Y.data_ptr(), C.byref(opts[l]))
+                if rc:
+                    raise RuntimeError(R.last_error())
+
+        run()
+        R.check(L.roaster_sync(), "prefill warmup")
+        ms = event_ms(torch, stream, run, reps)
+        R.check(L.roaster_sync(), "prefill")
+        counts = cnt.cpu().numpy()
+        rows = int(counts.sum()) + NL * T                     # routed rows + shared rows
+        flops = rows * FFN_FLOPS_PER_ROW
+        nbytes = NL * ((int((counts > 0).sum(axis=1).mean()) + 1) * EXPERT_BYTES_Q6) + NL * (T * H * 4 * 2 + T * E * 4)
+        tf = flops / (ms * 1e-3) / 1e12
+        out["all_q6k_2048x4"] = {
+            "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_pass": round(ms, 4), "layers": NL,
+            "ms_per_layer": round(ms / NL, 4), "precision": "fp16 operands (row-scaled), fp32 accumulate",
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                         "kernel": "whole prefill block (7 kernels per layer)",
+                         "algorithmic_flops_per_layer": int(flops // NL)},
+            "hbm_GBps_algorithmic": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    finally:
+        L.roaster_table_destroy(t)
+    # Q4_K/Q6_K, T = 512, router + Zipf bias, one layer
+    T, seed = 512, 2
+    desc = R.table_desc(1)
+    t = L.roaster_table_create(C.byref(desc))
+    assert t, R.last_error()
+    try:
+        R.check(L.roaster_table_synth(t, seed, None), "table_synth")
+        Xh = bf16_round(np.stack([R.synth_normal(seed, R.synth_stream(0, i, 5), H) for i in range(T)]))
+        X = torch.from_numpy(Xh).to(dev)
+        bias = torch.from_numpy(zipf_bias(E, seed)).to(dev)
+        Y = torch.empty_like(X)
+        ids = torch.empty((T, 8), dtype=torch.int32, device=dev)
+        torch.cuda.synchronize()
+        o = R.RoasterPrefillOpts(R.PREC_F16, None, bias.data_ptr(), None, ids.data_ptr(), None, None)
+
+        def run3():
+            rc = L.roaster_moe_prefill(t, 0, X.data_ptr(), T, Y.data_ptr(), C.byref(o))
+            if rc:
+                raise RuntimeError(R.last_error())
+
+        run3()
+        R.check(L.roaster_sync(), "prefill warmup")
+        ms = event_ms(torch, stream, run3, reps)
+        R.check(L.roaster_sync(), "prefill")
+        flops = 9 * T * FFN_FLOPS_PER_ROW + T * (E + 1) * H * 2
+        tf = flops / (ms * 1e-3) / 1e12
+        leg = {"tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_layer": round(ms, 4),
+               "achieved_TFLOPs": round(tf, 2), "frac_mfma_peak": round(tf / MFMA_PEAK_TFLOPS, 4)}
+        if with_cpu:
+            cb = cpu_baseline_prefill(t, desc, seed, Xh, zipf_bias(E, seed), ids.cpu().numpy())
+            if cb:
+                leg["cpu_baseline"] = cb
+        out["zipf_512x1"] = leg
+    finally:
+        L.roaster_table_destroy(t)
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU: the MoE-FFN hot path is measured "
-                                   "on one MI355X; see DESIGN.md for how it would shard"}))
+                                   "on one MI355X; DESIGN.md describes how it would shard"}))
         sys.exit(2)
     import torch
     import roaster_amd as R
@@ -147,52 +318,42 @@ def main():
     L = R.lib()
     dev = torch.device("cuda:0")
     torch.cuda.init()
-    B = args.batch
     seed = 3
     desc = R.table_desc(N_LAYERS)
     t = L.roaster_table_create(C.byref(desc))
     assert t, R.last_error()
     R.check(L.roaster_table_synth(t, seed, None), "table_synth")
     stream = torch.cuda.ExternalStream(L.roaster_stream(), device=dev)
-    h0 = torch.from_numpy(np.stack([R.synth_normal(seed, R.synth_stream(0, b, 5), H) for b in range(B)])).to(dev)
-    h = torch.empty_like(h0)
-    ids = torch.empty((N_LAYERS, B, 8), dtype=torch.int32, device=dev)
-    torch.cuda.synchronize()
 
-    def step():
+    def stack_setup(B):
+        h0 = torch.from_numpy(np.stack([R.synth_normal(seed, R.synth_stream(0, b, 5), H) for b in range(B)])).to(dev)
+        return h0, torch.empty_like(h0), torch.empty((N_LAYERS, B, 8), dtype=torch.int32, device=dev)
+
+    def stack_step(B, h0, h, ids):
         with torch.cuda.stream(stream):
             h.copy_(h0)
-        rc = L.roaster_moe_decode_stack(t, h.data_ptr(), B, 0, N_LAYERS, None, C.c_float(1e-6),
-                                        ids.data_ptr(), None)
+        rc = L.roaster_moe_decode_stack(t, h.data_ptr(), B, 0, N_LAYERS, None, C.c_float(1e-6), ids.data_ptr(), None)
         if rc:
             raise RuntimeError(R.last_error())
 
+    B = args.batch
+    h0, h, ids = stack_setup(B)
+    torch.cuda.synchronize()
     for _ in range(args.warmup):
-        step()
+        stack_step(B, h0, h, ids)
     R.check(L.roaster_sync(), "warmup")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        stack_step(B, h0, h, ids)
     R.check(L.roaster_sync(), "timed steps")
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
 
-    # kernel-only duration with HIP events on the library's stream
-    nev = min(args.steps, 50)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nev)]
-    for a, b in evs:
-        with torch.cuda.stream(stream):
-            h.copy_(h0)
-            a.record(stream)
-        rc = L.roaster_moe_decode_stack(t, h.data_ptr(), B, 0, N_LAYERS, None, C.c_float(1e-6), ids.data_ptr(), None)
-        assert rc == 0
-        with torch.cuda.stream(stream):
-            b.record(stream)
+    # device time per step with HIP events on the library's stream
+    kern_ms = event_ms(torch, stream, lambda: stack_step(B, h0, h, ids), min(args.steps, 50))
     R.check(L.roaster_sync(), "event steps")
-    kern_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
-    ids_np = ids.cpu().numpy()
-    nbytes = decode_bytes(ids_np)
+    nbytes = decode_bytes(ids.cpu().numpy())
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
 
     ms = elapsed / args.steps * 1e3
@@ -214,12 +375,25 @@ def main():
                    "gate_up": "Q4_K", "down": "Q6_K", "resident_table_bytes": int(L.roaster_table_bytes(t))},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "moe_decode_kernel", "kernel_ms": round(kern_ms, 5),
-                     "algorithmic_bytes_per_launch": int(nbytes)},
+                     "kernel": "decode stack (router, gate/up, down kernels x 40 layers)",
+                     "kernel_ms": round(kern_ms, 5), "algorithmic_bytes_per_launch": int(nbytes)},
     }
+    if B == 1:
+        h8_0, h8, ids8 = stack_setup(8)
+        for _ in range(3):
+            stack_step(8, h8_0, h8, ids8)
+        R.check(L.roaster_sync(), "batch8 warmup")
+        ms8 = event_ms(torch, stream, lambda: stack_step(8, h8_0, h8, ids8), 20)
+        R.check(L.roaster_sync(), "batch8")
+        b8 = decode_bytes(ids8.cpu().numpy())
+        line["batch8"] = {"tokens_per_s": round(8 / (ms8 * 1e-3), 1), "ms_per_step": round(ms8, 4),
+                          "hbm_GBps": round(b8 / (ms8 * 1e-3) / 1e9, 1),
+                          "frac_hbm_peak": round(b8 / (ms8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(seed, args.cpu_tokens, t)
+        line["cpu_baseline"] = cpu_baseline_decode(seed, args.cpu_tokens, t)
     L.roaster_table_destroy(t)
+    if not args.no_prefill:
+        line["prefill"] = prefill_legs(torch, L, R, dev, stream, args.prefill_reps, not args.no_cpu)
     print(json.dumps(line), flush=True)
 
 
