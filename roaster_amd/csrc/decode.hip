@@ -36,9 +36,13 @@
 
 #define DT 256                        /* threads per workgroup */
 #define DW (DT / 64)                  /* waves per workgroup */
+#ifndef GU_PF
 #define GU_PF 2                       /* tasks in flight per wave */
+#endif
 #define D_ROWS 4                      /* output rows per down workgroup */
+#ifndef D_PF
 #define D_PF 4                        /* down tasks in flight per wave */
+#endif
 
 /* Opt-in phase tracing (build with -DROASTER_PHASE_TS): thread 0 of every
  * workgroup records the 100 MHz real-time counter at phase boundaries;
@@ -237,14 +241,14 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A,
 
 /* Active-expert plan: union of the tokens' experts in first-appearance order
  * over (t, k), then the shared expert.  Pair p = t*9 + k (k = 8: shared).
- * emask: 256 x 64-bit LDS scratch; sk: 16 x 64-bit per wave. */
+ * emask: 256 x 64-bit LDS scratch. */
 __device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, const float (*lg4)[4], float sg,
-                           unsigned long long *emask, unsigned long long (*sk)[16])
+                           unsigned long long *emask)
 {
     const int B = A.B, E = A.E, tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
     if (tid == 0) P.err = 0;
     __syncthreads();
-    for (int t = wv, r = 0; t < B; t += DW, r++) topk8_wave(lg4[r], E, P.ids[t], P.w[t], &P.err, sk[wv]);
+    for (int t = wv, r = 0; t < B; t += DW, r++) topk8_wave(lg4[r], E, P.ids[t], P.w[t], &P.err);
     if (tid < B) P.w[tid][8] = 1.0f / (1.0f + expf(-sg));
     __syncthreads();
     PHASE_TS(1, 4);
@@ -382,7 +386,6 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int
     __shared__ float red[DW][RMAX_B];
     __shared__ float inv_rms[RMAX_B];
     __shared__ unsigned long long emask[256];
-    __shared__ unsigned long long sk[DW][16];
     const int I = A.I, B = A.B, E = A.E;
     float *xn = lds, *xsum = lds + B * A.H;
     PHASE_TS(1, 0);
@@ -406,7 +409,7 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int
         block_copy16(xn, A.xn_g, B * (A.H + A.H / 16) / 4);
         __syncthreads();
         PHASE_TS(1, 1);
-        build_plan(A, L, P, lg4, sg, emask, sk);
+        build_plan(A, L, P, lg4, sg, emask);
     }
     PHASE_TS(1, 2);
     if (blockIdx.x == 0) {

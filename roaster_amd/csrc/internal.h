@@ -18,6 +18,11 @@
 #define RQ6K_BYTES 210
 #define RTOPK 8
 #define RMAX_B 8                 /* decode tokens per call */
+/* Every device allocation that kernels read weights or activations from carries
+ * this many spare bytes: the prefill GEMM loads whole 16-byte-aligned windows
+ * around each 210-byte Q6_K block, which can reach up to 14 bytes past a
+ * matrix's last block (80 past a Q4_K block). */
+#define RT_TAIL_PAD 256
 
 static inline size_t rq_block_bytes(int q6) { return q6 ? RQ6K_BYTES : RQ4K_BYTES; }
 static inline size_t rq_row_bytes(int q6, size_t cols) { return cols / RQK * rq_block_bytes(q6); }

@@ -114,22 +114,15 @@ __global__ void __launch_bounds__(GT) pf_gu_kernel(PfGemmArgs A)
     const int slot = meta.slot[m];
     const float fwd = meta.fwd[m];
     float e8[8];
-    float mx = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const float g = Cs[m * 65 + 8 * q + i] * fwd, u = Cs[m * 65 + 32 + 8 * q + i] * fwd;
         e8[i] = pf_silu_mul(g, u);
-        mx = fmaxf(mx, fabsf(e8[i]));
     }
     if (slot >= 0) {
         float4 *dst = (float4 *)(A.act + (size_t)slot * A.I + j0 + 8 * q);
         dst[0] = make_float4(e8[0], e8[1], e8[2], e8[3]);
         dst[1] = make_float4(e8[4], e8[5], e8[6], e8[7]);
-    }
-    if (A.amax) {
-        mx = fmaxf(mx, __shfl_xor(mx, 1));
-        mx = fmaxf(mx, __shfl_xor(mx, 2));
-        if (q == 0 && slot >= 0) atomicMax(A.amax + slot, __builtin_bit_cast(unsigned, mx));
     }
 }
 
@@ -153,10 +146,8 @@ __global__ void __launch_bounds__(GT) pf_down_kernel(PfGemmArgs A)
             const int slot = G.slot0 + a;
             meta.src[t] = A.act + (size_t)slot * A.I;
             meta.slot[t] = slot;
-            float inv = 1.0f, fwd = 1.0f;
-            if (A.amax) row_scale(__builtin_bit_cast(float, A.amax[slot]), inv, fwd);
-            meta.inv[t] = inv;
-            meta.fwd[t] = fwd;
+            meta.inv[t] = 1.0f;
+            meta.fwd[t] = 1.0f;
         } else {
             meta.src[t] = nullptr;
             meta.slot[t] = -1;
@@ -194,10 +185,10 @@ __global__ void __launch_bounds__(GT) pf_down_kernel(PfGemmArgs A)
 
 
 /* ---- v2 ------------------------------------------------------------------- */
-#define V2_T 256                  /* threads */
-#define V2_W 4                    /* waves */
-#define V2_GU_J (32 * V2_W)       /* gate/up j columns per workgroup */
-#define V2_DN_N (64 * V2_W)       /* down output rows per workgroup */
+#define V2_T 512                  /* threads */
+#define V2_W 8                    /* waves */
+#define V2_GU_J (16 * V2_W)       /* gate/up j columns per workgroup */
+#define V2_DN_N (32 * V2_W)       /* down output rows per workgroup */
 #define V2_MC 96                  /* rows per tile */
 #define V2_LD (GK + 8)            /* LDS row stride (fp16 elements) */
 
@@ -209,34 +200,6 @@ struct RawQ4 { uint32_t hd[4], Q[16]; };
 template <bool Q6> struct RawOf;
 template <> struct RawOf<true> { typedef RawQ6 T; };
 template <> struct RawOf<false> { typedef RawQ4 T; };
-
-__device__ __forceinline__ void raw_load(RawQ6 &r, const uint8_t *blk, int h)
-{
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint4 v = gld_u4a2(blk + 64 * h + 16 * i);
-        r.L[4 * i] = v.x; r.L[4 * i + 1] = v.y; r.L[4 * i + 2] = v.z; r.L[4 * i + 3] = v.w;
-    }
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const uint4 v = gld_u4a2(blk + 128 + 32 * h + 16 * i);
-        r.Hh[4 * i] = v.x; r.Hh[4 * i + 1] = v.y; r.Hh[4 * i + 2] = v.z; r.Hh[4 * i + 3] = v.w;
-    }
-    const uint2 s = gld_u2a2(blk + 192 + 8 * h);
-    r.S[0] = s.x; r.S[1] = s.y;
-    r.d = gld_u16(blk + 208);
-}
-
-__device__ __forceinline__ void raw_load(RawQ4 &r, const uint8_t *blk, int h)
-{
-    const uint4 hd = gld_u4(blk);
-    r.hd[0] = hd.x; r.hd[1] = hd.y; r.hd[2] = hd.z; r.hd[3] = hd.w;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint4 v = gld_u4(blk + 16 + 64 * h + 16 * i);
-        r.Q[4 * i] = v.x; r.Q[4 * i + 1] = v.y; r.Q[4 * i + 2] = v.z; r.Q[4 * i + 3] = v.w;
-    }
-}
 
 /* Per super-block constants of one lane's half. */
 struct ConstQ6 { f16x2 sc[8], bias[8], d; };   /* sc[s] = (S[s], S[s]), bias = -1056 sc */
@@ -333,53 +296,159 @@ __device__ __forceinline__ int perm_slot4(int p)
     return (8 * hi + (l0 >> 2)) * 16 + 8 * h + i0;
 }
 
-struct V2Meta {
+
+/* ---- v2 workgroup: 8 waves, two per SIMD -------------------------------------
+ * Each wave owns one 32-row MFMA column block of weights: for gate/up, lanes
+ * n = 0..15 hold gate row j0 + 16w + n and lanes 16..31 the up row of the same
+ * column, so SiLU(gate) * up pairs lane n with lane n + 16 in the epilogue; for
+ * down, output rows n0 + 32w + n.  Two waves per SIMD let one wave's dequant
+ * VALU work run under the other's MFMAs.
+ *
+ * Per K step (one super-block): the 256 weight rows' blocks arrive in LDS by
+ * direct global->LDS loads of the 16-byte-aligned 224-byte window around each
+ * block (consecutive lanes on consecutive 16-byte pieces, so each load
+ * instruction covers one contiguous kilobyte); every lane copies its own row's
+ * dwords out of the window, realigned with v_alignbyte_b32 (a block starts
+ * a = addr % 16 <= 14 bytes into its window; 14 + 210 <= 224).  Activations
+ * (MS x 32 rows x 256 fp16, permuted K order) are double-buffered in LDS
+ * through registers.  Sequence per step: raw dwords LDS -> registers;
+ * barrier; issue next step's window loads and activation loads; MFMA work;
+ * store the activations; wait for the windows; barrier. */
+#define V3_CH 224                          /* LDS bytes per staged window */
+#define V3_NP 14                           /* 16-byte pieces per window */
+#define V3_NCH (32 * V2_W)                 /* weight rows (windows) per workgroup */
+#define V3_WBYTES (V3_NCH * V3_CH + 16)    /* + one dword of read-ahead after the last window */
+#define V3_PPT (V3_NCH * V3_NP / V2_T)     /* window pieces per thread */
+#define V3_XBUF (V2_MC * V2_LD)            /* fp16 elements per activation buffer */
+
+static_assert(V3_NCH * V3_NP % V2_T == 0, "window pieces split evenly over the threads");
+
+#define AS1 __attribute__((address_space(1)))
+#define AS3 __attribute__((address_space(3)))
+
+__device__ __forceinline__ uint32_t lds_al(const uint32_t *p, int i, int sh)
+{
+    return __builtin_amdgcn_alignbyte(p[i + 1], p[i], sh);
+}
+
+__device__ __forceinline__ void raw_from_lds(RawQ6 &r, const uint32_t *p, int sh, int h)
+{
+#pragma unroll
+    for (int j = 0; j < 16; j++) r.L[j] = lds_al(p, 16 * h + j, sh);
+#pragma unroll
+    for (int j = 0; j < 8; j++) r.Hh[j] = lds_al(p, 32 + 8 * h + j, sh);
+    r.S[0] = lds_al(p, 48 + 2 * h, sh);
+    r.S[1] = lds_al(p, 49 + 2 * h, sh);
+    r.d = lds_al(p, 52, sh) & 0xFFFFu;
+}
+
+__device__ __forceinline__ void raw_from_lds(RawQ4 &r, const uint32_t *p, int sh, int h)
+{
+#pragma unroll
+    for (int k = 0; k < 4; k++) r.hd[k] = lds_al(p, k, sh);
+#pragma unroll
+    for (int j = 0; j < 16; j++) r.Q[j] = lds_al(p, 4 + 16 * h + j, sh);
+}
+
+/* MFMA work of one K step: MS row blocks x this wave's 32 weight columns; the
+ * two accumulators per row block take k-slices j and j + 8 (independent
+ * chains).  Xs: activation buffer, row stride V2_LD. */
+template <int MS, bool Q6>
+__device__ __forceinline__ void v4_mfma(f32x16 (&acc)[MS][2], const _Float16 *Xs, const typename RawOf<Q6>::T &r,
+                                        int h)
+{
+    typename ConstOf<Q6>::T c;
+    raw_consts(r, h, c);
+    const int l = threadIdx.x & 63;
+    const _Float16 *xa = Xs + (l & 31) * V2_LD + 8 * (l >> 5);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        f16x8 b0, b1;
+        dequant_pair(r, c, j, b0, b1);
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++) {
+            const f16x8 x0 = *(const f16x8 *)(xa + ms * 32 * V2_LD + 16 * j);
+            const f16x8 x1 = *(const f16x8 *)(xa + ms * 32 * V2_LD + 16 * (j + 8));
+            acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, b0, acc[ms][0], 0, 0, 0);
+            acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, b1, acc[ms][1], 0, 0, 0);
+        }
+    }
+}
+
+/* Issue the direct global->LDS loads of K step kb's windows.  Thread t covers
+ * pieces p = t + i * V2_T; piece p is window p / 14, 16-byte piece p % 14, and
+ * lands at LDS byte 16 p (the lanes of one load instruction cover 64
+ * consecutive pieces = one contiguous kilobyte of LDS). */
+__device__ __forceinline__ void v4_window_loads(const uint8_t *const (&pbase)[V3_PPT], const int (&pbb)[V3_PPT], int kb,
+                                                uint8_t *Wb)
+{
+    const int w = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < V3_PPT; i++) {
+        const uintptr_t q = (uintptr_t)(pbase[i] + (size_t)kb * pbb[i]) & ~(uintptr_t)15;
+        __builtin_amdgcn_global_load_lds((const AS1 void *)q, (AS3 void *)(Wb + 1024 * (w + V2_W * i)), 16, 0, 0);
+    }
+}
+
+/* Window piece bases of this thread: window c -> (row pointer + 16 * piece),
+ * the K step's block is then at + kb * block bytes, rounded down to 16. */
+template <bool GATEUP>
+__device__ __forceinline__ void v4_window_bases(const PfGroup &G, int first, int nkb, const uint8_t *(&pbase)[V3_PPT],
+                                                int (&pbb)[V3_PPT])
+{
+#pragma unroll
+    for (int i = 0; i < V3_PPT; i++) {
+        const int p = threadIdx.x + i * V2_T, c = p / V3_NP, j = p - c * V3_NP;
+        const uint8_t *row;
+        int bb;
+        if (GATEUP) {
+            const int n = c & 31, ww = c >> 5;
+            const bool up = n >= 16;
+            bb = (up ? G.uq6 : G.gq6) ? RQ6K_BYTES : RQ4K_BYTES;
+            row = (up ? G.u : G.g) + (size_t)(first + 16 * ww + (n & 15)) * nkb * bb;
+        } else {
+            bb = G.dq6 ? RQ6K_BYTES : RQ4K_BYTES;
+            row = G.d + (size_t)(first + c) * nkb * bb;
+        }
+        pbase[i] = row + 16 * j;
+        pbb[i] = bb;
+    }
+}
+
+/* The lane's raw block of K step kb from LDS (its window is 32 w + n). */
+template <bool Q6>
+__device__ __forceinline__ void v4_lane_raw(typename RawOf<Q6>::T &r, const uint8_t *Wb, const uint8_t *myrow, int kb,
+                                            int h)
+{
+    constexpr int bb = Q6 ? RQ6K_BYTES : RQ4K_BYTES;
+    const int a = (int)((uintptr_t)(myrow + (size_t)kb * bb) & 15);
+    const int c = 32 * (threadIdx.x >> 6) + (threadIdx.x & 31);     /* window 32 w + n */
+    raw_from_lds(r, (const uint32_t *)(Wb + c * V3_CH) + (a >> 2), a & 3, h);
+}
+
+struct V4Shared {
     int tok[V2_MC];
     int slot[V2_MC];
     float inv[V2_MC], fwd[V2_MC];
 };
 
-/* One K step (super-block) of MS row blocks x two 32-row weight blocks. */
-template <int MS, bool Q6A, bool Q6B>
-__device__ __forceinline__ void v2_kstep(f32x16 (&acc)[MS][2], const _Float16 *Xs, int ld,
-                                         const typename RawOf<Q6A>::T &ra, const typename RawOf<Q6B>::T &rb, int h)
+template <int MS, bool QG, bool QU>
+__device__ __forceinline__ void v4_gu_body(const PfGemmArgs &A, const PfGroup &G, const V4Shared &meta, int mlen, int j0,
+                                           uint8_t *lds)
 {
-    typename ConstOf<Q6A>::T ca;
-    typename ConstOf<Q6B>::T cb;
-    raw_consts(ra, h, ca);
-    raw_consts(rb, h, cb);
-    const int l = threadIdx.x & 63;
-    const _Float16 *xa = Xs + (l & 31) * ld + 8 * (l >> 5);
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        f16x8 a0b0, a0b1, a1b0, a1b1;
-        dequant_pair(ra, ca, j, a0b0, a0b1);
-        dequant_pair(rb, cb, j, a1b0, a1b1);
-#pragma unroll
-        for (int ms = 0; ms < MS; ms++) {
-            const f16x8 x0 = *(const f16x8 *)(xa + ms * 32 * ld + 16 * j);
-            const f16x8 x1 = *(const f16x8 *)(xa + ms * 32 * ld + 16 * (j + 8));
-            acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, a0b0, acc[ms][0], 0, 0, 0);
-            acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, a1b0, acc[ms][1], 0, 0, 0);
-            acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, a0b1, acc[ms][0], 0, 0, 0);
-            acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, a1b1, acc[ms][1], 0, 0, 0);
-        }
-    }
-}
-
-/* gate/up: block = (tile, V2_GU_J j's); wave w: gate and up rows jw .. jw+31. */
-template <int MS, bool G6, bool U6>
-__device__ __forceinline__ void v2_gu_body(const PfGemmArgs &A, const PfGroup &G, const V2Meta &meta, int mlen, int jw,
-                           _Float16 *Xs)
-{
-    typedef typename RawOf<G6>::T RG;
-    typedef typename RawOf<U6>::T RU;
-    const int t = threadIdx.x, l = t & 63, h = l >> 5;
+    const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
     const int nkb = A.H / GK;
-    const size_t bg = G6 ? RQ6K_BYTES : RQ4K_BYTES, bu = U6 ? RQ6K_BYTES : RQ4K_BYTES;
-    const uint8_t *gr = G.g + (size_t)(jw + (l & 31)) * nkb * bg;
-    const uint8_t *ur = G.u + (size_t)(jw + (l & 31)) * nkb * bu;
-    /* activation staging: 16-byte pieces, row = idx / 32, piece = idx % 32 */
+    _Float16 *Xb = (_Float16 *)lds;
+    uint8_t *Wb = lds + 2 * V3_XBUF * 2;
+    const uint8_t *pbase[V3_PPT];
+    int pbb[V3_PPT];
+    v4_window_bases<true>(G, j0, nkb, pbase, pbb);
+    const bool up = n >= 16;
+    const int jcol = j0 + 16 * w + (n & 15);
+    constexpr int bG = QG ? RQ6K_BYTES : RQ4K_BYTES, bU = QU ? RQ6K_BYTES : RQ4K_BYTES;
+    const uint8_t *myrow = up ? G.u + (size_t)jcol * nkb * bU : G.g + (size_t)jcol * nkb * bG;
+    /* activation staging through registers: 16-byte pieces idx = t + i * V2_T,
+     * row idx / 32, piece idx % 32 */
     constexpr int NP = (MS * 32 * 32 + V2_T - 1) / V2_T;
     uint4 xr[NP];
     const uint16_t *xrow[NP];
@@ -402,105 +471,126 @@ __device__ __forceinline__ void v2_gu_body(const PfGemmArgs &A, const PfGroup &G
     f32x16 acc[MS][2];
 #pragma unroll
     for (int ms = 0; ms < MS; ms++) acc[ms][0] = acc[ms][1] = (f32x16){};
-    RG rg;
-    RU ru;
-    raw_load(rg, gr, h);            /* issued before the staging loads, so that the wait */
-    raw_load(ru, ur, h);            /* for those leaves nothing pending at the loop head */
+    v4_window_loads(pbase, pbb, 0, Wb);
     x_load(0);
-    x_store(Xs);
+    x_store(Xb);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int kb = 0; kb < nkb; kb++) {
-        _Float16 *cur = Xs + (kb & 1) * (V2_MC * V2_LD);
-        RG ng;
-        RU nu;
         const bool more = kb + 1 < nkb;
+        typename RawOf<QG>::T rg;
+        typename RawOf<QU>::T ru;
+        if (QG == QU) {
+            v4_lane_raw<QG>(rg, Wb, myrow, kb, h);
+        } else if (up) {
+            v4_lane_raw<QU>(ru, Wb, myrow, kb, h);
+        } else {
+            v4_lane_raw<QG>(rg, Wb, myrow, kb, h);
+        }
+        __syncthreads();                    /* windows consumed: the buffer is free */
         if (more) {
+            v4_window_loads(pbase, pbb, kb + 1, Wb);
             x_load(kb + 1);
-            raw_load(ng, gr + (kb + 1) * bg, h);
-            raw_load(nu, ur + (kb + 1) * bu, h);
         }
-        v2_kstep<MS, G6, U6>(acc, cur, V2_LD, rg, ru, h);
+        const _Float16 *Xs = Xb + (kb & 1) * V3_XBUF;
+        if (QG == QU) {
+            v4_mfma<MS, QG>(acc, Xs, rg, h);
+        } else if (up) {
+            v4_mfma<MS, QU>(acc, Xs, ru, h);
+        } else {
+            v4_mfma<MS, QG>(acc, Xs, rg, h);
+        }
         if (more) {
-            x_store(Xs + ((kb + 1) & 1) * (V2_MC * V2_LD));
-            rg = ng;
-            ru = nu;
+            x_store(Xb + ((kb + 1) & 1) * V3_XBUF);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
         }
-        __syncthreads();
     }
-    /* epilogue: act = silu(gate) * up (f32), and each row's largest |act|
-     * over this workgroup's columns into amax[slot] (the down GEMM's row scale) */
+    /* epilogue: lane n < 16 holds gate, lane n + 16 up of column jcol; act =
+     * silu(gate) * up (f32), and each row's largest |act| over this wave's 16
+     * columns into pmax[slot][jcol / 16] (the down GEMM's row scale) */
+    const int npart = A.I / 16, part = (j0 + 16 * w) >> 4;
 #pragma unroll
     for (int ms = 0; ms < MS; ms++)
 #pragma unroll
         for (int i = 0; i < 16; i++) {
+            const float v = acc[ms][0][i] + acc[ms][1][i];
+            const float pv = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
             const int m0 = 32 * ms + 8 * (i >> 2) + (i & 3), m = m0 + 4 * h;
             float e = 0.0f;
-            if (m < mlen) {
+            if (m < mlen && !up) {
                 const float f = meta.fwd[m];
-                e = pf_silu_mul(acc[ms][0][i] * f, acc[ms][1][i] * f);
-                A.act[(size_t)meta.slot[m] * A.I + jw + (l & 31)] = e;
+                e = pf_silu_mul(v * f, pv * f);
+                A.act[(size_t)meta.slot[m] * A.I + jcol] = e;
             }
-            float lo, hi;
-            half_max(fabsf(e), lo, hi);
-            if (l == 0) {
-                if (m0 < mlen) atomicMax(A.amax + meta.slot[m0], __builtin_bit_cast(unsigned, lo));
-                if (m0 + 4 < mlen) atomicMax(A.amax + meta.slot[m0 + 4], __builtin_bit_cast(unsigned, hi));
-            }
+            /* max over the 16 gate lanes of each half (DPP rows 0 and 2) */
+            float mx = fabsf(e);
+            mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
+            mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
+            mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
+            mx = fmaxf(mx, dpp_f<DPP_MIRROR>(mx));
+            if (n == 0 && m < mlen) A.pmax[(size_t)meta.slot[m] * npart + part] = mx;
         }
 }
 
-/* down: block = (tile, V2_DN_N output rows); wave w: rows nw .. nw+63.  The
- * act rows (f32) are staged whole (K = inter) into LDS as scaled fp16 in the
- * permuted K order, after the first K step's weight loads are in flight. */
-template <int MS, bool D6>
-__device__ __forceinline__ void v2_dn_body(const PfGemmArgs &A, const V2Meta &meta, const PfGroup &G, int mlen,
-                                           int nw, _Float16 *Xs)
+template <int MS, bool QD>
+__device__ __forceinline__ void v4_dn_body(const PfGemmArgs &A, const PfGroup &G, const V4Shared &meta, int mlen, int n0,
+                                           uint8_t *lds)
 {
-    typedef typename RawOf<D6>::T RD;
-    const int t = threadIdx.x, l = t & 63, h = l >> 5;
-    const int nkb = A.I / GK, ld = A.I + 8;
-    const size_t bd = D6 ? RQ6K_BYTES : RQ4K_BYTES;
-    const uint8_t *r0 = G.d + (size_t)(nw + (l & 31)) * nkb * bd;
-    const uint8_t *r1 = G.d + (size_t)(nw + 32 + (l & 31)) * nkb * bd;
-    RD a0, a1;
-    raw_load(a0, r0, h);
-    raw_load(a1, r1, h);
-    /* staging: float4 pieces, 16 in flight per thread */
-    const int per_row = A.I / 4, total = mlen * per_row;
-    for (int base = 0; base < total; base += 16 * V2_T) {
-        float4 v[16];
+    const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
+    const int nkb = A.I / GK;
+    _Float16 *Xb = (_Float16 *)lds;
+    uint8_t *Wb = lds + 2 * V3_XBUF * 2;
+    const uint8_t *pbase[V3_PPT];
+    int pbb[V3_PPT];
+    v4_window_bases<false>(G, n0, nkb, pbase, pbb);
+    constexpr int bD = QD ? RQ6K_BYTES : RQ4K_BYTES;
+    const int orow = n0 + 32 * w + n;
+    const uint8_t *myrow = G.d + (size_t)orow * nkb * bD;
+    /* activation staging: act rows f32 (natural order) -> scaled fp16 in the
+     * permuted K order; float4 pieces idx = t + i * V2_T, row idx / 64.  The
+     * first two K steps are staged up front (both buffers); a later step kb is
+     * staged into buffer kb & 1 once step kb - 2 is done with it. */
+    constexpr int NP = MS * 32 * 64 / V2_T;
+    auto x_stage = [&](int kb, _Float16 *dst) {
+        float4 xr[NP];
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
-            const int idx = base + t + u * V2_T, row = idx / per_row, c = idx - row * per_row;
-            v[u] = idx < total ? gld_f4(A.act + (size_t)meta.slot[row] * A.I + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int i = 0; i < NP; i++) {
+            const int idx = t + i * V2_T, row = idx >> 6;
+            xr[i] = row < mlen ? gld_f4(A.act + (size_t)meta.slot[row] * A.I + kb * GK + 4 * (idx & 63))
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
-            const int idx = base + t + u * V2_T, row = idx / per_row, c = idx - row * per_row;
-            if (idx < total) {
-                const float s = meta.inv[row];
-                const f32x8 e = { v[u].x * s, v[u].y * s, v[u].z * s, v[u].w * s, 0.f, 0.f, 0.f, 0.f };
-                const uint4 cu = __builtin_bit_cast(uint4, __builtin_convertvector(e, f16x8));
-                const int k = 4 * c;
-                *(uint2 *)(Xs + row * ld + (k & ~255) + perm_slot4(k & 255)) = make_uint2(cu.x, cu.y);
-            }
+        for (int i = 0; i < NP; i++) {
+            const int idx = t + i * V2_T, row = idx >> 6;
+            const float s = row < mlen ? meta.inv[row] : 0.0f;
+            const f32x8 e = { xr[i].x * s, xr[i].y * s, xr[i].z * s, xr[i].w * s, 0.f, 0.f, 0.f, 0.f };
+            const uint4 cu = __builtin_bit_cast(uint4, __builtin_convertvector(e, f16x8));
+            *(uint2 *)(dst + row * V2_LD + perm_slot4(4 * (idx & 63))) = make_uint2(cu.x, cu.y);
         }
-    }
-    __syncthreads();
+    };
     f32x16 acc[MS][2];
 #pragma unroll
     for (int ms = 0; ms < MS; ms++) acc[ms][0] = acc[ms][1] = (f32x16){};
+    v4_window_loads(pbase, pbb, 0, Wb);
+    x_stage(0, Xb);
+    if (nkb > 1) x_stage(1, Xb + V3_XBUF);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     for (int kb = 0; kb < nkb; kb++) {
-        RD n0, n1;
         const bool more = kb + 1 < nkb;
-        if (more) {
-            raw_load(n0, r0 + (kb + 1) * bd, h);
-            raw_load(n1, r1 + (kb + 1) * bd, h);
+        typename RawOf<QD>::T r;
+        v4_lane_raw<QD>(r, Wb, myrow, kb, h);
+        __syncthreads();
+        if (more) v4_window_loads(pbase, pbb, kb + 1, Wb);
+        v4_mfma<MS, QD>(acc, Xb + (kb & 1) * V3_XBUF, r, h);
+        if (kb + 2 < nkb) {
+            __syncthreads();                /* every wave is done with buffer kb & 1 */
+            x_stage(kb + 2, Xb + (kb & 1) * V3_XBUF);
         }
-        v2_kstep<MS, D6, D6>(acc, Xs + kb * GK, ld, a0, a1, h);
         if (more) {
-            a0 = n0;
-            a1 = n1;
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
         }
     }
 #pragma unroll
@@ -508,12 +598,7 @@ __device__ __forceinline__ void v2_dn_body(const PfGemmArgs &A, const V2Meta &me
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (m < mlen) {
-                const float f = meta.fwd[m];
-                float *o = A.out + (size_t)meta.slot[m] * A.H + nw + (l & 31);
-                o[0] = acc[ms][0][i] * f;
-                o[32] = acc[ms][1][i] * f;
-            }
+            if (m < mlen) A.out[(size_t)meta.slot[m] * A.H + orow] = (acc[ms][0][i] + acc[ms][1][i]) * meta.fwd[m];
         }
 }
 
@@ -529,8 +614,8 @@ __device__ __forceinline__ bool v2_tile(const PfGemmArgs &A, int nblk, int &v, P
 
 extern "C" __global__ void __launch_bounds__(V2_T) pf2_gu_kernel(PfGemmArgs A)
 {
-    extern __shared__ __attribute__((aligned(16))) _Float16 xs2[];
-    __shared__ V2Meta meta;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds4[];
+    __shared__ V4Shared meta;
     const int nblk = A.I / V2_GU_J;
     int v;
     PfTile tile;
@@ -538,25 +623,23 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_gu_kernel(PfGemmArgs A)
     const PfGroup &G = A.groups[tile.grp];
     const int mlen = min(V2_MC, G.n - tile.m0);
     const int t = threadIdx.x;
-    if (t < V2_MC) {
+    if (t < mlen) {
         const int a = tile.m0 + t;
-        if (t < mlen) {
-            const int tok = G.tok ? G.tok[a] : G.tok0 + a;
-            meta.tok[t] = tok;
-            meta.slot[t] = G.slot0 + a;
-            meta.fwd[t] = A.xfwd ? A.xfwd[tok] : 1.0f;
-        }
+        const int tok = G.tok ? G.tok[a] : G.tok0 + a;
+        meta.tok[t] = tok;
+        meta.slot[t] = G.slot0 + a;
+        meta.fwd[t] = A.xfwd ? A.xfwd[tok] : 1.0f;
     }
     __syncthreads();
-    const int jw = (v % nblk) * V2_GU_J + 32 * (t >> 6);
+    const int j0 = (v % nblk) * V2_GU_J;
     const int ms = (mlen + 31) >> 5;
     const int ty = (G.gq6 ? 2 : 0) | (G.uq6 ? 1 : 0);
 #define GU_CASE(M)                                                                   \
     if (ms == M) {                                                                   \
-        if (ty == 3) v2_gu_body<M, true, true>(A, G, meta, mlen, jw, xs2);          \
-        else if (ty == 2) v2_gu_body<M, true, false>(A, G, meta, mlen, jw, xs2);    \
-        else if (ty == 1) v2_gu_body<M, false, true>(A, G, meta, mlen, jw, xs2);    \
-        else v2_gu_body<M, false, false>(A, G, meta, mlen, jw, xs2);                \
+        if (ty == 3) v4_gu_body<M, true, true>(A, G, meta, mlen, j0, lds4);          \
+        else if (ty == 2) v4_gu_body<M, true, false>(A, G, meta, mlen, j0, lds4);   \
+        else if (ty == 1) v4_gu_body<M, false, true>(A, G, meta, mlen, j0, lds4);   \
+        else v4_gu_body<M, false, false>(A, G, meta, mlen, j0, lds4);               \
         return;                                                                      \
     }
     GU_CASE(1)
@@ -567,30 +650,33 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_gu_kernel(PfGemmArgs A)
 
 extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
 {
-    extern __shared__ __attribute__((aligned(16))) _Float16 xs2[];
-    __shared__ V2Meta meta;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds4[];
+    __shared__ V4Shared meta;
     const int nblk = A.H / V2_DN_N;
     int v;
     PfTile tile;
     if (!v2_tile(A, nblk, v, tile)) return;
     const PfGroup &G = A.groups[tile.grp];
     const int mlen = min(V2_MC, G.n - tile.m0);
-    const int t = threadIdx.x, w = t >> 6;
+    const int t = threadIdx.x;
     if (t < mlen) {
         const int slot = G.slot0 + tile.m0 + t;
+        const int nb = A.I / 16;
+        float mx = 0.0f;
+        for (int b = 0; b < nb; b++) mx = fmaxf(mx, A.pmax[(size_t)slot * nb + b]);
         float inv, fwd;
-        row_scale(__builtin_bit_cast(float, A.amax[slot]), inv, fwd);
+        row_scale(mx, inv, fwd);
         meta.slot[t] = slot;
         meta.inv[t] = inv;
         meta.fwd[t] = fwd;
     }
     __syncthreads();
-    const int nw = (v % nblk) * V2_DN_N + 64 * w;
+    const int n0 = (v % nblk) * V2_DN_N;
     const int ms = (mlen + 31) >> 5;
 #define DN_CASE(M)                                                                   \
     if (ms == M) {                                                                   \
-        if (G.dq6) v2_dn_body<M, true>(A, meta, G, mlen, nw, xs2);                  \
-        else v2_dn_body<M, false>(A, meta, G, mlen, nw, xs2);                       \
+        if (G.dq6) v4_dn_body<M, true>(A, G, meta, mlen, n0, lds4);                 \
+        else v4_dn_body<M, false>(A, G, meta, mlen, n0, lds4);                      \
         return;                                                                      \
     }
     DN_CASE(1)
@@ -620,7 +706,7 @@ int pf_gemm_launch(const PfGemmArgs &A, int max_tiles, int op)
     if (op == PF_SPLIT) return launch_v1<PF_SPLIT>(A, max_tiles);
     if (op == PF_BF16) return launch_v1<PF_BF16>(A, max_tiles);
     RtState &R = rt();
-    const size_t lds_gu = 2 * (size_t)V2_MC * V2_LD * 2, lds_dn = (size_t)V2_MC * (A.I + 8) * 2;
+    const size_t lds_gu = 2 * (size_t)V3_XBUF * 2 + V3_WBYTES, lds_dn = lds_gu;
     hipLaunchKernelGGL(pf2_gu_kernel, dim3(max_tiles * (A.I / V2_GU_J)), dim3(V2_T), lds_gu, R.stream, A);
     if (rt_check(hipGetLastError(), "prefill gate/up launch")) return ROASTER_EDEVICE;
     hipLaunchKernelGGL(pf2_down_kernel, dim3(max_tiles * (A.H / V2_DN_N)), dim3(V2_T), lds_dn, R.stream, A);

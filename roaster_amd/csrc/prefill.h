@@ -34,7 +34,7 @@ struct PfGemmArgs {
     const uint16_t *X16;            /* [* x H] fp16 activations, scaled, permuted (v2), or NULL */
     const float *xinv, *xfwd;       /* per X row power-of-two scales (fp16 mode), or NULL */
     float *act;                     /* [slots x I]: silu(gate) * up */
-    unsigned *amax;                 /* [slots] max |act| bits (fp16 mode), or NULL */
+    float *pmax;                    /* [slots][inter / 16] partial max |act| (fp16 mode) */
     float *out;                     /* [slots x H]: down products */
     int H, I;
 };

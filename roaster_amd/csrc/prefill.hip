@@ -133,14 +133,12 @@ struct PfTokArgs {
     float *sg;                  /* [T] */
     float *xinv, *xfwd;         /* [T] (fp16 mode) or NULL */
     uint16_t *x16;              /* [T x H] fp16 X * xinv in the GEMM's permuted K order, or NULL */
-    unsigned *amax;             /* [9T] per-slot max |act| bits, zeroed here, or NULL */
     int *err;
     int T, E, H;
 };
 
 extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
 {
-    __shared__ unsigned long long sk[4][16];
     __shared__ int bad[4];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + wv;
@@ -174,7 +172,6 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
             }
     }
     if (lane == 0) A.sg[t] = 1.0f / (1.0f + expf(-dot));
-    if (A.amax && lane < 9) A.amax[(size_t)t * 9 + lane] = 0u;
     /* logits */
     float v4[4];
 #pragma unroll
@@ -196,7 +193,7 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
     }
     if (lane == 0) bad[wv] = 0;
     __builtin_amdgcn_wave_barrier();
-    topk8_wave(v4, A.E, A.ids + (size_t)t * 8, A.w + (size_t)t * 8, &bad[wv], sk[wv]);
+    topk8_wave(v4, A.E, A.ids + (size_t)t * 8, A.w + (size_t)t * 8, &bad[wv]);
     if (lane < 8) {
         if (A.ids_out) A.ids_out[(size_t)t * 8 + lane] = A.ids[(size_t)t * 8 + lane];
         if (A.w_out) A.w_out[(size_t)t * 8 + lane] = A.w[(size_t)t * 8 + lane];
@@ -373,7 +370,7 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     const size_t o_x16 = op == PF_F16 ? take(TT * H * 2) : 0;
     const size_t o_cnt = take((size_t)E * 4), o_off = take((size_t)E * 4), o_list = take((size_t)E * TT * 4);
     const size_t o_grp = take(sizeof(PfGroup) * (E + 1)), o_tiles = take(sizeof(PfTile) * max_tiles);
-    const size_t o_nt = take(4), o_amax = take(slots * 4);
+    const size_t o_nt = take(4), o_pmax = take(slots * (size_t)(I / 16) * 4);
     const size_t o_act = take(slots * I * 4), o_ed = take(slots * H * 4);
     uint8_t *ws = (uint8_t *)rt_scratch(SCR_PF, sz);
     unsigned *ctrl = rt_ctrl();
@@ -401,7 +398,6 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     ta.xinv = op == PF_F16 ? (float *)(ws + o_xinv) : nullptr;
     ta.xfwd = op == PF_F16 ? (float *)(ws + o_xfwd) : nullptr;
     ta.x16 = op == PF_F16 ? (uint16_t *)(ws + o_x16) : nullptr;
-    ta.amax = op == PF_F16 ? (unsigned *)(ws + o_amax) : nullptr;
     ta.err = (int *)(ctrl + 16);
     ta.T = T; ta.E = E; ta.H = H;
     hipLaunchKernelGGL(pf_token_kernel, dim3((T + 3) / 4), dim3(256), 0, R.stream, ta);
@@ -437,7 +433,7 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     ga.xinv = ta.xinv;
     ga.xfwd = ta.xfwd;
     ga.act = (float *)(ws + o_act);
-    ga.amax = ta.amax;
+    ga.pmax = op == PF_F16 ? (float *)(ws + o_pmax) : nullptr;
     ga.out = (float *)(ws + o_ed);
     ga.H = H; ga.I = I;
     if (int rc = pf_gemm_launch(ga, max_tiles, op)) return rc;

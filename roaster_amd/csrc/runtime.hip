@@ -146,7 +146,7 @@ extern "C" void *roaster_dev_alloc(size_t bytes)
     std::lock_guard<std::recursive_mutex> g(g_lock);
     if (rt_init_locked()) return NULL;
     void *p = NULL;
-    if (rt_check(hipMalloc(&p, bytes ? bytes : 1), "hipMalloc")) return NULL;
+    if (rt_check(hipMalloc(&p, bytes + RT_TAIL_PAD), "hipMalloc")) return NULL;
     rt_register_device_range(p, bytes ? bytes : 1);
     return p;
 }
@@ -197,7 +197,7 @@ void *rt_scratch(int slot, size_t bytes)
     if (b.p) { (void)hipStreamSynchronize(g_rt.stream); (void)hipFree(b.p); b.p = NULL; b.n = 0; }
     size_t n = bytes < 4096 ? 4096 : bytes;
     n = (n + 4095) & ~(size_t)4095;
-    if (rt_check(hipMalloc(&b.p, n), "scratch hipMalloc")) { b.p = NULL; return NULL; }
+    if (rt_check(hipMalloc(&b.p, n + RT_TAIL_PAD), "scratch hipMalloc")) { b.p = NULL; return NULL; }
     b.n = n;
     return b.p;
 }
@@ -294,7 +294,7 @@ const void *rt_weight_dev(const void *ptr, size_t bytes)
     auto im = g_imports.find(key);
     if (im != g_imports.end()) return im->second;
     void *d = NULL;
-    if (rt_check(hipMalloc(&d, bytes), "import hipMalloc")) return NULL;
+    if (rt_check(hipMalloc(&d, bytes + RT_TAIL_PAD), "import hipMalloc")) return NULL;
     if (rt_check(hipMemcpy(d, ptr, bytes, hipMemcpyHostToDevice), "import upload")) { (void)hipFree(d); return NULL; }
     g_imports[key] = d;
     return d;
@@ -330,7 +330,7 @@ extern "C" void *kernel_vk_alloc_weights(size_t size, size_t *granted)
         Arena na;
         na.host = (uint8_t *)mmap(NULL, asz, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS | MAP_NORESERVE, -1, 0);
         if (na.host == MAP_FAILED) { rt_fail(ROASTER_ENOMEM, "mmap of %zu bytes failed", asz); return NULL; }
-        if (hipMalloc((void **)&na.dev, asz) != hipSuccess) {
+        if (hipMalloc((void **)&na.dev, asz + RT_TAIL_PAD) != hipSuccess) {
             (void)hipGetLastError();
             munmap(na.host, asz);
             rt_fail(ROASTER_ENOMEM, "HBM arena of %zu bytes unavailable", asz);
@@ -372,7 +372,7 @@ extern "C" int kernel_vk_register_region(const void *ptr, size_t size)
     Region R;
     R.size = size;
     R.dev = NULL;
-    if (hipMalloc((void **)&R.dev, size) != hipSuccess) { (void)hipGetLastError(); return 0; }
+    if (hipMalloc((void **)&R.dev, size + RT_TAIL_PAD) != hipSuccess) { (void)hipGetLastError(); return 0; }
     g_regions[(uintptr_t)ptr] = R;
     return 1;
 }

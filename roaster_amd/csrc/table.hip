@@ -44,7 +44,7 @@ extern "C" RoasterTable *roaster_table_create(const RoasterTableDesc *d)
     t->layer_bytes = off;
     t->qbytes = off * (size_t)d->n_layers;
     t->fbytes = (size_t)d->n_layers * (E * H + H) * sizeof(float);
-    if (hipMalloc((void **)&t->qmem, t->qbytes) != hipSuccess ||
+    if (hipMalloc((void **)&t->qmem, t->qbytes + RT_TAIL_PAD) != hipSuccess ||
         hipMalloc((void **)&t->fmem, t->fbytes) != hipSuccess ||
         hipMalloc((void **)&t->layers_d, sizeof(DecLayer) * d->n_layers) != hipSuccess) {
         (void)hipGetLastError();

@@ -30,59 +30,50 @@ __device__ __forceinline__ float key_logit(uint32_t k)
     return __builtin_bit_cast(float, u);
 }
 
-/* Wave-level top-8 of one token (model.c:869-897).  Each logit becomes a
- * distinct 40-bit key (logit key << 8 | 255 - expert), so the order is "larger
- * logit, then lower index" and no two keys tie; NaN / -inf get key 0.  A radix
- * select over the 40 bits (ballot counts per bit) finds the 8th largest key,
- * the (at most 8) keys >= it are ranked in 8 lanes, and the softmax over the
- * selected logits is summed in slot order like the reference.  v4[i] holds the
- * logit of expert lane + 64*i (E <= 256).  sk: 16 entries of LDS scratch. */
-static __device__ void topk8_wave(const float v4in[4], int E, int *ids, float *w, int *bad, unsigned long long *sk)
+/* Wave-level top-8 of one token (model.c:869-897).  Each logit becomes an
+ * order-preserving 32-bit key (NaN and -inf: key 0, never selected).  Eight
+ * rounds each take the wave maximum of the keys (DPP within 16-lane rows, then
+ * the four row maxima) and, among the experts holding it, the lowest index
+ * (ballot, first set bit): "larger logit, then lower index", the order the
+ * reference's strict-greater insertion produces.  The softmax over the selected
+ * logits is then summed in slot order like the reference.  v4[i] holds the
+ * logit of expert lane + 64*i (E <= 256).  Fewer than 8 selectable logits:
+ * the remaining ids are -1 and *bad is set. */
+static __device__ void topk8_wave(const float v4in[4], int E, int *ids, float *w, int *bad)
 {
     const int lane = threadIdx.x & 63;
-    unsigned long long key[4];
+    uint32_t key[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int e = lane + 64 * i;
-        const uint32_t k32 = e < E ? logit_key(v4in[i]) : 0u;
-        key[i] = k32 ? (((unsigned long long)k32 << 8) | (unsigned long long)(255 - e)) : 0ull;
+        key[i] = e < E ? logit_key(v4in[i]) : 0u;
     }
-    unsigned long long P = 0ull;
-    for (int b = 39; b >= 0; b--) {
-        const unsigned long long C = P | (1ull << b);
-        int cnt = 0;
+    float v = -INFINITY;
+    int myid = -1, nsel = 0;
+    for (int r = 0; r < RTOPK; r++) {
+        uint32_t m = max(max(key[0], key[1]), max(key[2], key[3]));
+        m = max(m, (uint32_t)dpp_i<DPP_XOR1>((int)m));
+        m = max(m, (uint32_t)dpp_i<DPP_XOR2>((int)m));
+        m = max(m, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)m));
+        m = max(m, (uint32_t)dpp_i<DPP_MIRROR>((int)m));
+        const uint32_t M = max(max((uint32_t)__builtin_amdgcn_readlane((int)m, 0), (uint32_t)__builtin_amdgcn_readlane((int)m, 16)),
+                               max((uint32_t)__builtin_amdgcn_readlane((int)m, 32), (uint32_t)__builtin_amdgcn_readlane((int)m, 48)));
+        if (M == 0u) break;                               /* no selectable logit left */
+        int e = -1;
 #pragma unroll
-        for (int i = 0; i < 4; i++) cnt += __popcll(__ballot(key[i] >= C));
-        if (cnt >= RTOPK) P = C;
-    }
-    /* the selected keys: >= P and valid; compact them into sk[0..nsel) */
-    int base = 0;
-    const unsigned long long lt = (1ull << lane) - 1ull;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const bool sel = key[i] != 0ull && key[i] >= P;
-        const unsigned long long m = __ballot(sel);
-        if (sel) {
-            const int pos = base + __popcll(m & lt);
-            if (pos < RTOPK) sk[pos] = key[i];
+        for (int i = 0; i < 4; i++) {
+            const unsigned long long b = __ballot(key[i] == M);
+            if (e < 0 && b) e = 64 * i + (int)__builtin_ctzll(b);
         }
-        base += __popcll(m);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (e == lane + 64 * i) key[i] = 0u;
+        if (lane == r) {
+            v = key_logit(M);
+            myid = e;
+        }
+        nsel++;
     }
-    const int nsel = base < RTOPK ? base : RTOPK;
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    /* rank the selected keys (descending) in lanes 0..7 */
-    if (lane < nsel) {
-        const unsigned long long my = sk[lane];
-        int r = 0;
-        for (int j = 0; j < nsel; j++) r += sk[j] > my;
-        sk[8 + r] = my;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    const unsigned long long kk = lane < nsel ? sk[8 + lane] : 0ull;
-    const int e = kk ? 255 - (int)(kk & 0xFFull) : -1;
-    const float v = kk ? key_logit((uint32_t)(kk >> 8)) : -INFINITY;
     const float mx = lane_f(v, 0);
     const float ex = expf(v - mx);
     float sum = 0.0f;
@@ -90,7 +81,7 @@ static __device__ void topk8_wave(const float v4in[4], int E, int *ids, float *w
     for (int k = 0; k < RTOPK; k++) sum += lane_f(ex, k);
     const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
     if (lane < RTOPK) {
-        ids[lane] = e;
+        ids[lane] = myid;
         w[lane] = ex * inv;
     }
     if (lane == 0 && nsel < RTOPK) *bad = 1;
