@@ -34,6 +34,9 @@
 #include "prefill.h"
 
 static __device__ __forceinline__ float pf_silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+/* SiLU(g) * u with the hardware exp and reciprocal (a few ulp in f32; the
+ * result is rounded to fp16 for the next GEMM anyway). */
+static __device__ __forceinline__ float pf_silu_mul_fast(float g, float u) { return g * __frcp_rn(1.0f + __expf(-g)) * u; }
 
 /* Virtual block id: blocks b < R = ntiles * nblk run; on a grid dispatched
  * round-robin over the 8 XCDs, XCD b % 8 takes the contiguous range of
@@ -444,9 +447,9 @@ __device__ __forceinline__ void v4_gu_body(const PfGemmArgs &A, const PfGroup &G
     int pbb[V3_PPT];
     v4_window_bases<true>(G, j0, nkb, pbase, pbb);
     const bool up = n >= 16;
-    const int jcol = j0 + 16 * w + (n & 15);
     constexpr int bG = QG ? RQ6K_BYTES : RQ4K_BYTES, bU = QU ? RQ6K_BYTES : RQ4K_BYTES;
-    const uint8_t *myrow = up ? G.u + (size_t)jcol * nkb * bU : G.g + (size_t)jcol * nkb * bG;
+    const int jrow = j0 + 16 * w + (n & 15);
+    const uint8_t *myrow = up ? G.u + (size_t)jrow * nkb * bU : G.g + (size_t)jrow * nkb * bG;
     /* activation staging through registers: 16-byte pieces idx = t + i * V2_T,
      * row idx / 32, piece idx % 32 */
     constexpr int NP = (MS * 32 * 32 + V2_T - 1) / V2_T;
@@ -506,30 +509,36 @@ __device__ __forceinline__ void v4_gu_body(const PfGemmArgs &A, const PfGroup &G
             __syncthreads();
         }
     }
-    /* epilogue: lane n < 16 holds gate, lane n + 16 up of column jcol; act =
-     * silu(gate) * up (f32), and each row's largest |act| over this wave's 16
-     * columns into pmax[slot][jcol / 16] (the down GEMM's row scale) */
+    /* epilogue: lane n < 16 holds gate and lane n + 16 up of column jcol.  For
+     * the row pair (i, i + 1) one swizzle (lane ^ 16) gives lanes n < 16 the up
+     * value of row i and lanes n >= 16 the gate value of row i + 1, so all 32
+     * lanes compute act = silu(gate) * up (f32) for one row each; a 16-lane max
+     * gives each row's largest |act| over this wave's 16 columns, stored to
+     * pmax[slot][jcol / 16] (the down GEMM's row scale). */
     const int npart = A.I / 16, part = (j0 + 16 * w) >> 4;
+    const int col = j0 + 16 * w + (n & 15);
 #pragma unroll
     for (int ms = 0; ms < MS; ms++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float v = acc[ms][0][i] + acc[ms][1][i];
-            const float pv = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-            const int m0 = 32 * ms + 8 * (i >> 2) + (i & 3), m = m0 + 4 * h;
+        for (int i = 0; i < 16; i += 2) {
+            const float v0 = acc[ms][0][i] + acc[ms][1][i], v1 = acc[ms][0][i + 1] + acc[ms][1][i + 1];
+            const float mine = up ? v1 : v0, other = up ? v0 : v1;
+            const float got = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, other), 0x401F));
+            /* lane n < 16: row i, gate = mine, up = got; lane n >= 16: row i + 1, gate = got, up = mine */
+            const float gsum = up ? got : mine, usum = up ? mine : got;
+            const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3) + (up ? 1 : 0);
             float e = 0.0f;
-            if (m < mlen && !up) {
+            if (m < mlen) {
                 const float f = meta.fwd[m];
-                e = pf_silu_mul(v * f, pv * f);
-                A.act[(size_t)meta.slot[m] * A.I + jcol] = e;
+                e = pf_silu_mul_fast(gsum * f, usum * f);
+                A.act[(size_t)meta.slot[m] * A.I + col] = e;
             }
-            /* max over the 16 gate lanes of each half (DPP rows 0 and 2) */
             float mx = fabsf(e);
             mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
             mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
             mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
             mx = fmaxf(mx, dpp_f<DPP_MIRROR>(mx));
-            if (n == 0 && m < mlen) A.pmax[(size_t)meta.slot[m] * npart + part] = mx;
+            if ((n & 15) == 0 && m < mlen) A.pmax[(size_t)meta.slot[m] * npart + part] = mx;
         }
 }
 
