@@ -32,6 +32,7 @@
 #include "internal.h"
 #include "gemm.h"
 #include "prefill.h"
+#include "tile.h"
 
 static __device__ __forceinline__ float pf_silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
 /* SiLU(g) * u with the hardware exp and reciprocal (a few ulp in f32; the
@@ -353,11 +354,10 @@ __device__ __forceinline__ void raw_from_lds(RawQ4 &r, const uint32_t *p, int sh
     for (int j = 0; j < 16; j++) r.Q[j] = lds_al(p, 4 + 16 * h + j, sh);
 }
 
-/* MFMA work of one K step: MS row blocks x this wave's 32 weight columns; the
- * two accumulators per row block take k-slices j and j + 8 (independent
- * chains).  Xs: activation buffer, row stride V2_LD. */
+/* MFMA work of one K step: MS row blocks x this wave's 32 weight columns, one
+ * accumulator per row block.  Xs: activation buffer, row stride V2_LD. */
 template <int MS, bool Q6>
-__device__ __forceinline__ void v4_mfma(f32x16 (&acc)[MS][2], const _Float16 *Xs, const typename RawOf<Q6>::T &r,
+__device__ __forceinline__ void v4_mfma(f32x16 (&acc)[MS], const _Float16 *Xs, const typename RawOf<Q6>::T &r,
                                         int h)
 {
     typename ConstOf<Q6>::T c;
@@ -372,8 +372,8 @@ __device__ __forceinline__ void v4_mfma(f32x16 (&acc)[MS][2], const _Float16 *Xs
         for (int ms = 0; ms < MS; ms++) {
             const f16x8 x0 = *(const f16x8 *)(xa + ms * 32 * V2_LD + 16 * j);
             const f16x8 x1 = *(const f16x8 *)(xa + ms * 32 * V2_LD + 16 * (j + 8));
-            acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, b0, acc[ms][0], 0, 0, 0);
-            acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, b1, acc[ms][1], 0, 0, 0);
+            acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, b0, acc[ms], 0, 0, 0);
+            acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, b1, acc[ms], 0, 0, 0);
         }
     }
 }
@@ -471,9 +471,9 @@ __device__ __forceinline__ void v4_gu_body(const PfGemmArgs &A, const PfGroup &G
             if (row < MS * 32) *(uint4 *)(dst + row * V2_LD + 8 * (idx & 31)) = xr[i];
         }
     };
-    f32x16 acc[MS][2];
+    f32x16 acc[MS];
 #pragma unroll
-    for (int ms = 0; ms < MS; ms++) acc[ms][0] = acc[ms][1] = (f32x16){};
+    for (int ms = 0; ms < MS; ms++) acc[ms] = (f32x16){};
     v4_window_loads(pbase, pbb, 0, Wb);
     x_load(0);
     x_store(Xb);
@@ -521,7 +521,7 @@ __device__ __forceinline__ void v4_gu_body(const PfGemmArgs &A, const PfGroup &G
     for (int ms = 0; ms < MS; ms++)
 #pragma unroll
         for (int i = 0; i < 16; i += 2) {
-            const float v0 = acc[ms][0][i] + acc[ms][1][i], v1 = acc[ms][0][i + 1] + acc[ms][1][i + 1];
+            const float v0 = acc[ms][i], v1 = acc[ms][i + 1];
             const float mine = up ? v1 : v0, other = up ? v0 : v1;
             const float got = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, other), 0x401F));
             /* lane n < 16: row i, gate = mine, up = got; lane n >= 16: row i + 1, gate = got, up = mine */
@@ -578,9 +578,9 @@ __device__ __forceinline__ void v4_dn_body(const PfGemmArgs &A, const PfGroup &G
             *(uint2 *)(dst + row * V2_LD + perm_slot4(4 * (idx & 63))) = make_uint2(cu.x, cu.y);
         }
     };
-    f32x16 acc[MS][2];
+    f32x16 acc[MS];
 #pragma unroll
-    for (int ms = 0; ms < MS; ms++) acc[ms][0] = acc[ms][1] = (f32x16){};
+    for (int ms = 0; ms < MS; ms++) acc[ms] = (f32x16){};
     v4_window_loads(pbase, pbb, 0, Wb);
     x_stage(0, Xb);
     if (nkb > 1) x_stage(1, Xb + V3_XBUF);
@@ -607,7 +607,212 @@ __device__ __forceinline__ void v4_dn_body(const PfGemmArgs &A, const PfGroup &G
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (m < mlen) A.out[(size_t)meta.slot[m] * A.H + orow] = (acc[ms][0][i] + acc[ms][1][i]) * meta.fwd[m];
+            if (m < mlen) A.out[(size_t)meta.slot[m] * A.H + orow] = acc[ms][i] * meta.fwd[m];
+        }
+}
+
+/* ---- v5: weights straight from the MFMA tile layout into registers ----------
+ * Workgroup shape, MFMA work and activation staging as in v4 (8 waves, two per
+ * SIMD; activations double-buffered in LDS through registers), but every lane
+ * loads its raw super-block half directly from the tile copy of the matrix
+ * (tile.h): six 16-byte loads and a 12-byte tail (Q6_K) or five 16-byte loads
+ * (Q4_K), each instruction covering contiguous runs of a wave's records (one
+ * kilobyte for down; two 256-byte runs for gate/up, whose waves pair 16 gate
+ * rows with 16 up rows).  The raw registers are double-buffered per wave: step
+ * kb + 1's loads are issued before step kb's MFMA work, with no workgroup
+ * barrier for them, and the LDS holds activations only. */
+__device__ __forceinline__ void tile_load(RawQ6 &r, const uint8_t *tile, int lane)
+{
+    const uint8_t *p = tile + 16 * lane;
+    uint4 s[6];
+#pragma unroll
+    for (int i = 0; i < 6; i++) s[i] = gld_u4(p + 1024 * i);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r.L[4 * i] = s[i].x; r.L[4 * i + 1] = s[i].y; r.L[4 * i + 2] = s[i].z; r.L[4 * i + 3] = s[i].w;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        r.Hh[4 * i] = s[4 + i].x; r.Hh[4 * i + 1] = s[4 + i].y; r.Hh[4 * i + 2] = s[4 + i].z; r.Hh[4 * i + 3] = s[4 + i].w;
+    }
+    const uint8_t *q = tile + TL_Q6_TAIL + 12 * lane;
+    r.S[0] = gld_u32(q);
+    r.S[1] = gld_u32(q + 4);
+    r.d = gld_u32(q + 8) & 0xFFFFu;
+}
+
+__device__ __forceinline__ void tile_load(RawQ4 &r, const uint8_t *tile, int lane)
+{
+    const uint8_t *p = tile + 16 * lane;
+    uint4 s[5];
+#pragma unroll
+    for (int i = 0; i < 5; i++) s[i] = gld_u4(p + 1024 * i);
+    r.hd[0] = s[0].x; r.hd[1] = s[0].y; r.hd[2] = s[0].z; r.hd[3] = s[0].w;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r.Q[4 * i] = s[1 + i].x; r.Q[4 * i + 1] = s[1 + i].y; r.Q[4 * i + 2] = s[1 + i].z; r.Q[4 * i + 3] = s[1 + i].w;
+    }
+}
+
+/* Gate/up tile: lanes n < 16 of wave w take gate row j0 + 16 w + n, lanes
+ * n >= 16 the up row of the same column.  QG == QU: one raw type per wave;
+ * otherwise the two halves take divergent paths. */
+template <int MS, bool QG, bool QU>
+__device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G, const V4Shared &meta, int mlen, int j0,
+                                           uint8_t *lds)
+{
+    const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
+    const int nkb = A.H / GK;
+    _Float16 *Xb = (_Float16 *)lds;
+    const bool up = n >= 16;
+    const int jrow = j0 + 16 * w + (n & 15);
+    const int tlane = (jrow & (TL_ROWS - 1)) + 32 * h;
+    constexpr int TG = TL_BYTES(QG), TU = TL_BYTES(QU);
+    const uint8_t *wt = up ? G.tu + (size_t)(jrow / TL_ROWS) * nkb * TU : G.tg + (size_t)(jrow / TL_ROWS) * nkb * TG;
+    const int tb = up ? TU : TG;
+    constexpr int NP = (MS * 32 * 32 + V2_T - 1) / V2_T;
+    uint4 xr[NP];
+    const uint16_t *xrow[NP];
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const int idx = t + i * V2_T, row = idx >> 5;
+        xrow[i] = row < mlen ? A.X16 + (size_t)meta.tok[row] * A.H + 8 * (idx & 31) : nullptr;
+    }
+    auto x_load = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < NP; i++) xr[i] = xrow[i] ? gld_u4(xrow[i] + kb * GK) : make_uint4(0u, 0u, 0u, 0u);
+    };
+    auto x_store = [&](_Float16 *dst) {
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int idx = t + i * V2_T, row = idx >> 5;
+            if (row < MS * 32) *(uint4 *)(dst + row * V2_LD + 8 * (idx & 31)) = xr[i];
+        }
+    };
+    f32x16 acc[MS];
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++) acc[ms] = (f32x16){};
+    typename RawOf<QG>::T rg[2];
+    typename RawOf<QU>::T ru[2];
+    auto w_load = [&](int buf, int kb) {
+        if (QG == QU || !up) tile_load(rg[buf], wt + (size_t)kb * tb, tlane);
+        else tile_load(ru[buf], wt + (size_t)kb * tb, tlane);
+    };
+    auto step = [&](int buf, const _Float16 *Xs) {
+        if (QG == QU) v4_mfma<MS, QG>(acc, Xs, rg[buf], h);
+        else if (up) v4_mfma<MS, QU>(acc, Xs, ru[buf], h);
+        else v4_mfma<MS, QG>(acc, Xs, rg[buf], h);
+    };
+    w_load(0, 0);
+    x_load(0);
+    x_store(Xb);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; kb += 2) {
+        /* step kb: raw buffer 0, activation buffer 0 */
+        const bool m1 = kb + 1 < nkb;
+        if (m1) {
+            w_load(1, kb + 1);
+            x_load(kb + 1);
+        }
+        step(0, Xb);
+        if (!m1) break;
+        x_store(Xb + V3_XBUF);
+        __syncthreads();
+        /* step kb + 1: raw buffer 1, activation buffer 1 */
+        const bool m2 = kb + 2 < nkb;
+        if (m2) {
+            w_load(0, kb + 2);
+            x_load(kb + 2);
+        }
+        step(1, Xb + V3_XBUF);
+        if (!m2) break;
+        x_store(Xb);
+        __syncthreads();
+    }
+    /* epilogue: as in v4 */
+    const int npart = A.I / 16, part = (j0 + 16 * w) >> 4;
+    const int col = j0 + 16 * w + (n & 15);
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            const float v0 = acc[ms][i], v1 = acc[ms][i + 1];
+            const float mine = up ? v1 : v0, other = up ? v0 : v1;
+            const float got = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, other), 0x401F));
+            const float gsum = up ? got : mine, usum = up ? mine : got;
+            const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3) + (up ? 1 : 0);
+            float e = 0.0f;
+            if (m < mlen) {
+                const float f = meta.fwd[m];
+                e = pf_silu_mul_fast(gsum * f, usum * f);
+                A.act[(size_t)meta.slot[m] * A.I + col] = e;
+            }
+            float mx = fabsf(e);
+            mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
+            mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
+            mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
+            mx = fmaxf(mx, dpp_f<DPP_MIRROR>(mx));
+            if ((n & 15) == 0 && m < mlen) A.pmax[(size_t)meta.slot[m] * npart + part] = mx;
+        }
+}
+
+/* Down tile: wave w takes output rows n0 + 32 w .. + 31 (one tile row group,
+ * its lane records in lane order). */
+template <int MS, bool QD>
+__device__ __forceinline__ void v5_dn_body(const PfGemmArgs &A, const PfGroup &G, const V4Shared &meta, int mlen, int n0,
+                                           uint8_t *lds)
+{
+    const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
+    const int nkb = A.I / GK;
+    _Float16 *Xb = (_Float16 *)lds;
+    constexpr int TD = TL_BYTES(QD);
+    const int orow = n0 + 32 * w + n;
+    const uint8_t *wt = G.td + (size_t)((n0 + 32 * w) / TL_ROWS) * nkb * TD;
+    constexpr int NP = MS * 32 * 64 / V2_T;
+    auto x_stage = [&](int kb, _Float16 *dst) {
+        float4 xr[NP];
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int idx = t + i * V2_T, row = idx >> 6;
+            xr[i] = row < mlen ? gld_f4(A.act + (size_t)meta.slot[row] * A.I + kb * GK + 4 * (idx & 63))
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int idx = t + i * V2_T, row = idx >> 6;
+            const float s = row < mlen ? meta.inv[row] : 0.0f;
+            const f32x8 e = { xr[i].x * s, xr[i].y * s, xr[i].z * s, xr[i].w * s, 0.f, 0.f, 0.f, 0.f };
+            const uint4 cu = __builtin_bit_cast(uint4, __builtin_convertvector(e, f16x8));
+            *(uint2 *)(dst + row * V2_LD + perm_slot4(4 * (idx & 63))) = make_uint2(cu.x, cu.y);
+        }
+    };
+    f32x16 acc[MS];
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++) acc[ms] = (f32x16){};
+    typename RawOf<QD>::T r[2];
+    tile_load(r[0], wt, l);
+    if (nkb > 1) tile_load(r[1], wt + TD, l);
+    x_stage(0, Xb);
+    if (nkb > 1) x_stage(1, Xb + V3_XBUF);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; kb += 2) {
+        v4_mfma<MS, QD>(acc, Xb, r[0], h);
+        if (kb + 1 >= nkb) break;
+        if (kb + 2 < nkb) tile_load(r[0], wt + (size_t)(kb + 2) * TD, l);
+        v4_mfma<MS, QD>(acc, Xb + V3_XBUF, r[1], h);
+        if (kb + 2 >= nkb) break;
+        if (kb + 3 < nkb) tile_load(r[1], wt + (size_t)(kb + 3) * TD, l);
+        __syncthreads();                    /* every wave is done with both buffers */
+        x_stage(kb + 2, Xb);
+        if (kb + 3 < nkb) x_stage(kb + 3, Xb + V3_XBUF);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (m < mlen) A.out[(size_t)meta.slot[m] * A.H + orow] = acc[ms][i] * meta.fwd[m];
         }
 }
 
@@ -645,10 +850,10 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_gu_kernel(PfGemmArgs A)
     const int ty = (G.gq6 ? 2 : 0) | (G.uq6 ? 1 : 0);
 #define GU_CASE(M)                                                                   \
     if (ms == M) {                                                                   \
-        if (ty == 3) v4_gu_body<M, true, true>(A, G, meta, mlen, j0, lds4);          \
-        else if (ty == 2) v4_gu_body<M, true, false>(A, G, meta, mlen, j0, lds4);   \
-        else if (ty == 1) v4_gu_body<M, false, true>(A, G, meta, mlen, j0, lds4);   \
-        else v4_gu_body<M, false, false>(A, G, meta, mlen, j0, lds4);               \
+        if (ty == 3) v5_gu_body<M, true, true>(A, G, meta, mlen, j0, lds4);          \
+        else if (ty == 2) v5_gu_body<M, true, false>(A, G, meta, mlen, j0, lds4);   \
+        else if (ty == 1) v5_gu_body<M, false, true>(A, G, meta, mlen, j0, lds4);   \
+        else v5_gu_body<M, false, false>(A, G, meta, mlen, j0, lds4);               \
         return;                                                                      \
     }
     GU_CASE(1)
@@ -684,8 +889,8 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
     const int ms = (mlen + 31) >> 5;
 #define DN_CASE(M)                                                                   \
     if (ms == M) {                                                                   \
-        if (G.dq6) v4_dn_body<M, true>(A, G, meta, mlen, n0, lds4);                 \
-        else v4_dn_body<M, false>(A, G, meta, mlen, n0, lds4);                      \
+        if (G.dq6) v5_dn_body<M, true>(A, G, meta, mlen, n0, lds4);                 \
+        else v5_dn_body<M, false>(A, G, meta, mlen, n0, lds4);                      \
         return;                                                                      \
     }
     DN_CASE(1)
@@ -715,7 +920,7 @@ int pf_gemm_launch(const PfGemmArgs &A, int max_tiles, int op)
     if (op == PF_SPLIT) return launch_v1<PF_SPLIT>(A, max_tiles);
     if (op == PF_BF16) return launch_v1<PF_BF16>(A, max_tiles);
     RtState &R = rt();
-    const size_t lds_gu = 2 * (size_t)V3_XBUF * 2 + V3_WBYTES, lds_dn = lds_gu;
+    const size_t lds_gu = 2 * (size_t)V3_XBUF * 2, lds_dn = lds_gu;
     hipLaunchKernelGGL(pf2_gu_kernel, dim3(max_tiles * (A.I / V2_GU_J)), dim3(V2_T), lds_gu, R.stream, A);
     if (rt_check(hipGetLastError(), "prefill gate/up launch")) return ROASTER_EDEVICE;
     hipLaunchKernelGGL(pf2_down_kernel, dim3(max_tiles * (A.H / V2_DN_N)), dim3(V2_T), lds_dn, R.stream, A);

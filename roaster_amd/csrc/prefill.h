@@ -14,6 +14,7 @@
 
 struct PfGroup {
     const uint8_t *g, *u, *d;      /* gate [I x H], up [I x H], down [H x I] */
+    const uint8_t *tg, *tu, *td;   /* the same matrices in the MFMA tile layout (tile.h) */
     int gq6, uq6, dq6;
     int n;                          /* rows */
     int slot0;                      /* first slot */

@@ -233,7 +233,9 @@ extern "C" __global__ void __launch_bounds__(256) pf_bucket_kernel(const int *id
 /* ---- plan: offsets, groups, tiles ----------------------------------------- */
 struct PfPlanArgs {
     DecLayer L;
+    TileLayer TL;
     size_t eb_g, eb_u, eb_d;    /* per-expert matrix bytes */
+    size_t teb_g, teb_u, teb_d; /* per-expert tile-layout bytes */
     int q6g, q6u, q6d, sq6g, sq6u, sq6d;
     const int *cnt;
     const int *list;
@@ -262,6 +264,9 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
         G.g = A.L.gate + (size_t)e * A.eb_g;
         G.u = A.L.up + (size_t)e * A.eb_u;
         G.d = A.L.down + (size_t)e * A.eb_d;
+        G.tg = A.TL.gate + (size_t)e * A.teb_g;
+        G.tu = A.TL.up + (size_t)e * A.teb_u;
+        G.td = A.TL.down + (size_t)e * A.teb_d;
         G.gq6 = A.q6g; G.uq6 = A.q6u; G.dq6 = A.q6d;
         G.n = c;
         G.slot0 = off;
@@ -275,6 +280,7 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
     if (e == 0) {
         PfGroup G;
         G.g = A.L.sgate; G.u = A.L.sup; G.d = A.L.sdown;
+        G.tg = A.TL.sgate; G.tu = A.TL.sup; G.td = A.TL.sdown;
         G.gq6 = A.sq6g; G.uq6 = A.sq6u; G.dq6 = A.sq6d;
         G.n = A.T;
         G.slot0 = 8 * A.T;
@@ -409,7 +415,9 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
 
     PfPlanArgs pa;
     pa.L = L;
+    pa.TL = t->tlayers_h[layer];
     pa.eb_g = t->eb[0]; pa.eb_u = t->eb[1]; pa.eb_d = t->eb[2];
+    pa.teb_g = t->teb[0]; pa.teb_u = t->teb[1]; pa.teb_d = t->teb[2];
     pa.q6g = t->d.q6[0]; pa.q6u = t->d.q6[1]; pa.q6d = t->d.q6[2];
     pa.sq6g = t->d.sh_q6[0]; pa.sq6u = t->d.sh_q6[1]; pa.sq6d = t->d.sh_q6[2];
     pa.cnt = (const int *)(ws + o_cnt);

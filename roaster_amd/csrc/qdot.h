@@ -57,6 +57,7 @@ __device__ __forceinline__ uint2 gld_u2a2(const void *p)
     return make_uint2(v.x, v.y);
 }
 __device__ __forceinline__ uint32_t gld_u16(const void *p) { return *(const GAS uint16_t *)p; }
+__device__ __forceinline__ uint32_t gld_u32(const void *p) { return *(const GAS uint32_t *)p; }
 __device__ __forceinline__ float4 gld_f4(const void *p)
 {
     const gf32x4 v = *(const GAS gf32x4 *)p;

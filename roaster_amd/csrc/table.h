@@ -7,6 +7,12 @@
 #include <vector>
 #include "decode.h"
 
+/* Device addresses of one layer's matrices in the MFMA tile layout (tile.h). */
+struct TileLayer {
+    const uint8_t *gate, *up, *down;      /* [E] consecutive matrices */
+    const uint8_t *sgate, *sup, *sdown;
+};
+
 struct RoasterTable {
     RoasterTableDesc d;
     size_t eb[3];            /* bytes of one routed expert's gate / up / down */
@@ -19,6 +25,11 @@ struct RoasterTable {
     float *fmem = nullptr;   /* routers and gate vectors */
     std::vector<DecLayer> layers_h;
     DecLayer *layers_d = nullptr;
+    /* the same matrices in the MFMA tile layout (prefill GEMM operands) */
+    size_t teb[3], tsb[3], toff_exps[3], toff_sh[3];
+    size_t tlayer_bytes, tbytes;
+    uint8_t *tmem = nullptr;
+    std::vector<TileLayer> tlayers_h;
 };
 
 #endif

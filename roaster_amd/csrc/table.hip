@@ -7,11 +7,15 @@
  * is exactly the GGUF 3-D *_exps tensor (weights.c:380-419 slices expert e at
  * e * size / E), followed by the shared expert's three matrices.  Routers
  * ([E x H] f32) and shared-gate vectors ([H] f32) sit in a second allocation.
+ * A third allocation holds every matrix again in the MFMA tile layout of
+ * tile.h (same order), rebuilt on the device after every upload; the prefill
+ * GEMMs read only that copy, decode only the GGML copy.
  */
 #include "internal.h"
 #include "decode.h"
 #include "table.h"
 #include "synth.h"
+#include "tile.h"
 
 #include <math.h>
 #include <stdlib.h>
@@ -44,12 +48,25 @@ extern "C" RoasterTable *roaster_table_create(const RoasterTableDesc *d)
     t->layer_bytes = off;
     t->qbytes = off * (size_t)d->n_layers;
     t->fbytes = (size_t)d->n_layers * (E * H + H) * sizeof(float);
+    t->teb[0] = tl_mat_bytes(d->q6[0], I, H);
+    t->teb[1] = tl_mat_bytes(d->q6[1], I, H);
+    t->teb[2] = tl_mat_bytes(d->q6[2], H, I);
+    t->tsb[0] = tl_mat_bytes(d->sh_q6[0], I, H);
+    t->tsb[1] = tl_mat_bytes(d->sh_q6[1], I, H);
+    t->tsb[2] = tl_mat_bytes(d->sh_q6[2], H, I);
+    off = 0;
+    for (int k = 0; k < 3; k++) { t->toff_exps[k] = off; off += align256(E * t->teb[k]); }
+    for (int k = 0; k < 3; k++) { t->toff_sh[k] = off; off += align256(t->tsb[k]); }
+    t->tlayer_bytes = off;
+    t->tbytes = off * (size_t)d->n_layers;
     if (hipMalloc((void **)&t->qmem, t->qbytes + RT_TAIL_PAD) != hipSuccess ||
+        hipMalloc((void **)&t->tmem, t->tbytes + RT_TAIL_PAD) != hipSuccess ||
         hipMalloc((void **)&t->fmem, t->fbytes) != hipSuccess ||
         hipMalloc((void **)&t->layers_d, sizeof(DecLayer) * d->n_layers) != hipSuccess) {
         (void)hipGetLastError();
-        rt_fail(ROASTER_ENOMEM, "expert table of %zu bytes does not fit in HBM", t->qbytes + t->fbytes);
+        rt_fail(ROASTER_ENOMEM, "expert table of %zu bytes does not fit in HBM", t->qbytes + t->tbytes + t->fbytes);
         if (t->qmem) (void)hipFree(t->qmem);
+        if (t->tmem) (void)hipFree(t->tmem);
         if (t->fmem) (void)hipFree(t->fmem);
         delete t;
         return NULL;
@@ -57,6 +74,7 @@ extern "C" RoasterTable *roaster_table_create(const RoasterTableDesc *d)
     rt_register_device_range(t->qmem, t->qbytes);
     rt_register_device_range(t->fmem, t->fbytes);
     t->layers_h.resize(d->n_layers);
+    t->tlayers_h.resize(d->n_layers);
     for (int l = 0; l < d->n_layers; l++) {
         DecLayer &L = t->layers_h[l];
         uint8_t *base = t->qmem + (size_t)l * t->layer_bytes;
@@ -68,6 +86,14 @@ extern "C" RoasterTable *roaster_table_create(const RoasterTableDesc *d)
         L.sdown = base + t->off_sh[2];
         L.router = t->fmem + (size_t)l * (E * H + H);
         L.gate_inp = L.router + E * H;
+        TileLayer &TL = t->tlayers_h[l];
+        uint8_t *tbase = t->tmem + (size_t)l * t->tlayer_bytes;
+        TL.gate = tbase + t->toff_exps[0];
+        TL.up = tbase + t->toff_exps[1];
+        TL.down = tbase + t->toff_exps[2];
+        TL.sgate = tbase + t->toff_sh[0];
+        TL.sup = tbase + t->toff_sh[1];
+        TL.sdown = tbase + t->toff_sh[2];
     }
     if (rt_check(hipMemcpy(t->layers_d, t->layers_h.data(), sizeof(DecLayer) * d->n_layers, hipMemcpyHostToDevice),
                  "layer table upload")) {
@@ -85,12 +111,13 @@ extern "C" void roaster_table_destroy(RoasterTable *t)
     rt_unregister_device_range(t->qmem);
     rt_unregister_device_range(t->fmem);
     (void)hipFree(t->qmem);
+    (void)hipFree(t->tmem);
     (void)hipFree(t->fmem);
     (void)hipFree(t->layers_d);
     delete t;
 }
 
-extern "C" size_t roaster_table_bytes(const RoasterTable *t) { return t ? t->qbytes + t->fbytes : 0; }
+extern "C" size_t roaster_table_bytes(const RoasterTable *t) { return t ? t->qbytes + t->tbytes + t->fbytes : 0; }
 
 static uint8_t *mat_ptr(const RoasterTable *t, int layer, int expert, int kind)
 {
@@ -104,6 +131,69 @@ static size_t mat_bytes(const RoasterTable *t, int expert, int kind)
     return expert == t->d.n_experts ? t->sb[kind] : t->eb[kind];
 }
 
+/* ---- MFMA tile layout ------------------------------------------------------ */
+__device__ __forceinline__ uint32_t rd32(const uint8_t *p)
+{
+    return p[0] | (p[1] << 8) | (p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+/* One thread per lane record of nmat consecutive [rows x cols] matrices
+ * (tile.h): record (m, tile g * nkb + kb, lane n + 32 h) from GGML block
+ * (row 32 g + n, kb) of matrix m. */
+__global__ void tile_repack_kernel(const uint8_t *src, uint8_t *dst, size_t src_mat, size_t dst_mat, int rows,
+                                   int cols, int nmat, int q6)
+{
+    const int nkb = cols / RQK;
+    const size_t per_mat = (size_t)(rows / TL_ROWS) * nkb * 64, total = per_mat * (size_t)nmat;
+    const size_t bb = q6 ? RQ6K_BYTES : RQ4K_BYTES;
+    for (size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x; gid < total;
+         gid += (size_t)gridDim.x * blockDim.x) {
+        const size_t m = gid / per_mat, rem = gid % per_mat, tt = rem / 64;
+        const int l = (int)(rem % 64), n = l & 31, h = l >> 5;
+        const int kb = (int)(tt % nkb), g = (int)(tt / nkb);
+        const uint8_t *blk = src + m * src_mat + ((size_t)(TL_ROWS * g + n) * nkb + kb) * bb;
+        uint8_t *tile = dst + m * dst_mat + tt * TL_BYTES(q6);
+        uint32_t rec[27];
+        if (q6) {
+            for (int i = 0; i < 16; i++) rec[i] = rd32(blk + 4 * (16 * h + i));
+            for (int i = 0; i < 8; i++) rec[16 + i] = rd32(blk + 128 + 4 * (8 * h + i));
+            rec[24] = rd32(blk + 192 + 8 * h);
+            rec[25] = rd32(blk + 196 + 8 * h);
+            rec[26] = blk[208] | (blk[209] << 8);
+        } else {
+            for (int i = 0; i < 4; i++) rec[i] = rd32(blk + 4 * i);
+            for (int i = 0; i < 16; i++) rec[4 + i] = rd32(blk + 16 + 4 * (16 * h + i));
+        }
+        const int nq = 4 * TL_SLICES(q6);
+        for (int q = 0; q < nq; q++) *(uint32_t *)(tile + 1024 * (q / 4) + 16 * l + 4 * (q % 4)) = rec[q];
+        if (q6)
+            for (int q = 24; q < 27; q++) *(uint32_t *)(tile + TL_Q6_TAIL + 12 * l + 4 * (q - 24)) = rec[q];
+    }
+}
+
+static uint8_t *tmat_ptr(const RoasterTable *t, int layer, int expert, int kind)
+{
+    uint8_t *base = t->tmem + (size_t)layer * t->tlayer_bytes;
+    if (expert == t->d.n_experts) return base + t->toff_sh[kind];
+    return base + t->toff_exps[kind] + (size_t)expert * t->teb[kind];
+}
+
+/* Rebuild the tile copy of nmat consecutive matrices of one kind (routed
+ * experts e0 .. e0 + nmat - 1, or the shared expert when e0 == E). */
+static int tile_repack(const RoasterTable *t, int layer, int e0, int nmat, int kind)
+{
+    const RoasterTableDesc &d = t->d;
+    const bool sh = e0 == d.n_experts;
+    const int q6 = sh ? d.sh_q6[kind] : d.q6[kind];
+    const int rows = kind == 2 ? d.hidden : d.inter, cols = kind == 2 ? d.inter : d.hidden;
+    const size_t total = (size_t)(rows / TL_ROWS) * (cols / RQK) * 64 * (size_t)nmat;
+    const int blocks = (int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
+    hipLaunchKernelGGL(tile_repack_kernel, dim3(blocks), dim3(256), 0, rt().stream, mat_ptr(t, layer, e0, kind),
+                       tmat_ptr(t, layer, e0, kind), mat_bytes(t, e0, kind), sh ? t->tsb[kind] : t->teb[kind], rows,
+                       cols, nmat, q6);
+    return rt_check(hipGetLastError(), "tile repack launch") ? ROASTER_EDEVICE : 0;
+}
+
 extern "C" int roaster_table_set_expert(RoasterTable *t, int layer, int expert, const void *gate, const void *up,
                                         const void *down)
 {
@@ -111,11 +201,13 @@ extern "C" int roaster_table_set_expert(RoasterTable *t, int layer, int expert, 
     if (!t || layer < 0 || layer >= t->d.n_layers || expert < 0 || expert > t->d.n_experts || !gate || !up || !down)
         return rt_fail(ROASTER_EINVAL, "roaster_table_set_expert: bad arguments");
     const void *src[3] = { gate, up, down };
-    for (int k = 0; k < 3; k++)
+    for (int k = 0; k < 3; k++) {
         if (rt_check(hipMemcpy(mat_ptr(t, layer, expert, k), src[k], mat_bytes(t, expert, k), hipMemcpyHostToDevice),
                      "expert upload"))
             return ROASTER_EDEVICE;
-    return 0;
+        if (int rc = tile_repack(t, layer, expert, 1, k)) return rc;
+    }
+    return rt_check(hipStreamSynchronize(rt().stream), "tile repack") ? ROASTER_EDEVICE : 0;
 }
 
 extern "C" int roaster_table_set_exps(RoasterTable *t, int layer, int kind, const void *data, size_t bytes)
@@ -125,8 +217,10 @@ extern "C" int roaster_table_set_exps(RoasterTable *t, int layer, int kind, cons
         bytes != (size_t)t->d.n_experts * t->eb[kind])
         return rt_fail(ROASTER_EINVAL, "roaster_table_set_exps: bad arguments (expected %zu bytes)",
                        t ? (size_t)t->d.n_experts * t->eb[kind < 0 || kind > 2 ? 0 : kind] : 0);
-    return rt_check(hipMemcpy(mat_ptr(t, layer, 0, kind), data, bytes, hipMemcpyHostToDevice), "exps upload")
-               ? ROASTER_EDEVICE : 0;
+    if (rt_check(hipMemcpy(mat_ptr(t, layer, 0, kind), data, bytes, hipMemcpyHostToDevice), "exps upload"))
+        return ROASTER_EDEVICE;
+    if (int rc = tile_repack(t, layer, 0, t->d.n_experts, kind)) return rc;
+    return rt_check(hipStreamSynchronize(rt().stream), "tile repack") ? ROASTER_EDEVICE : 0;
 }
 
 extern "C" int roaster_table_set_router(RoasterTable *t, int layer, const float *router, const float *gate_inp)
@@ -233,6 +327,7 @@ extern "C" int roaster_table_synth(RoasterTable *t, uint64_t seed, const Roaster
                 hipLaunchKernelGGL(synth_blocks_kernel, dim3(blocks), dim3(256), 0, st, dst, mb, bpm, nmat, seed, l,
                                    e0, k, q6, lo, hi);
                 if (rt_check(hipGetLastError(), "synth launch")) return ROASTER_EDEVICE;
+                if (int rc = tile_repack(t, l, e0, nmat, k)) return rc;
             }
         }
     }
