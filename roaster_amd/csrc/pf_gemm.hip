@@ -670,17 +670,21 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
     constexpr int TG = TL_BYTES(QG), TU = TL_BYTES(QU);
     const uint8_t *wt = up ? G.tu + (size_t)(jrow / TL_ROWS) * nkb * TU : G.tg + (size_t)(jrow / TL_ROWS) * nkb * TG;
     const int tb = up ? TU : TG;
+    /* activation staging: rows >= mlen read row 0 (their products are never
+     * stored), so every load is unconditional and the K loop has no branches
+     * around its loads */
     constexpr int NP = (MS * 32 * 32 + V2_T - 1) / V2_T;
     uint4 xr[NP];
-    const uint16_t *xrow[NP];
+    uint32_t xoff[NP];                  /* byte offsets into X16 (< 2^28: T <= 65536, H <= 2048) */
 #pragma unroll
     for (int i = 0; i < NP; i++) {
         const int idx = t + i * V2_T, row = idx >> 5;
-        xrow[i] = row < mlen ? A.X16 + (size_t)meta.tok[row] * A.H + 8 * (idx & 31) : nullptr;
+        xoff[i] = 2u * ((uint32_t)meta.tok[row < mlen ? row : 0] * (uint32_t)A.H + 8u * (idx & 31));
     }
+    const uint8_t *x16 = (const uint8_t *)A.X16;
     auto x_load = [&](int kb) {
 #pragma unroll
-        for (int i = 0; i < NP; i++) xr[i] = xrow[i] ? gld_u4(xrow[i] + kb * GK) : make_uint4(0u, 0u, 0u, 0u);
+        for (int i = 0; i < NP; i++) xr[i] = gld_u4(x16 + xoff[i] + 2 * kb * GK);
     };
     auto x_store = [&](_Float16 *dst) {
 #pragma unroll
@@ -698,36 +702,45 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
         if (QG == QU || !up) tile_load(rg[buf], wt + (size_t)kb * tb, tlane);
         else tile_load(ru[buf], wt + (size_t)kb * tb, tlane);
     };
+    /* a step's MFMA work; the scheduling fences keep the next step's loads
+     * ahead of it and the activation store (which waits for those loads)
+     * after it */
     auto step = [&](int buf, const _Float16 *Xs) {
+        __builtin_amdgcn_sched_barrier(0);
         if (QG == QU) v4_mfma<MS, QG>(acc, Xs, rg[buf], h);
         else if (up) v4_mfma<MS, QU>(acc, Xs, ru[buf], h);
         else v4_mfma<MS, QG>(acc, Xs, rg[buf], h);
+        __builtin_amdgcn_sched_barrier(0);
     };
     w_load(0, 0);
     x_load(0);
     x_store(Xb);
     __syncthreads();
-    for (int kb = 0; kb < nkb; kb += 2) {
-        /* step kb: raw buffer 0, activation buffer 0 */
-        const bool m1 = kb + 1 < nkb;
-        if (m1) {
-            w_load(1, kb + 1);
-            x_load(kb + 1);
-        }
+    /* steady state: steps kb (raw buffer 0, activation buffer 0) and kb + 1
+     * (buffers 1), each issuing the next step's loads first */
+    int kb = 0;
+    for (; kb + 2 < nkb; kb += 2) {
+        w_load(1, kb + 1);
+        x_load(kb + 1);
         step(0, Xb);
-        if (!m1) break;
         x_store(Xb + V3_XBUF);
         __syncthreads();
-        /* step kb + 1: raw buffer 1, activation buffer 1 */
-        const bool m2 = kb + 2 < nkb;
-        if (m2) {
-            w_load(0, kb + 2);
-            x_load(kb + 2);
-        }
+        w_load(0, kb + 2);
+        x_load(kb + 2);
         step(1, Xb + V3_XBUF);
-        if (!m2) break;
         x_store(Xb);
         __syncthreads();
+    }
+    /* last one or two steps */
+    if (kb + 1 < nkb) {
+        w_load(1, kb + 1);
+        x_load(kb + 1);
+        step(0, Xb);
+        x_store(Xb + V3_XBUF);
+        __syncthreads();
+        step(1, Xb + V3_XBUF);
+    } else {
+        step(0, Xb);
     }
     /* epilogue: as in v4 */
     const int npart = A.I / 16, part = (j0 + 16 * w) >> 4;
