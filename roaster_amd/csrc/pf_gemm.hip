@@ -35,6 +35,12 @@
 #include "tile.h"
 
 static __device__ __forceinline__ float pf_silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+/* The exponent s of row_scale(amax): fwd = 2^s, clamped to [-100, 100]. */
+static __device__ __forceinline__ int pf_scale_exp(float amax)
+{
+    const int s = (int)((__builtin_bit_cast(uint32_t, amax) >> 23) & 255u) - 127 - 14;
+    return s < -100 ? -100 : (s > 100 ? 100 : s);
+}
 /* SiLU(g) * u with the hardware exp and reciprocal (a few ulp in f32; the
  * result is rounded to fp16 for the next GEMM anyway). */
 static __device__ __forceinline__ float pf_silu_mul_fast(float g, float u) { return g * __frcp_rn(1.0f + __expf(-g)) * u; }
@@ -197,6 +203,7 @@ __global__ void __launch_bounds__(GT) pf_down_kernel(PfGemmArgs A)
 #define V2_LD (GK + 8)            /* LDS row stride (fp16 elements) */
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 /* One lane's raw share of a super-block: half h (weights 128h .. 128h+127). */
 struct RawQ6 { uint32_t L[16], Hh[8], S[2], d; };
@@ -429,10 +436,12 @@ __device__ __forceinline__ void v4_lane_raw(typename RawOf<Q6>::T &r, const uint
     raw_from_lds(r, (const uint32_t *)(Wb + c * V3_CH) + (a >> 2), a & 3, h);
 }
 
+#define V5_MAXPART 128                 /* inter / 16 for inter <= 2048 */
 struct V4Shared {
     int tok[V2_MC];
     int slot[V2_MC];
     float inv[V2_MC], fwd[V2_MC];
+    int8_t psh[V2_MC][V5_MAXPART];     /* down: part scale exponent - row scale exponent (<= 0) */
 };
 
 template <int MS, bool QG, bool QU>
@@ -742,7 +751,13 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
     } else {
         step(0, Xb);
     }
-    /* epilogue: as in v4 */
+    /* epilogue: lane n < 16 holds gate and lane n + 16 up of column col.  For
+     * the row pair (i, i + 1) one swizzle (lane ^ 16) gives lanes n < 16 the up
+     * value of row i and lanes n >= 16 the gate value of row i + 1, so all 32
+     * lanes compute act = silu(gate) * up (f32) for one row each; a 16-lane max
+     * gives the row's largest |act| over this wave's 16 columns (one part),
+     * stored to pmax[slot][part], and act is stored in fp16 scaled by that
+     * part's power of two (row_scale of the part max). */
     const int npart = A.I / 16, part = (j0 + 16 * w) >> 4;
     const int col = j0 + 16 * w + (n & 15);
 #pragma unroll
@@ -758,14 +773,18 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
             if (m < mlen) {
                 const float f = meta.fwd[m];
                 e = pf_silu_mul_fast(gsum * f, usum * f);
-                A.act[(size_t)meta.slot[m] * A.I + col] = e;
             }
             float mx = fabsf(e);
             mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
             mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
             mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
             mx = fmaxf(mx, dpp_f<DPP_MIRROR>(mx));
-            if ((n & 15) == 0 && m < mlen) A.pmax[(size_t)meta.slot[m] * npart + part] = mx;
+            if (m < mlen) {
+                float pinv, pfwd;
+                row_scale(mx, pinv, pfwd);
+                A.act16[(size_t)meta.slot[m] * A.I + col] = __builtin_bit_cast(uint16_t, (_Float16)(e * pinv));
+                if ((n & 15) == 0) A.pmax[(size_t)meta.slot[m] * npart + part] = mx;
+            }
         }
 }
 
@@ -781,22 +800,30 @@ __device__ __forceinline__ void v5_dn_body(const PfGemmArgs &A, const PfGroup &G
     constexpr int TD = TL_BYTES(QD);
     const int orow = n0 + 32 * w + n;
     const uint8_t *wt = G.td + (size_t)((n0 + 32 * w) / TL_ROWS) * nkb * TD;
+    /* activation staging: act16 rows (natural order, each 16-column part at
+     * its own power of two) -> fp16 at the row's power of two (ldexp by the
+     * part's shift, exact unless the value turns subnormal), in the permuted K
+     * order; 4-element pieces idx = t + i * V2_T, row idx / 64 */
     constexpr int NP = MS * 32 * 64 / V2_T;
+    const uint8_t *a16 = (const uint8_t *)A.act16;
     auto x_stage = [&](int kb, _Float16 *dst) {
-        float4 xr[NP];
+        uint2 xr[NP];
 #pragma unroll
         for (int i = 0; i < NP; i++) {
             const int idx = t + i * V2_T, row = idx >> 6;
-            xr[i] = row < mlen ? gld_f4(A.act + (size_t)meta.slot[row] * A.I + kb * GK + 4 * (idx & 63))
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int slot = meta.slot[row < mlen ? row : 0];
+            xr[i] = gld_u2(a16 + 2 * ((size_t)slot * A.I + kb * GK + 4 * (idx & 63)));
         }
 #pragma unroll
         for (int i = 0; i < NP; i++) {
-            const int idx = t + i * V2_T, row = idx >> 6;
-            const float s = row < mlen ? meta.inv[row] : 0.0f;
-            const f32x8 e = { xr[i].x * s, xr[i].y * s, xr[i].z * s, xr[i].w * s, 0.f, 0.f, 0.f, 0.f };
+            const int idx = t + i * V2_T, row = idx >> 6, c4 = 4 * (idx & 63);
+            const int sh = row < mlen ? (int)meta.psh[row][(kb * GK + c4) >> 4] : -200;
+            const f16x4 hv = __builtin_bit_cast(f16x4, xr[i]);
+            const f32x8 e = { __builtin_ldexpf((float)hv[0], sh), __builtin_ldexpf((float)hv[1], sh),
+                              __builtin_ldexpf((float)hv[2], sh), __builtin_ldexpf((float)hv[3], sh),
+                              0.f, 0.f, 0.f, 0.f };
             const uint4 cu = __builtin_bit_cast(uint4, __builtin_convertvector(e, f16x8));
-            *(uint2 *)(dst + row * V2_LD + perm_slot4(4 * (idx & 63))) = make_uint2(cu.x, cu.y);
+            *(uint2 *)(dst + row * V2_LD + perm_slot4(c4)) = make_uint2(cu.x, cu.y);
         }
     };
     f32x16 acc[MS];
@@ -896,6 +923,10 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
         meta.slot[t] = slot;
         meta.inv[t] = inv;
         meta.fwd[t] = fwd;
+        /* shift of part b: exponent of its scale minus the row's (fp16 mode) */
+        const int er = pf_scale_exp(mx);
+        for (int b = 0; b < nb && b < V5_MAXPART; b++)
+            meta.psh[t][b] = (int8_t)max(pf_scale_exp(A.pmax[(size_t)slot * nb + b]) - er, -64);   /* 2^-64: 0 in fp16 */
     }
     __syncthreads();
     const int n0 = (v % nblk) * V2_DN_N;

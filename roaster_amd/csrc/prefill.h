@@ -34,7 +34,9 @@ struct PfGemmArgs {
     const float *X;                 /* [* x H] activations (f32, natural order) */
     const uint16_t *X16;            /* [* x H] fp16 activations, scaled, permuted (v2), or NULL */
     const float *xinv, *xfwd;       /* per X row power-of-two scales (fp16 mode), or NULL */
-    float *act;                     /* [slots x I]: silu(gate) * up */
+    float *act;                     /* [slots x I]: silu(gate) * up (f32 operand modes) */
+    uint16_t *act16;                /* [slots x I]: the same in fp16, each 16-column part scaled by the
+                                       power of two of its pmax entry (fp16 mode) */
     float *pmax;                    /* [slots][inter / 16] partial max |act| (fp16 mode) */
     float *out;                     /* [slots x H]: down products */
     int H, I;

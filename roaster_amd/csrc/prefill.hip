@@ -441,6 +441,7 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     ga.xinv = ta.xinv;
     ga.xfwd = ta.xfwd;
     ga.act = (float *)(ws + o_act);
+    ga.act16 = (uint16_t *)(ws + o_act);
     ga.pmax = op == PF_F16 ? (float *)(ws + o_pmax) : nullptr;
     ga.out = (float *)(ws + o_ed);
     ga.H = H; ga.I = I;

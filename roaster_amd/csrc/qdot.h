@@ -51,6 +51,11 @@ __device__ __forceinline__ uint4 gld_u4a2(const void *p)        /* 2-byte aligne
     const gu32x4 v = *(const GAS gu32x4_a2 *)p;
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ uint2 gld_u2(const void *p)           /* 8-byte aligned */
+{
+    const gu32x2 v = *(const GAS gu32x2 *)p;
+    return make_uint2(v.x, v.y);
+}
 __device__ __forceinline__ uint2 gld_u2a2(const void *p)
 {
     const gu32x2 v = *(const GAS gu32x2_a2 *)p;
