@@ -65,6 +65,10 @@ typedef struct {
 typedef struct RoasterTable RoasterTable;
 
 RoasterTable *roaster_table_create(const RoasterTableDesc *desc);
+/* The same with per-layer matrix types, as quantised GGUF files mix them:
+ * types[6 * layer + k] for k = routed gate, up, down, shared gate, up, down
+ * (0 = Q4_K, 1 = Q6_K); NULL = desc's types in every layer. */
+RoasterTable *roaster_table_create_layers(const RoasterTableDesc *desc, const int *types);
 void   roaster_table_destroy(RoasterTable *t);
 size_t roaster_table_bytes(const RoasterTable *t);
 /* Upload one expert's three matrices from host memory (expert == n_experts is
@@ -79,6 +83,33 @@ int roaster_table_set_router(RoasterTable *t, int layer, const float *router, co
 /* Device addresses of an expert's matrices (usable as kernels.h weight pointers). */
 int roaster_table_expert_ptrs(const RoasterTable *t, int layer, int expert,
                               const void **gate, const void **up, const void **down);
+
+/* ---- GGUF v3 model files (weights.c:657-922 parsing rules) -------------- */
+typedef struct {
+    int      version;         /* 3 */
+    uint64_t n_tensors;
+    uint64_t alignment;       /* general.alignment, default 32 */
+    uint64_t data_offset;     /* file offset of the tensor data section */
+    int      n_layers;        /* layers 0 .. n_layers-1, each with the eight MoE tensors */
+    int      n_experts;       /* dims[2] of the *_exps tensors */
+    size_t   hidden, inter;
+    int      q6[3], sh_q6[3]; /* layer 0's types (0 = Q4_K, 1 = Q6_K) */
+    int      mixed_types;     /* 1 if some layer's types differ from layer 0's */
+    int      router_type;     /* GGML type of blk.0.ffn_gate_inp.weight: 0 F32, 1 F16, 12 Q4_K, 14 Q6_K */
+} RoasterGgufInfo;
+
+/* Parse the header, metadata and tensor table and check the MoE tensors of
+ * every layer: blk.L.ffn_{gate,up,down}_exps.weight (3-D [hidden, inter, E] /
+ * [inter, hidden, E], Q4_K or Q6_K), ffn_gate_inp.weight (router [hidden, E]:
+ * F32, F16, Q4_K or Q6_K), ffn_gate_inp_shexp.weight ([hidden], F32 or F16),
+ * ffn_{gate,up,down}_shexp.weight (2-D, Q4_K or Q6_K).  Host only (no GPU
+ * call).  ROASTER_EINVAL with the reason in roaster_last_error(). */
+int roaster_gguf_scan(const char *path, RoasterGgufInfo *info);
+/* Create an expert table from the file and upload every MoE tensor once:
+ * *_exps tensors whole (the table's routed regions are those tensors byte for
+ * byte), the router and gate vector converted to f32, the shared expert as it
+ * is.  info may be NULL.  NULL on error. */
+RoasterTable *roaster_table_load_gguf(const char *path, RoasterGgufInfo *info);
 
 /* ---- synthetic inputs (deterministic; identical on host and device) ------ */
 typedef struct {

@@ -48,6 +48,13 @@ class RoasterTableDesc(C.Structure):
                 ("inter", C.c_size_t), ("q6", C.c_int * 3), ("sh_q6", C.c_int * 3)]
 
 
+class RoasterGgufInfo(C.Structure):
+    _fields_ = [("version", C.c_int), ("n_tensors", C.c_uint64), ("alignment", C.c_uint64),
+                ("data_offset", C.c_uint64), ("n_layers", C.c_int), ("n_experts", C.c_int),
+                ("hidden", C.c_size_t), ("inter", C.c_size_t), ("q6", C.c_int * 3), ("sh_q6", C.c_int * 3),
+                ("mixed_types", C.c_int), ("router_type", C.c_int)]
+
+
 class RoasterSynthSpec(C.Structure):
     _fields_ = [("q4k_lo", C.c_float), ("q4k_hi", C.c_float), ("q6k_lo", C.c_float),
                 ("q6k_hi", C.c_float), ("router_sigma", C.c_float), ("gate_inp_sigma", C.c_float)]
@@ -105,6 +112,9 @@ _SIG = {
     "roaster_d2h": (C.c_int, [_P, _P, C.c_size_t]),
     "roaster_memset": (C.c_int, [_P, C.c_int, C.c_size_t]),
     "roaster_table_create": (_P, [C.POINTER(RoasterTableDesc)]),
+    "roaster_table_create_layers": (_P, [C.POINTER(RoasterTableDesc), _P]),
+    "roaster_gguf_scan": (C.c_int, [C.c_char_p, C.POINTER(RoasterGgufInfo)]),
+    "roaster_table_load_gguf": (_P, [C.c_char_p, C.POINTER(RoasterGgufInfo)]),
     "roaster_table_destroy": (None, [_P]),
     "roaster_table_bytes": (C.c_size_t, [_P]),
     "roaster_table_set_expert": (C.c_int, [_P, C.c_int, C.c_int, _P, _P, _P]),

@@ -348,9 +348,6 @@ static void fill_table_args(DecArgs &A, const RoasterTable *t)
     A.E = t->d.n_experts;
     A.H = (int)t->d.hidden;
     A.I = (int)t->d.inter;
-    A.q6g = t->d.q6[0]; A.q6u = t->d.q6[1]; A.q6d = t->d.q6[2];
-    A.sq6g = t->d.sh_q6[0]; A.sq6u = t->d.sh_q6[1]; A.sq6d = t->d.sh_q6[2];
-    A.bytes_g = t->eb[0]; A.bytes_u = t->eb[1]; A.bytes_d = t->eb[2];
 }
 
 static int dec_scratch(DecArgs &A)

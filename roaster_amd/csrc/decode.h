@@ -10,12 +10,16 @@
 
 #define RMAX_ACT (8 * 8 + 1)        /* distinct routed experts of 8 tokens + shared */
 
-/* Device addresses of one layer's tensors in the expert table. */
+/* Device addresses of one layer's tensors in the expert table, with the
+ * layer's matrix types (a GGUF file may quantise layers differently). */
 struct DecLayer {
     const uint8_t *gate, *up, *down;      /* [E][rows][row_bytes], GGUF *_exps layout */
     const uint8_t *sgate, *sup, *sdown;   /* shared expert */
     const float *router;                  /* [E x H] */
     const float *gate_inp;                /* [H] */
+    size_t eb[3];                         /* bytes of one routed expert's gate / up / down */
+    int q6[3];                            /* routed gate / up / down: 0 = Q4_K, 1 = Q6_K */
+    int sq6[3];                           /* shared expert gate / up / down */
 };
 
 /* One active expert of a decode plan: its matrices and the (token, slot)
@@ -43,8 +47,6 @@ struct DecArgs {
     const DecLayer *layers;     /* device array indexed by layer */
     int layer0, nlayers;
     int E, H, I, B;
-    int q6g, q6u, q6d, sq6g, sq6u, sq6d;
-    size_t bytes_g, bytes_u, bytes_d;     /* per-expert matrix bytes */
     float *h;                   /* [B x H]: stack state (in/out), or the layer input */
     float *y;                   /* [B x H] layer output, or NULL in stack mode */
     const float *norm_w;        /* [nlayers x H] or NULL */

@@ -176,7 +176,7 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A,
     const bool is_row = task <= nrouter;
     const int j = task - nrouter - 1;
     const bool is_sh = !is_row && j < I;
-    const int kind = (A.sq6g ? 2 : 0) | (A.sq6u ? 1 : 0);
+    const int kind = (L.sq6[0] ? 2 : 0) | (L.sq6[1] ? 1 : 0);
     if (threadIdx.x < B) sh_tk[threadIdx.x] = threadIdx.x * 9 + 8;
     /* 1. weight loads first (independent of h) */
     float4 w[8];
@@ -269,10 +269,10 @@ __device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, cons
         const int nroute = __popcll(lead_mask);
         if (leader) {
             DecActive &X = P.a[a];
-            X.g = L.gate + (size_t)e * A.bytes_g;
-            X.u = L.up + (size_t)e * A.bytes_u;
-            X.d = L.down + (size_t)e * A.bytes_d;
-            X.gq6 = A.q6g; X.uq6 = A.q6u; X.dq6 = A.q6d;
+            X.g = L.gate + (size_t)e * L.eb[0];
+            X.u = L.up + (size_t)e * L.eb[1];
+            X.d = L.down + (size_t)e * L.eb[2];
+            X.gq6 = L.q6[0]; X.uq6 = L.q6[1]; X.dq6 = L.q6[2];
             int nt = 0;
             for (unsigned long long mm = m; mm; mm &= mm - 1ull) {
                 const int jj = __ffsll((long long)mm) - 1;
@@ -283,7 +283,7 @@ __device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, cons
         if (lane == 0) {
             DecActive &X = P.a[nroute];
             X.g = L.sgate; X.u = L.sup; X.d = L.sdown;
-            X.gq6 = A.sq6g; X.uq6 = A.sq6u; X.dq6 = A.sq6d;
+            X.gq6 = L.sq6[0]; X.uq6 = L.sq6[1]; X.dq6 = L.sq6[2];
             X.ntok = B;
             for (int t = 0; t < B; t++) X.tk[t] = t * 9 + 8;
             P.nroute = nroute;
@@ -428,7 +428,7 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int
      * into a condition that is never true so the load is kept. */
     uint32_t warm = 0;
     if (!A.ffn_out) {
-        const size_t lpe = (size_t)A.H * (A.I / RQK) * (A.q6d ? RQ6K_BYTES : RQ4K_BYTES) / 128;
+        const size_t lpe = (size_t)A.H * (A.I / RQK) * RQ6K_BYTES / 128;   /* lines per expert slot (Q6_K bound) */
         const size_t g = (size_t)blockIdx.x * DT + threadIdx.x;
         const int a = (int)(g / lpe);
         if (a < P.nact) {

@@ -416,10 +416,11 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     PfPlanArgs pa;
     pa.L = L;
     pa.TL = t->tlayers_h[layer];
-    pa.eb_g = t->eb[0]; pa.eb_u = t->eb[1]; pa.eb_d = t->eb[2];
-    pa.teb_g = t->teb[0]; pa.teb_u = t->teb[1]; pa.teb_d = t->teb[2];
-    pa.q6g = t->d.q6[0]; pa.q6u = t->d.q6[1]; pa.q6d = t->d.q6[2];
-    pa.sq6g = t->d.sh_q6[0]; pa.sq6u = t->d.sh_q6[1]; pa.sq6d = t->d.sh_q6[2];
+    const LayerGeo &LG = t->geo[layer];
+    pa.eb_g = LG.eb[0]; pa.eb_u = LG.eb[1]; pa.eb_d = LG.eb[2];
+    pa.teb_g = LG.teb[0]; pa.teb_u = LG.teb[1]; pa.teb_d = LG.teb[2];
+    pa.q6g = LG.q6[0]; pa.q6u = LG.q6[1]; pa.q6d = LG.q6[2];
+    pa.sq6g = LG.sh_q6[0]; pa.sq6u = LG.sh_q6[1]; pa.sq6d = LG.sh_q6[2];
     pa.cnt = (const int *)(ws + o_cnt);
     pa.list = (const int *)(ws + o_list);
     pa.off = (int *)(ws + o_off);

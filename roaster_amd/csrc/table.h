@@ -13,22 +13,25 @@ struct TileLayer {
     const uint8_t *sgate, *sup, *sdown;
 };
 
+/* Types, sizes and offsets of one layer's matrices (types may differ by layer). */
+struct LayerGeo {
+    int q6[3], sh_q6[3];                  /* 0 = Q4_K, 1 = Q6_K */
+    size_t eb[3], sb[3];                  /* GGML bytes: one routed expert's matrix / the shared one's */
+    size_t off_exps[3], off_sh[3];        /* offsets inside the layer's GGML region */
+    size_t teb[3], tsb[3];                /* the same in the tile layout */
+    size_t toff_exps[3], toff_sh[3];
+    size_t base, tbase;                   /* the layer's offsets in qmem / tmem */
+};
+
 struct RoasterTable {
     RoasterTableDesc d;
-    size_t eb[3];            /* bytes of one routed expert's gate / up / down */
-    size_t sb[3];            /* bytes of the shared expert's gate / up / down */
-    size_t off_exps[3];      /* offsets inside a layer */
-    size_t off_sh[3];
-    size_t layer_bytes;
-    size_t qbytes, fbytes;
-    uint8_t *qmem = nullptr; /* quantised matrices, all layers */
+    std::vector<LayerGeo> geo;
+    size_t qbytes, tbytes, fbytes;
+    uint8_t *qmem = nullptr; /* quantised matrices (GGML layout), all layers */
+    uint8_t *tmem = nullptr; /* the same matrices in the MFMA tile layout (prefill GEMM operands) */
     float *fmem = nullptr;   /* routers and gate vectors */
     std::vector<DecLayer> layers_h;
     DecLayer *layers_d = nullptr;
-    /* the same matrices in the MFMA tile layout (prefill GEMM operands) */
-    size_t teb[3], tsb[3], toff_exps[3], toff_sh[3];
-    size_t tlayer_bytes, tbytes;
-    uint8_t *tmem = nullptr;
     std::vector<TileLayer> tlayers_h;
 };
 

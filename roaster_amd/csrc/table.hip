@@ -24,7 +24,9 @@
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-extern "C" RoasterTable *roaster_table_create(const RoasterTableDesc *d)
+/* types: [n_layers][6] = routed gate, up, down, shared gate, up, down (0 = Q4_K,
+ * 1 = Q6_K), or NULL for the description's types in every layer. */
+extern "C" RoasterTable *roaster_table_create_layers(const RoasterTableDesc *d, const int *types)
 {
     std::lock_guard<std::recursive_mutex> g(rt_lock());
     if (rt_init_locked()) return NULL;
@@ -33,32 +35,42 @@ extern "C" RoasterTable *roaster_table_create(const RoasterTableDesc *d)
         rt_fail(ROASTER_EINVAL, "invalid table description");
         return NULL;
     }
+    for (int i = 0; types && i < 6 * d->n_layers; i++)
+        if (types[i] != 0 && types[i] != 1) {
+            rt_fail(ROASTER_EINVAL, "invalid matrix type %d (0 = Q4_K, 1 = Q6_K)", types[i]);
+            return NULL;
+        }
     RoasterTable *t = new RoasterTable();
     t->d = *d;
     const size_t H = d->hidden, I = d->inter, E = (size_t)d->n_experts;
-    t->eb[0] = rq_mat_bytes(d->q6[0], I, H);
-    t->eb[1] = rq_mat_bytes(d->q6[1], I, H);
-    t->eb[2] = rq_mat_bytes(d->q6[2], H, I);
-    t->sb[0] = rq_mat_bytes(d->sh_q6[0], I, H);
-    t->sb[1] = rq_mat_bytes(d->sh_q6[1], I, H);
-    t->sb[2] = rq_mat_bytes(d->sh_q6[2], H, I);
-    size_t off = 0;
-    for (int k = 0; k < 3; k++) { t->off_exps[k] = off; off += align256(E * t->eb[k]); }
-    for (int k = 0; k < 3; k++) { t->off_sh[k] = off; off += align256(t->sb[k]); }
-    t->layer_bytes = off;
-    t->qbytes = off * (size_t)d->n_layers;
+    t->geo.resize(d->n_layers);
+    size_t qoff = 0, toff = 0;
+    for (int l = 0; l < d->n_layers; l++) {
+        LayerGeo &G = t->geo[l];
+        for (int k = 0; k < 3; k++) {
+            G.q6[k] = types ? types[6 * l + k] : (d->q6[k] ? 1 : 0);
+            G.sh_q6[k] = types ? types[6 * l + 3 + k] : (d->sh_q6[k] ? 1 : 0);
+            const size_t rows = k == 2 ? H : I, cols = k == 2 ? I : H;
+            G.eb[k] = rq_mat_bytes(G.q6[k], rows, cols);
+            G.sb[k] = rq_mat_bytes(G.sh_q6[k], rows, cols);
+            G.teb[k] = tl_mat_bytes(G.q6[k], rows, cols);
+            G.tsb[k] = tl_mat_bytes(G.sh_q6[k], rows, cols);
+        }
+        size_t off = 0, tof = 0;
+        for (int k = 0; k < 3; k++) {
+            G.off_exps[k] = off; off += align256(E * G.eb[k]);
+            G.toff_exps[k] = tof; tof += align256(E * G.teb[k]);
+        }
+        for (int k = 0; k < 3; k++) {
+            G.off_sh[k] = off; off += align256(G.sb[k]);
+            G.toff_sh[k] = tof; tof += align256(G.tsb[k]);
+        }
+        G.base = qoff; qoff += off;
+        G.tbase = toff; toff += tof;
+    }
+    t->qbytes = qoff;
+    t->tbytes = toff;
     t->fbytes = (size_t)d->n_layers * (E * H + H) * sizeof(float);
-    t->teb[0] = tl_mat_bytes(d->q6[0], I, H);
-    t->teb[1] = tl_mat_bytes(d->q6[1], I, H);
-    t->teb[2] = tl_mat_bytes(d->q6[2], H, I);
-    t->tsb[0] = tl_mat_bytes(d->sh_q6[0], I, H);
-    t->tsb[1] = tl_mat_bytes(d->sh_q6[1], I, H);
-    t->tsb[2] = tl_mat_bytes(d->sh_q6[2], H, I);
-    off = 0;
-    for (int k = 0; k < 3; k++) { t->toff_exps[k] = off; off += align256(E * t->teb[k]); }
-    for (int k = 0; k < 3; k++) { t->toff_sh[k] = off; off += align256(t->tsb[k]); }
-    t->tlayer_bytes = off;
-    t->tbytes = off * (size_t)d->n_layers;
     if (hipMalloc((void **)&t->qmem, t->qbytes + RT_TAIL_PAD) != hipSuccess ||
         hipMalloc((void **)&t->tmem, t->tbytes + RT_TAIL_PAD) != hipSuccess ||
         hipMalloc((void **)&t->fmem, t->fbytes) != hipSuccess ||
@@ -76,24 +88,30 @@ extern "C" RoasterTable *roaster_table_create(const RoasterTableDesc *d)
     t->layers_h.resize(d->n_layers);
     t->tlayers_h.resize(d->n_layers);
     for (int l = 0; l < d->n_layers; l++) {
+        const LayerGeo &G = t->geo[l];
         DecLayer &L = t->layers_h[l];
-        uint8_t *base = t->qmem + (size_t)l * t->layer_bytes;
-        L.gate = base + t->off_exps[0];
-        L.up = base + t->off_exps[1];
-        L.down = base + t->off_exps[2];
-        L.sgate = base + t->off_sh[0];
-        L.sup = base + t->off_sh[1];
-        L.sdown = base + t->off_sh[2];
+        uint8_t *base = t->qmem + G.base;
+        L.gate = base + G.off_exps[0];
+        L.up = base + G.off_exps[1];
+        L.down = base + G.off_exps[2];
+        L.sgate = base + G.off_sh[0];
+        L.sup = base + G.off_sh[1];
+        L.sdown = base + G.off_sh[2];
         L.router = t->fmem + (size_t)l * (E * H + H);
         L.gate_inp = L.router + E * H;
+        for (int k = 0; k < 3; k++) {
+            L.eb[k] = G.eb[k];
+            L.q6[k] = G.q6[k];
+            L.sq6[k] = G.sh_q6[k];
+        }
         TileLayer &TL = t->tlayers_h[l];
-        uint8_t *tbase = t->tmem + (size_t)l * t->tlayer_bytes;
-        TL.gate = tbase + t->toff_exps[0];
-        TL.up = tbase + t->toff_exps[1];
-        TL.down = tbase + t->toff_exps[2];
-        TL.sgate = tbase + t->toff_sh[0];
-        TL.sup = tbase + t->toff_sh[1];
-        TL.sdown = tbase + t->toff_sh[2];
+        uint8_t *tbase = t->tmem + G.tbase;
+        TL.gate = tbase + G.toff_exps[0];
+        TL.up = tbase + G.toff_exps[1];
+        TL.down = tbase + G.toff_exps[2];
+        TL.sgate = tbase + G.toff_sh[0];
+        TL.sup = tbase + G.toff_sh[1];
+        TL.sdown = tbase + G.toff_sh[2];
     }
     if (rt_check(hipMemcpy(t->layers_d, t->layers_h.data(), sizeof(DecLayer) * d->n_layers, hipMemcpyHostToDevice),
                  "layer table upload")) {
@@ -102,6 +120,8 @@ extern "C" RoasterTable *roaster_table_create(const RoasterTableDesc *d)
     }
     return t;
 }
+
+extern "C" RoasterTable *roaster_table_create(const RoasterTableDesc *d) { return roaster_table_create_layers(d, NULL); }
 
 extern "C" void roaster_table_destroy(RoasterTable *t)
 {
@@ -121,14 +141,16 @@ extern "C" size_t roaster_table_bytes(const RoasterTable *t) { return t ? t->qby
 
 static uint8_t *mat_ptr(const RoasterTable *t, int layer, int expert, int kind)
 {
-    uint8_t *base = t->qmem + (size_t)layer * t->layer_bytes;
-    if (expert == t->d.n_experts) return base + t->off_sh[kind];
-    return base + t->off_exps[kind] + (size_t)expert * t->eb[kind];
+    const LayerGeo &G = t->geo[layer];
+    uint8_t *base = t->qmem + G.base;
+    if (expert == t->d.n_experts) return base + G.off_sh[kind];
+    return base + G.off_exps[kind] + (size_t)expert * G.eb[kind];
 }
 
-static size_t mat_bytes(const RoasterTable *t, int expert, int kind)
+static size_t mat_bytes(const RoasterTable *t, int layer, int expert, int kind)
 {
-    return expert == t->d.n_experts ? t->sb[kind] : t->eb[kind];
+    const LayerGeo &G = t->geo[layer];
+    return expert == t->d.n_experts ? G.sb[kind] : G.eb[kind];
 }
 
 /* ---- MFMA tile layout ------------------------------------------------------ */
@@ -173,9 +195,10 @@ __global__ void tile_repack_kernel(const uint8_t *src, uint8_t *dst, size_t src_
 
 static uint8_t *tmat_ptr(const RoasterTable *t, int layer, int expert, int kind)
 {
-    uint8_t *base = t->tmem + (size_t)layer * t->tlayer_bytes;
-    if (expert == t->d.n_experts) return base + t->toff_sh[kind];
-    return base + t->toff_exps[kind] + (size_t)expert * t->teb[kind];
+    const LayerGeo &G = t->geo[layer];
+    uint8_t *base = t->tmem + G.tbase;
+    if (expert == t->d.n_experts) return base + G.toff_sh[kind];
+    return base + G.toff_exps[kind] + (size_t)expert * G.teb[kind];
 }
 
 /* Rebuild the tile copy of nmat consecutive matrices of one kind (routed
@@ -183,13 +206,14 @@ static uint8_t *tmat_ptr(const RoasterTable *t, int layer, int expert, int kind)
 static int tile_repack(const RoasterTable *t, int layer, int e0, int nmat, int kind)
 {
     const RoasterTableDesc &d = t->d;
+    const LayerGeo &G = t->geo[layer];
     const bool sh = e0 == d.n_experts;
-    const int q6 = sh ? d.sh_q6[kind] : d.q6[kind];
+    const int q6 = sh ? G.sh_q6[kind] : G.q6[kind];
     const int rows = kind == 2 ? d.hidden : d.inter, cols = kind == 2 ? d.inter : d.hidden;
     const size_t total = (size_t)(rows / TL_ROWS) * (cols / RQK) * 64 * (size_t)nmat;
     const int blocks = (int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
     hipLaunchKernelGGL(tile_repack_kernel, dim3(blocks), dim3(256), 0, rt().stream, mat_ptr(t, layer, e0, kind),
-                       tmat_ptr(t, layer, e0, kind), mat_bytes(t, e0, kind), sh ? t->tsb[kind] : t->teb[kind], rows,
+                       tmat_ptr(t, layer, e0, kind), mat_bytes(t, layer, e0, kind), sh ? G.tsb[kind] : G.teb[kind], rows,
                        cols, nmat, q6);
     return rt_check(hipGetLastError(), "tile repack launch") ? ROASTER_EDEVICE : 0;
 }
@@ -202,7 +226,7 @@ extern "C" int roaster_table_set_expert(RoasterTable *t, int layer, int expert, 
         return rt_fail(ROASTER_EINVAL, "roaster_table_set_expert: bad arguments");
     const void *src[3] = { gate, up, down };
     for (int k = 0; k < 3; k++) {
-        if (rt_check(hipMemcpy(mat_ptr(t, layer, expert, k), src[k], mat_bytes(t, expert, k), hipMemcpyHostToDevice),
+        if (rt_check(hipMemcpy(mat_ptr(t, layer, expert, k), src[k], mat_bytes(t, layer, expert, k), hipMemcpyHostToDevice),
                      "expert upload"))
             return ROASTER_EDEVICE;
         if (int rc = tile_repack(t, layer, expert, 1, k)) return rc;
@@ -213,10 +237,11 @@ extern "C" int roaster_table_set_expert(RoasterTable *t, int layer, int expert, 
 extern "C" int roaster_table_set_exps(RoasterTable *t, int layer, int kind, const void *data, size_t bytes)
 {
     std::lock_guard<std::recursive_mutex> g(rt_lock());
-    if (!t || layer < 0 || layer >= t->d.n_layers || kind < 0 || kind > 2 || !data ||
-        bytes != (size_t)t->d.n_experts * t->eb[kind])
-        return rt_fail(ROASTER_EINVAL, "roaster_table_set_exps: bad arguments (expected %zu bytes)",
-                       t ? (size_t)t->d.n_experts * t->eb[kind < 0 || kind > 2 ? 0 : kind] : 0);
+    if (!t || layer < 0 || layer >= t->d.n_layers || kind < 0 || kind > 2 || !data)
+        return rt_fail(ROASTER_EINVAL, "roaster_table_set_exps: bad arguments");
+    if (bytes != (size_t)t->d.n_experts * t->geo[layer].eb[kind])
+        return rt_fail(ROASTER_EINVAL, "roaster_table_set_exps: expected %zu bytes, got %zu",
+                       (size_t)t->d.n_experts * t->geo[layer].eb[kind], bytes);
     if (rt_check(hipMemcpy(mat_ptr(t, layer, 0, kind), data, bytes, hipMemcpyHostToDevice), "exps upload"))
         return ROASTER_EDEVICE;
     if (int rc = tile_repack(t, layer, 0, t->d.n_experts, kind)) return rc;
@@ -316,11 +341,11 @@ extern "C" int roaster_table_synth(RoasterTable *t, uint64_t seed, const Roaster
             const size_t rows = k == 2 ? H : I, cols = k == 2 ? I : H;
             const size_t bpm = rows * (cols / RQK);
             for (int shared = 0; shared < 2; shared++) {
-                const int q6 = shared ? d.sh_q6[k] : d.q6[k];
+                const int q6 = shared ? t->geo[l].sh_q6[k] : t->geo[l].q6[k];
                 const int nmat = shared ? 1 : (int)E;
                 const int e0 = shared ? (int)E : 0;
                 uint8_t *dst = mat_ptr(t, l, e0, k);
-                const size_t mb = mat_bytes(t, e0, k);
+                const size_t mb = mat_bytes(t, l, e0, k);
                 const float lo = q6 ? s.q6k_lo : s.q4k_lo, hi = q6 ? s.q6k_hi : s.q4k_hi;
                 const size_t total = bpm * (size_t)nmat;
                 const int blocks = (int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
