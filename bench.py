@@ -15,6 +15,8 @@ Also reported in the same JSON line:
               layers with N(0,1) logits given (the MFMA roofline line), and 512
               tokens through one Q4_K/Q6_K layer with the router and a
               Zipf(1.1) per-expert logit bias;
+  dense    -- the LM head [248320 x 2048] Q6_K as a dense projection, 1 and 8
+              tokens, with its HBM roofline;
   roofline / cpu_baseline -- see below.
 Kernel times come from HIP events recorded on the library's stream.  The CPU
 baselines run the reference's own C kernels (compiled from the reference tree
@@ -308,6 +310,32 @@ def prefill_legs(torch, L, R, dev, stream, reps, with_cpu):
     return out
 
 
+def dense_leg(torch, L, R, dev, stream):
+    """The LM head as a dense Q6_K projection [248320 x 2048] (model.c:1368-1370)
+    for 1 and 8 tokens through roaster_matvec_q: device time from HIP events,
+    HBM roofline over the matrix bytes."""
+    rows, cols = 248320, 2048
+    W = R.synth_q6k(5, R.synth_stream(0, 0, 9), rows * (cols // 256))
+    dw = torch.from_numpy(W).to(dev)
+    out = {"workload": "LM head Q6_K [248320 x 2048]", "matrix_bytes": int(W.nbytes)}
+    for T in (1, 8):
+        x = torch.from_numpy(np.stack([R.synth_normal(5, R.synth_stream(0, t, 5), cols) for t in range(T)])).to(dev)
+        y = torch.empty((T, rows), dtype=torch.float32, device=dev)
+
+        def run():
+            rc = L.roaster_matvec_q(dw.data_ptr(), 1, x.data_ptr(), y.data_ptr(), rows, cols, T)
+            if rc:
+                raise RuntimeError(R.last_error())
+        run()
+        R.check(L.roaster_sync(), "dense warmup")
+        ms = event_ms(torch, stream, run, 50)
+        gbs = W.nbytes / (ms * 1e-3) / 1e9
+        out["T%d" % T] = {"us": round(ms * 1e3, 1), "tokens_per_s": round(T / (ms * 1e-3), 1),
+                          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                       "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -396,6 +424,7 @@ def main():
     L.roaster_table_destroy(t)
     if not args.no_prefill:
         line["prefill"] = prefill_legs(torch, L, R, dev, stream, args.prefill_reps, not args.no_cpu)
+    line["dense"] = dense_leg(torch, L, R, dev, stream)
     print(json.dumps(line), flush=True)
 
 

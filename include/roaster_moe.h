@@ -148,6 +148,15 @@ int roaster_moe_decode(RoasterTable *t, int layer, const float *x, int B, float 
 int roaster_moe_decode_stack(RoasterTable *t, float *h, int B, int layer0, int n_layers,
                              const float *norm_w, float eps, int *ids_out, float *w_out);
 
+/* ---- dense projections ---------------------------------------------------- */
+/* Y[t * rows + r] = W[r] . X[t * cols ..] for t < T (1..8): a quantised
+ * [rows x cols] matrix on the device (q6: 0 = Q4_K, 1 = Q6_K, cols a multiple
+ * of 256, at most 2048) -- the projections on either side of the MoE block and
+ * the LM head (model.c:795-800, 1284-1290, 1368-1370), the products
+ * kernel_matvec_q4_k / _q6_k compute from host buffers.  Device pointers;
+ * ordered on the library stream. */
+int roaster_matvec_q(const void *W, int q6, const float *X, float *Y, size_t rows, size_t cols, int T);
+
 /* ---- prefill ------------------------------------------------------------ */
 typedef struct {
     int precision;             /* ROASTER_PREC_F16 (default), _SPLIT or _BF16 */

@@ -114,6 +114,7 @@ _SIG = {
     "roaster_table_create": (_P, [C.POINTER(RoasterTableDesc)]),
     "roaster_table_create_layers": (_P, [C.POINTER(RoasterTableDesc), _P]),
     "roaster_gguf_scan": (C.c_int, [C.c_char_p, C.POINTER(RoasterGgufInfo)]),
+    "roaster_matvec_q": (C.c_int, [_P, C.c_int, _P, _P, C.c_size_t, C.c_size_t, C.c_int]),
     "roaster_table_load_gguf": (_P, [C.c_char_p, C.POINTER(RoasterGgufInfo)]),
     "roaster_table_destroy": (None, [_P]),
     "roaster_table_bytes": (C.c_size_t, [_P]),

@@ -462,7 +462,7 @@ __device__ void down_tasks(const DecArgs &A, const DecPlan &P, int q0, int q1, f
 {
     const int H = A.H, I = A.I, nb = I / RQK;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int lpr = nb >= 8 ? 64 : 8 * nb, rpw = 64 / lpr;
+    const int lpr = lanes_per_row(nb), rpw = 64 / lpr;
     const int rw = lane / lpr, lr = lane % lpr, c = lr & 7, lb = lr >> 3;
     const size_t dbs = D6 ? RQ6K_BYTES : RQ4K_BYTES;
     const int r0 = blockIdx.x * D_ROWS;
@@ -527,7 +527,7 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_down_kernel(DecArgs A, i
         for (int r = tid; r < npair * (I / 16); r += DT) ehs[r] = sum16(ehl + r * 16);
         __syncthreads();
     }
-    const int lpr = nb >= 8 ? 64 : 8 * nb, rpw = 64 / lpr;
+    const int lpr = lanes_per_row(nb), rpw = 64 / lpr;
     const int ngroups = (D_ROWS + rpw - 1) / rpw;
     const int r0 = blockIdx.x * D_ROWS;
     PHASE_TS(2, 1);

@@ -267,6 +267,10 @@ __device__ __forceinline__ void half_max(float v, float &lo, float &hi)
     hi = fmaxf(lane_f(v, 32), lane_f(v, 48));
 }
 
+/* Lanes serving one row of nb super-blocks: 8 per block, rounded up to the
+ * power of two group_sum_w reduces over (lanes past 8 * nb stay idle). */
+__host__ __device__ __forceinline__ int lanes_per_row(int nb) { return nb >= 5 ? 64 : nb >= 3 ? 32 : 8 * nb; }
+
 /* Runtime group width (8, 16, 32 or 64). */
 __device__ __forceinline__ float group_sum_w(float v, int w)
 {
