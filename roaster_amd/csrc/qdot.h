@@ -237,6 +237,8 @@ __device__ __forceinline__ float lane_f(float v, int l)
 #define DPP_XOR2 0x4E          /* quad_perm [2,3,0,1] */
 #define DPP_HALF_MIRROR 0x141  /* lane i <-> 7-i within 8 */
 #define DPP_MIRROR 0x140       /* lane i <-> 15-i within 16 */
+#define DPP_ROW_BCAST15 0x142  /* lane 15 of each row -> the next row (row_mask selects receivers) */
+#define DPP_ROW_BCAST31 0x143  /* lane 31 -> rows 2 and 3 */
 
 /* Sum over aligned groups of W lanes (W a power of two <= 64); every lane of a
  * group receives the group's sum (fixed order, so results are deterministic). */

@@ -30,15 +30,39 @@ __device__ __forceinline__ float key_logit(uint32_t k)
     return __builtin_bit_cast(float, u);
 }
 
+/* Wave reductions (all 64 lanes): DPP within each 16-lane row, then row
+ * broadcasts fold the rows into lane 63, read once into a scalar. */
+__device__ __forceinline__ uint32_t topk_wave_max(uint32_t m)
+{
+    m = max(m, (uint32_t)dpp_i<DPP_XOR1>((int)m));
+    m = max(m, (uint32_t)dpp_i<DPP_XOR2>((int)m));
+    m = max(m, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)m));
+    m = max(m, (uint32_t)dpp_i<DPP_MIRROR>((int)m));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, DPP_ROW_BCAST15, 0xA, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, DPP_ROW_BCAST31, 0xC, 0xF, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)m, 63);
+}
+
+__device__ __forceinline__ int topk_wave_min(int m)
+{
+    m = min(m, dpp_i<DPP_XOR1>(m));
+    m = min(m, dpp_i<DPP_XOR2>(m));
+    m = min(m, dpp_i<DPP_HALF_MIRROR>(m));
+    m = min(m, dpp_i<DPP_MIRROR>(m));
+    m = min(m, __builtin_amdgcn_update_dpp(m, m, DPP_ROW_BCAST15, 0xA, 0xF, false));
+    m = min(m, __builtin_amdgcn_update_dpp(m, m, DPP_ROW_BCAST31, 0xC, 0xF, false));
+    return __builtin_amdgcn_readlane(m, 63);
+}
+
 /* Wave-level top-8 of one token (model.c:869-897).  Each logit becomes an
  * order-preserving 32-bit key (NaN and -inf: key 0, never selected).  Eight
- * rounds each take the wave maximum of the keys (DPP within 16-lane rows, then
- * the four row maxima) and, among the experts holding it, the lowest index
- * (ballot, first set bit): "larger logit, then lower index", the order the
- * reference's strict-greater insertion produces.  The softmax over the selected
- * logits is then summed in slot order like the reference.  v4[i] holds the
- * logit of expert lane + 64*i (E <= 256).  Fewer than 8 selectable logits:
- * the remaining ids are -1 and *bad is set. */
+ * rounds each take the wave maximum M of the keys and then, among the experts
+ * holding M, the lowest index (each lane offers its lowest such index, a wave
+ * minimum picks one): "larger logit, then lower index", the order the
+ * reference's strict-greater insertion produces.  The softmax over the
+ * selected logits is then summed in slot order like the reference.  v4[i]
+ * holds the logit of expert lane + 64*i (E <= 256).  Fewer than 8 selectable
+ * logits: the remaining ids are -1 and *bad is set. */
 static __device__ void topk8_wave(const float v4in[4], int E, int *ids, float *w, int *bad)
 {
     const int lane = threadIdx.x & 63;
@@ -50,21 +74,13 @@ static __device__ void topk8_wave(const float v4in[4], int E, int *ids, float *w
     }
     float v = -INFINITY;
     int myid = -1, nsel = 0;
-    for (int r = 0; r < RTOPK; r++) {
-        uint32_t m = max(max(key[0], key[1]), max(key[2], key[3]));
-        m = max(m, (uint32_t)dpp_i<DPP_XOR1>((int)m));
-        m = max(m, (uint32_t)dpp_i<DPP_XOR2>((int)m));
-        m = max(m, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)m));
-        m = max(m, (uint32_t)dpp_i<DPP_MIRROR>((int)m));
-        const uint32_t M = max(max((uint32_t)__builtin_amdgcn_readlane((int)m, 0), (uint32_t)__builtin_amdgcn_readlane((int)m, 16)),
-                               max((uint32_t)__builtin_amdgcn_readlane((int)m, 32), (uint32_t)__builtin_amdgcn_readlane((int)m, 48)));
-        if (M == 0u) break;                               /* no selectable logit left */
-        int e = -1;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const unsigned long long b = __ballot(key[i] == M);
-            if (e < 0 && b) e = 64 * i + (int)__builtin_ctzll(b);
-        }
+    for (int r = 0; r < RTOPK; r++) {
+        const uint32_t M = topk_wave_max(max(max(key[0], key[1]), max(key[2], key[3])));
+        if (M == 0u) break;                               /* no selectable logit left */
+        const int cand = key[0] == M ? lane : key[1] == M ? 64 + lane : key[2] == M ? 128 + lane
+                       : key[3] == M ? 192 + lane : 1 << 20;
+        const int e = topk_wave_min(cand);
 #pragma unroll
         for (int i = 0; i < 4; i++)
             if (e == lane + 64 * i) key[i] = 0u;
