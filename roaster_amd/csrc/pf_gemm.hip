@@ -201,6 +201,9 @@ __global__ void __launch_bounds__(GT) pf_down_kernel(PfGemmArgs A)
 #define V2_DN_N (32 * V2_W)       /* down output rows per workgroup */
 #define V2_MC 96                  /* rows per tile */
 #define V2_LD (GK + 8)            /* LDS row stride (fp16 elements) */
+#ifndef PF_DN_NT
+#define PF_DN_NT 2                /* down output tiles per workgroup (inter <= 512) */
+#endif
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
@@ -856,6 +859,77 @@ __device__ __forceinline__ void v5_dn_body(const PfGemmArgs &A, const PfGroup &G
         }
 }
 
+/* Down, K <= 512 (one or two K steps): a workgroup keeps the whole activation
+ * tile in LDS (both K steps, staged once) and walks nt_count consecutive
+ * 256-row output tiles; the next tile's weight registers are loaded while the
+ * current tile computes, with no workgroup barrier after the staging. */
+template <int MS, bool QD>
+__device__ __forceinline__ void v6_dn_body(const PfGemmArgs &A, const PfGroup &G, const V4Shared &meta, int mlen, int n0,
+                                           int nt_count, uint8_t *lds)
+{
+    const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
+    const int nkb = A.I / GK;                  /* 1 or 2 */
+    _Float16 *Xb = (_Float16 *)lds;
+    constexpr int TD = TL_BYTES(QD);
+    constexpr int NP = MS * 32 * 64 / V2_T;
+    const uint8_t *a16 = (const uint8_t *)A.act16;
+    auto x_stage = [&](int kb, _Float16 *dst) {
+        uint2 xr[NP];
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int idx = t + i * V2_T, row = idx >> 6;
+            const int slot = meta.slot[row < mlen ? row : 0];
+            xr[i] = gld_u2(a16 + 2 * ((size_t)slot * A.I + kb * GK + 4 * (idx & 63)));
+        }
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int idx = t + i * V2_T, row = idx >> 6, c4 = 4 * (idx & 63);
+            const int sh = row < mlen ? (int)meta.psh[row][(kb * GK + c4) >> 4] : -200;
+            const f16x4 hv = __builtin_bit_cast(f16x4, xr[i]);
+            const f32x8 e = { __builtin_ldexpf((float)hv[0], sh), __builtin_ldexpf((float)hv[1], sh),
+                              __builtin_ldexpf((float)hv[2], sh), __builtin_ldexpf((float)hv[3], sh),
+                              0.f, 0.f, 0.f, 0.f };
+            const uint4 cu = __builtin_bit_cast(uint4, __builtin_convertvector(e, f16x8));
+            *(uint2 *)(dst + row * V2_LD + perm_slot4(c4)) = make_uint2(cu.x, cu.y);
+        }
+    };
+    auto tile_base = [&](int nt) {
+        return G.td + (size_t)((n0 + nt * V2_DN_N + 32 * w) / TL_ROWS) * nkb * TD;
+    };
+    typename RawOf<QD>::T r[2];
+    const uint8_t *wt = tile_base(0);
+    tile_load(r[0], wt, l);
+    if (nkb > 1) tile_load(r[1], wt + TD, l);
+    x_stage(0, Xb);
+    if (nkb > 1) x_stage(1, Xb + V3_XBUF);
+    __syncthreads();
+    for (int nt = 0; nt < nt_count; nt++) {
+        const bool more = nt + 1 < nt_count;
+        const uint8_t *wn = tile_base(more ? nt + 1 : nt);
+        f32x16 acc[MS];
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++) acc[ms] = (f32x16){};
+        __builtin_amdgcn_sched_barrier(0);
+        v4_mfma<MS, QD>(acc, Xb, r[0], h);
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) tile_load(r[0], wn, l);
+        if (nkb > 1) {
+            __builtin_amdgcn_sched_barrier(0);
+            v4_mfma<MS, QD>(acc, Xb + V3_XBUF, r[1], h);
+            __builtin_amdgcn_sched_barrier(0);
+            if (more) tile_load(r[1], wn + TD, l);
+        }
+        const int orow = n0 + nt * V2_DN_N + 32 * w + n;
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3);
+                if (m < mlen) A.out[(size_t)meta.slot[m] * A.H + orow] = acc[ms][i] * meta.fwd[m];
+            }
+    }
+}
+
 __device__ __forceinline__ bool v2_tile(const PfGemmArgs &A, int nblk, int &v, PfTile &tile)
 {
     const int R = *A.ntiles * nblk;
@@ -906,7 +980,8 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds4[];
     __shared__ V4Shared meta;
-    const int nblk = A.H / V2_DN_N;
+    const int nt_count = A.dn_nt;              /* output tiles per workgroup */
+    const int nblk = A.H / V2_DN_N / nt_count;
     int v;
     PfTile tile;
     if (!v2_tile(A, nblk, v, tile)) return;
@@ -929,12 +1004,18 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
             meta.psh[t][b] = (int8_t)max(pf_scale_exp(A.pmax[(size_t)slot * nb + b]) - er, -64);   /* 2^-64: 0 in fp16 */
     }
     __syncthreads();
-    const int n0 = (v % nblk) * V2_DN_N;
+    const int n0 = (v % nblk) * nt_count * V2_DN_N;
     const int ms = (mlen + 31) >> 5;
+    const bool whole_k = A.I <= 2 * GK;        /* activations for every K step fit in LDS */
 #define DN_CASE(M)                                                                   \
     if (ms == M) {                                                                   \
-        if (G.dq6) v5_dn_body<M, true>(A, G, meta, mlen, n0, lds4);                 \
-        else v5_dn_body<M, false>(A, G, meta, mlen, n0, lds4);                      \
+        if (whole_k) {                                                               \
+            if (G.dq6) v6_dn_body<M, true>(A, G, meta, mlen, n0, nt_count, lds4);   \
+            else v6_dn_body<M, false>(A, G, meta, mlen, n0, nt_count, lds4);        \
+        } else {                                                                     \
+            if (G.dq6) v5_dn_body<M, true>(A, G, meta, mlen, n0, lds4);             \
+            else v5_dn_body<M, false>(A, G, meta, mlen, n0, lds4);                  \
+        }                                                                            \
         return;                                                                      \
     }
     DN_CASE(1)
@@ -967,6 +1048,10 @@ int pf_gemm_launch(const PfGemmArgs &A, int max_tiles, int op)
     const size_t lds_gu = 2 * (size_t)V3_XBUF * 2, lds_dn = lds_gu;
     hipLaunchKernelGGL(pf2_gu_kernel, dim3(max_tiles * (A.I / V2_GU_J)), dim3(V2_T), lds_gu, R.stream, A);
     if (rt_check(hipGetLastError(), "prefill gate/up launch")) return ROASTER_EDEVICE;
-    hipLaunchKernelGGL(pf2_down_kernel, dim3(max_tiles * (A.H / V2_DN_N)), dim3(V2_T), lds_dn, R.stream, A);
+    PfGemmArgs D = A;
+    /* several output tiles per workgroup when every K step's activations fit in
+     * LDS and the tile count divides evenly, else one */
+    D.dn_nt = A.I <= 2 * GK && (A.H / V2_DN_N) % PF_DN_NT == 0 ? PF_DN_NT : 1;
+    hipLaunchKernelGGL(pf2_down_kernel, dim3(max_tiles * (A.H / V2_DN_N / D.dn_nt)), dim3(V2_T), lds_dn, R.stream, D);
     return rt_check(hipGetLastError(), "prefill down launch") ? ROASTER_EDEVICE : 0;
 }

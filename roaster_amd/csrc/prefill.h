@@ -40,6 +40,7 @@ struct PfGemmArgs {
     float *pmax;                    /* [slots][inter / 16] partial max |act| (fp16 mode) */
     float *out;                     /* [slots x H]: down products */
     int H, I;
+    int dn_nt;                      /* down GEMM: output tiles per workgroup (set by the launcher) */
 };
 
 /* Rows per tile the GEMMs of operand mode op expect in the tile list. */
