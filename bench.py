@@ -4,7 +4,7 @@ Headline (value): batch-1 decode through the 40-layer MoE-FFN stack -- hidden
 2048, 256 routed experts (top-8) + 1 shared expert per layer, gate/up Q4_K
 [512 x 2048], down Q6_K [2048 x 512], F32 router, RMSNorm (eps 1e-6) carried
 between layers -- with every expert resident in HBM (21.05 GB in the GGML layout
-the decode kernels read, plus the 22.6 GB MFMA tile-layout copy the prefill
+the decode kernels read, plus the 22.9 GB MFMA tile-layout copy the prefill
 GEMMs read).  A step is one token through all 40 layers (one library call, 3
 kernels per layer).  Inputs
 and weights are synthetic (seeded) and already in HBM when timing starts.

@@ -316,53 +316,9 @@ __device__ __forceinline__ int perm_slot4(int p)
  * n = 0..15 hold gate row j0 + 16w + n and lanes 16..31 the up row of the same
  * column, so SiLU(gate) * up pairs lane n with lane n + 16 in the epilogue; for
  * down, output rows n0 + 32w + n.  Two waves per SIMD let one wave's dequant
- * VALU work run under the other's MFMAs.
- *
- * Per K step (one super-block): the 256 weight rows' blocks arrive in LDS by
- * direct global->LDS loads of the 16-byte-aligned 224-byte window around each
- * block (consecutive lanes on consecutive 16-byte pieces, so each load
- * instruction covers one contiguous kilobyte); every lane copies its own row's
- * dwords out of the window, realigned with v_alignbyte_b32 (a block starts
- * a = addr % 16 <= 14 bytes into its window; 14 + 210 <= 224).  Activations
- * (MS x 32 rows x 256 fp16, permuted K order) are double-buffered in LDS
- * through registers.  Sequence per step: raw dwords LDS -> registers;
- * barrier; issue next step's window loads and activation loads; MFMA work;
- * store the activations; wait for the windows; barrier. */
-#define V3_CH 224                          /* LDS bytes per staged window */
-#define V3_NP 14                           /* 16-byte pieces per window */
-#define V3_NCH (32 * V2_W)                 /* weight rows (windows) per workgroup */
-#define V3_WBYTES (V3_NCH * V3_CH + 16)    /* + one dword of read-ahead after the last window */
-#define V3_PPT (V3_NCH * V3_NP / V2_T)     /* window pieces per thread */
+ * VALU work run under the other's MFMAs.  Activations (MS x 32 rows x 256
+ * fp16 per K step, permuted K order) are double-buffered in LDS. */
 #define V3_XBUF (V2_MC * V2_LD)            /* fp16 elements per activation buffer */
-
-static_assert(V3_NCH * V3_NP % V2_T == 0, "window pieces split evenly over the threads");
-
-#define AS1 __attribute__((address_space(1)))
-#define AS3 __attribute__((address_space(3)))
-
-__device__ __forceinline__ uint32_t lds_al(const uint32_t *p, int i, int sh)
-{
-    return __builtin_amdgcn_alignbyte(p[i + 1], p[i], sh);
-}
-
-__device__ __forceinline__ void raw_from_lds(RawQ6 &r, const uint32_t *p, int sh, int h)
-{
-#pragma unroll
-    for (int j = 0; j < 16; j++) r.L[j] = lds_al(p, 16 * h + j, sh);
-#pragma unroll
-    for (int j = 0; j < 8; j++) r.Hh[j] = lds_al(p, 32 + 8 * h + j, sh);
-    r.S[0] = lds_al(p, 48 + 2 * h, sh);
-    r.S[1] = lds_al(p, 49 + 2 * h, sh);
-    r.d = lds_al(p, 52, sh) & 0xFFFFu;
-}
-
-__device__ __forceinline__ void raw_from_lds(RawQ4 &r, const uint32_t *p, int sh, int h)
-{
-#pragma unroll
-    for (int k = 0; k < 4; k++) r.hd[k] = lds_al(p, k, sh);
-#pragma unroll
-    for (int j = 0; j < 16; j++) r.Q[j] = lds_al(p, 4 + 16 * h + j, sh);
-}
 
 /* MFMA work of one K step: MS row blocks x this wave's 32 weight columns, one
  * accumulator per row block.  Xs: activation buffer, row stride V2_LD. */
@@ -388,57 +344,6 @@ __device__ __forceinline__ void v4_mfma(f32x16 (&acc)[MS], const _Float16 *Xs, c
     }
 }
 
-/* Issue the direct global->LDS loads of K step kb's windows.  Thread t covers
- * pieces p = t + i * V2_T; piece p is window p / 14, 16-byte piece p % 14, and
- * lands at LDS byte 16 p (the lanes of one load instruction cover 64
- * consecutive pieces = one contiguous kilobyte of LDS). */
-__device__ __forceinline__ void v4_window_loads(const uint8_t *const (&pbase)[V3_PPT], const int (&pbb)[V3_PPT], int kb,
-                                                uint8_t *Wb)
-{
-    const int w = threadIdx.x >> 6;
-#pragma unroll
-    for (int i = 0; i < V3_PPT; i++) {
-        const uintptr_t q = (uintptr_t)(pbase[i] + (size_t)kb * pbb[i]) & ~(uintptr_t)15;
-        __builtin_amdgcn_global_load_lds((const AS1 void *)q, (AS3 void *)(Wb + 1024 * (w + V2_W * i)), 16, 0, 0);
-    }
-}
-
-/* Window piece bases of this thread: window c -> (row pointer + 16 * piece),
- * the K step's block is then at + kb * block bytes, rounded down to 16. */
-template <bool GATEUP>
-__device__ __forceinline__ void v4_window_bases(const PfGroup &G, int first, int nkb, const uint8_t *(&pbase)[V3_PPT],
-                                                int (&pbb)[V3_PPT])
-{
-#pragma unroll
-    for (int i = 0; i < V3_PPT; i++) {
-        const int p = threadIdx.x + i * V2_T, c = p / V3_NP, j = p - c * V3_NP;
-        const uint8_t *row;
-        int bb;
-        if (GATEUP) {
-            const int n = c & 31, ww = c >> 5;
-            const bool up = n >= 16;
-            bb = (up ? G.uq6 : G.gq6) ? RQ6K_BYTES : RQ4K_BYTES;
-            row = (up ? G.u : G.g) + (size_t)(first + 16 * ww + (n & 15)) * nkb * bb;
-        } else {
-            bb = G.dq6 ? RQ6K_BYTES : RQ4K_BYTES;
-            row = G.d + (size_t)(first + c) * nkb * bb;
-        }
-        pbase[i] = row + 16 * j;
-        pbb[i] = bb;
-    }
-}
-
-/* The lane's raw block of K step kb from LDS (its window is 32 w + n). */
-template <bool Q6>
-__device__ __forceinline__ void v4_lane_raw(typename RawOf<Q6>::T &r, const uint8_t *Wb, const uint8_t *myrow, int kb,
-                                            int h)
-{
-    constexpr int bb = Q6 ? RQ6K_BYTES : RQ4K_BYTES;
-    const int a = (int)((uintptr_t)(myrow + (size_t)kb * bb) & 15);
-    const int c = 32 * (threadIdx.x >> 6) + (threadIdx.x & 31);     /* window 32 w + n */
-    raw_from_lds(r, (const uint32_t *)(Wb + c * V3_CH) + (a >> 2), a & 3, h);
-}
-
 #define V5_MAXPART 128                 /* inter / 16 for inter <= 2048 */
 struct V4Shared {
     int tok[V2_MC];
@@ -447,188 +352,41 @@ struct V4Shared {
     int8_t psh[V2_MC][V5_MAXPART];     /* down: part scale exponent - row scale exponent (<= 0) */
 };
 
+/* v4_mfma for a wave whose lanes n < 16 hold gate rows of type QG and lanes
+ * n >= 16 up rows of type QU != QG: each lane dequantises its own record
+ * (divergent VALU work, exec-masked), then every MFMA runs with the whole
+ * wave active: an MFMA ignores the exec mask and reads all 64 lanes. */
 template <int MS, bool QG, bool QU>
-__device__ __forceinline__ void v4_gu_body(const PfGemmArgs &A, const PfGroup &G, const V4Shared &meta, int mlen, int j0,
-                                           uint8_t *lds)
+__device__ __forceinline__ void v4_mfma_mixed(f32x16 (&acc)[MS], const _Float16 *Xs, const typename RawOf<QG>::T &rg,
+                                              const typename RawOf<QU>::T &ru, bool up, int h)
 {
-    const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
-    const int nkb = A.H / GK;
-    _Float16 *Xb = (_Float16 *)lds;
-    uint8_t *Wb = lds + 2 * V3_XBUF * 2;
-    const uint8_t *pbase[V3_PPT];
-    int pbb[V3_PPT];
-    v4_window_bases<true>(G, j0, nkb, pbase, pbb);
-    const bool up = n >= 16;
-    constexpr int bG = QG ? RQ6K_BYTES : RQ4K_BYTES, bU = QU ? RQ6K_BYTES : RQ4K_BYTES;
-    const int jrow = j0 + 16 * w + (n & 15);
-    const uint8_t *myrow = up ? G.u + (size_t)jrow * nkb * bU : G.g + (size_t)jrow * nkb * bG;
-    /* activation staging through registers: 16-byte pieces idx = t + i * V2_T,
-     * row idx / 32, piece idx % 32 */
-    constexpr int NP = (MS * 32 * 32 + V2_T - 1) / V2_T;
-    uint4 xr[NP];
-    const uint16_t *xrow[NP];
+    typename ConstOf<QG>::T cg;
+    typename ConstOf<QU>::T cu;
+    if (up) raw_consts(ru, h, cu);
+    else raw_consts(rg, h, cg);
+    const int l = threadIdx.x & 63;
+    const _Float16 *xa = Xs + (l & 31) * V2_LD + 8 * (l >> 5);
 #pragma unroll
-    for (int i = 0; i < NP; i++) {
-        const int idx = t + i * V2_T, row = idx >> 5;
-        xrow[i] = row < mlen ? A.X16 + (size_t)meta.tok[row] * A.H + 8 * (idx & 31) : nullptr;
-    }
-    auto x_load = [&](int kb) {
+    for (int j = 0; j < 8; j++) {
+        f16x8 b0, b1;
+        if (up) dequant_pair(ru, cu, j, b0, b1);
+        else dequant_pair(rg, cg, j, b0, b1);
 #pragma unroll
-        for (int i = 0; i < NP; i++) xr[i] = xrow[i] ? gld_u4(xrow[i] + kb * GK) : make_uint4(0u, 0u, 0u, 0u);
-    };
-    auto x_store = [&](_Float16 *dst) {
-#pragma unroll
-        for (int i = 0; i < NP; i++) {
-            const int idx = t + i * V2_T, row = idx >> 5;
-            if (row < MS * 32) *(uint4 *)(dst + row * V2_LD + 8 * (idx & 31)) = xr[i];
-        }
-    };
-    f32x16 acc[MS];
-#pragma unroll
-    for (int ms = 0; ms < MS; ms++) acc[ms] = (f32x16){};
-    v4_window_loads(pbase, pbb, 0, Wb);
-    x_load(0);
-    x_store(Xb);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int kb = 0; kb < nkb; kb++) {
-        const bool more = kb + 1 < nkb;
-        typename RawOf<QG>::T rg;
-        typename RawOf<QU>::T ru;
-        if (QG == QU) {
-            v4_lane_raw<QG>(rg, Wb, myrow, kb, h);
-        } else if (up) {
-            v4_lane_raw<QU>(ru, Wb, myrow, kb, h);
-        } else {
-            v4_lane_raw<QG>(rg, Wb, myrow, kb, h);
-        }
-        __syncthreads();                    /* windows consumed: the buffer is free */
-        if (more) {
-            v4_window_loads(pbase, pbb, kb + 1, Wb);
-            x_load(kb + 1);
-        }
-        const _Float16 *Xs = Xb + (kb & 1) * V3_XBUF;
-        if (QG == QU) {
-            v4_mfma<MS, QG>(acc, Xs, rg, h);
-        } else if (up) {
-            v4_mfma<MS, QU>(acc, Xs, ru, h);
-        } else {
-            v4_mfma<MS, QG>(acc, Xs, rg, h);
-        }
-        if (more) {
-            x_store(Xb + ((kb + 1) & 1) * V3_XBUF);
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
+        for (int ms = 0; ms < MS; ms++) {
+            const f16x8 x0 = *(const f16x8 *)(xa + ms * 32 * V2_LD + 16 * j);
+            const f16x8 x1 = *(const f16x8 *)(xa + ms * 32 * V2_LD + 16 * (j + 8));
+            acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, b0, acc[ms], 0, 0, 0);
+            acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, b1, acc[ms], 0, 0, 0);
         }
     }
-    /* epilogue: lane n < 16 holds gate and lane n + 16 up of column jcol.  For
-     * the row pair (i, i + 1) one swizzle (lane ^ 16) gives lanes n < 16 the up
-     * value of row i and lanes n >= 16 the gate value of row i + 1, so all 32
-     * lanes compute act = silu(gate) * up (f32) for one row each; a 16-lane max
-     * gives each row's largest |act| over this wave's 16 columns, stored to
-     * pmax[slot][jcol / 16] (the down GEMM's row scale). */
-    const int npart = A.I / 16, part = (j0 + 16 * w) >> 4;
-    const int col = j0 + 16 * w + (n & 15);
-#pragma unroll
-    for (int ms = 0; ms < MS; ms++)
-#pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-            const float v0 = acc[ms][i], v1 = acc[ms][i + 1];
-            const float mine = up ? v1 : v0, other = up ? v0 : v1;
-            const float got = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, other), 0x401F));
-            /* lane n < 16: row i, gate = mine, up = got; lane n >= 16: row i + 1, gate = got, up = mine */
-            const float gsum = up ? got : mine, usum = up ? mine : got;
-            const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3) + (up ? 1 : 0);
-            float e = 0.0f;
-            if (m < mlen) {
-                const float f = meta.fwd[m];
-                e = pf_silu_mul_fast(gsum * f, usum * f);
-                A.act[(size_t)meta.slot[m] * A.I + col] = e;
-            }
-            float mx = fabsf(e);
-            mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
-            mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
-            mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
-            mx = fmaxf(mx, dpp_f<DPP_MIRROR>(mx));
-            if ((n & 15) == 0 && m < mlen) A.pmax[(size_t)meta.slot[m] * npart + part] = mx;
-        }
-}
-
-template <int MS, bool QD>
-__device__ __forceinline__ void v4_dn_body(const PfGemmArgs &A, const PfGroup &G, const V4Shared &meta, int mlen, int n0,
-                                           uint8_t *lds)
-{
-    const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
-    const int nkb = A.I / GK;
-    _Float16 *Xb = (_Float16 *)lds;
-    uint8_t *Wb = lds + 2 * V3_XBUF * 2;
-    const uint8_t *pbase[V3_PPT];
-    int pbb[V3_PPT];
-    v4_window_bases<false>(G, n0, nkb, pbase, pbb);
-    constexpr int bD = QD ? RQ6K_BYTES : RQ4K_BYTES;
-    const int orow = n0 + 32 * w + n;
-    const uint8_t *myrow = G.d + (size_t)orow * nkb * bD;
-    /* activation staging: act rows f32 (natural order) -> scaled fp16 in the
-     * permuted K order; float4 pieces idx = t + i * V2_T, row idx / 64.  The
-     * first two K steps are staged up front (both buffers); a later step kb is
-     * staged into buffer kb & 1 once step kb - 2 is done with it. */
-    constexpr int NP = MS * 32 * 64 / V2_T;
-    auto x_stage = [&](int kb, _Float16 *dst) {
-        float4 xr[NP];
-#pragma unroll
-        for (int i = 0; i < NP; i++) {
-            const int idx = t + i * V2_T, row = idx >> 6;
-            xr[i] = row < mlen ? gld_f4(A.act + (size_t)meta.slot[row] * A.I + kb * GK + 4 * (idx & 63))
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int i = 0; i < NP; i++) {
-            const int idx = t + i * V2_T, row = idx >> 6;
-            const float s = row < mlen ? meta.inv[row] : 0.0f;
-            const f32x8 e = { xr[i].x * s, xr[i].y * s, xr[i].z * s, xr[i].w * s, 0.f, 0.f, 0.f, 0.f };
-            const uint4 cu = __builtin_bit_cast(uint4, __builtin_convertvector(e, f16x8));
-            *(uint2 *)(dst + row * V2_LD + perm_slot4(4 * (idx & 63))) = make_uint2(cu.x, cu.y);
-        }
-    };
-    f32x16 acc[MS];
-#pragma unroll
-    for (int ms = 0; ms < MS; ms++) acc[ms] = (f32x16){};
-    v4_window_loads(pbase, pbb, 0, Wb);
-    x_stage(0, Xb);
-    if (nkb > 1) x_stage(1, Xb + V3_XBUF);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int kb = 0; kb < nkb; kb++) {
-        const bool more = kb + 1 < nkb;
-        typename RawOf<QD>::T r;
-        v4_lane_raw<QD>(r, Wb, myrow, kb, h);
-        __syncthreads();
-        if (more) v4_window_loads(pbase, pbb, kb + 1, Wb);
-        v4_mfma<MS, QD>(acc, Xb + (kb & 1) * V3_XBUF, r, h);
-        if (kb + 2 < nkb) {
-            __syncthreads();                /* every wave is done with buffer kb & 1 */
-            x_stage(kb + 2, Xb + (kb & 1) * V3_XBUF);
-        }
-        if (more) {
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-        }
-    }
-#pragma unroll
-    for (int ms = 0; ms < MS; ms++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (m < mlen) A.out[(size_t)meta.slot[m] * A.H + orow] = acc[ms][i] * meta.fwd[m];
-        }
 }
 
 /* ---- v5: weights straight from the MFMA tile layout into registers ----------
  * Workgroup shape, MFMA work and activation staging as in v4 (8 waves, two per
  * SIMD; activations double-buffered in LDS through registers), but every lane
  * loads its raw super-block half directly from the tile copy of the matrix
- * (tile.h): six 16-byte loads and a 12-byte tail (Q6_K) or five 16-byte loads
- * (Q4_K), each instruction covering contiguous runs of a wave's records (one
+ * (tile.h): seven 16-byte loads (Q6_K) or five (Q4_K), each instruction
+ * covering contiguous runs of a wave's records (one
  * kilobyte for down; two 256-byte runs for gate/up, whose waves pair 16 gate
  * rows with 16 up rows).  The raw registers are double-buffered per wave: step
  * kb + 1's loads are issued before step kb's MFMA work, with no workgroup
@@ -639,6 +397,7 @@ __device__ __forceinline__ void tile_load(RawQ6 &r, const uint8_t *tile, int lan
     uint4 s[6];
 #pragma unroll
     for (int i = 0; i < 6; i++) s[i] = gld_u4(p + 1024 * i);
+    const uint3 s6 = gld_u3(p + 1024 * 6);          /* the record's last dword is padding */
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         r.L[4 * i] = s[i].x; r.L[4 * i + 1] = s[i].y; r.L[4 * i + 2] = s[i].z; r.L[4 * i + 3] = s[i].w;
@@ -647,10 +406,9 @@ __device__ __forceinline__ void tile_load(RawQ6 &r, const uint8_t *tile, int lan
     for (int i = 0; i < 2; i++) {
         r.Hh[4 * i] = s[4 + i].x; r.Hh[4 * i + 1] = s[4 + i].y; r.Hh[4 * i + 2] = s[4 + i].z; r.Hh[4 * i + 3] = s[4 + i].w;
     }
-    const uint8_t *q = tile + TL_Q6_TAIL + 12 * lane;
-    r.S[0] = gld_u32(q);
-    r.S[1] = gld_u32(q + 4);
-    r.d = gld_u32(q + 8) & 0xFFFFu;
+    r.S[0] = s6.x;
+    r.S[1] = s6.y;
+    r.d = s6.z & 0xFFFFu;
 }
 
 __device__ __forceinline__ void tile_load(RawQ4 &r, const uint8_t *tile, int lane)
@@ -668,7 +426,8 @@ __device__ __forceinline__ void tile_load(RawQ4 &r, const uint8_t *tile, int lan
 
 /* Gate/up tile: lanes n < 16 of wave w take gate row j0 + 16 w + n, lanes
  * n >= 16 the up row of the same column.  QG == QU: one raw type per wave;
- * otherwise the two halves take divergent paths. */
+ * otherwise the two halves load and dequantise on divergent paths and share
+ * the MFMAs (v4_mfma_mixed). */
 template <int MS, bool QG, bool QU>
 __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G, const V4Shared &meta, int mlen, int j0,
                                            uint8_t *lds)
@@ -702,7 +461,7 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
 #pragma unroll
         for (int i = 0; i < NP; i++) {
             const int idx = t + i * V2_T, row = idx >> 5;
-            if (row < MS * 32) *(uint4 *)(dst + row * V2_LD + 8 * (idx & 31)) = xr[i];
+            if ((MS * 32 * 32) % V2_T == 0 || row < MS * 32) *(uint4 *)(dst + row * V2_LD + 8 * (idx & 31)) = xr[i];
         }
     };
     f32x16 acc[MS];
@@ -720,8 +479,7 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
     auto step = [&](int buf, const _Float16 *Xs) {
         __builtin_amdgcn_sched_barrier(0);
         if (QG == QU) v4_mfma<MS, QG>(acc, Xs, rg[buf], h);
-        else if (up) v4_mfma<MS, QU>(acc, Xs, ru[buf], h);
-        else v4_mfma<MS, QG>(acc, Xs, rg[buf], h);
+        else v4_mfma_mixed<MS, QG, QU>(acc, Xs, rg[buf], ru[buf], up, h);
         __builtin_amdgcn_sched_barrier(0);
     };
     w_load(0, 0);
@@ -949,7 +707,7 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_gu_kernel(PfGemmArgs A)
     PfTile tile;
     if (!v2_tile(A, nblk, v, tile)) return;
     const PfGroup &G = A.groups[tile.grp];
-    const int mlen = min(V2_MC, G.n - tile.m0);
+    const int mlen = min(A.chunk, G.n - tile.m0);
     const int t = threadIdx.x;
     if (t < mlen) {
         const int a = tile.m0 + t;
@@ -962,17 +720,22 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_gu_kernel(PfGemmArgs A)
     const int j0 = (v % nblk) * V2_GU_J;
     const int ms = (mlen + 31) >> 5;
     const int ty = (G.gq6 ? 2 : 0) | (G.uq6 ? 1 : 0);
+    /* three row blocks come with one weight type only (pf_gemm_chunk) */
+    if (ms == 3) {
+        if (ty == 3) v5_gu_body<3, true, true>(A, G, meta, mlen, j0, lds4);
+        else if (ty == 0) v5_gu_body<3, false, false>(A, G, meta, mlen, j0, lds4);
+        return;
+    }
 #define GU_CASE(M)                                                                   \
     if (ms == M) {                                                                   \
         if (ty == 3) v5_gu_body<M, true, true>(A, G, meta, mlen, j0, lds4);          \
         else if (ty == 2) v5_gu_body<M, true, false>(A, G, meta, mlen, j0, lds4);   \
         else if (ty == 1) v5_gu_body<M, false, true>(A, G, meta, mlen, j0, lds4);   \
-        else v5_gu_body<M, false, false>(A, G, meta, mlen, j0, lds4);               \
+        else v5_gu_body<M, false, false>(A, G, meta, mlen, j0, lds4);                \
         return;                                                                      \
     }
     GU_CASE(1)
     GU_CASE(2)
-    GU_CASE(3)
 #undef GU_CASE
 }
 
@@ -986,7 +749,7 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
     PfTile tile;
     if (!v2_tile(A, nblk, v, tile)) return;
     const PfGroup &G = A.groups[tile.grp];
-    const int mlen = min(V2_MC, G.n - tile.m0);
+    const int mlen = min(A.chunk, G.n - tile.m0);
     const int t = threadIdx.x;
     if (t < mlen) {
         const int slot = G.slot0 + tile.m0 + t;
@@ -1037,7 +800,10 @@ static int launch_v1(const PfGemmArgs &A, int max_tiles)
     return rt_check(hipGetLastError(), "prefill down launch") ? ROASTER_EDEVICE : 0;
 }
 
-int pf_gemm_chunk(int op) { return op == PF_F16 ? V2_MC : GM; }
+/* fp16 mode: up to three 32-row blocks; two when gate and up differ in type
+ * (a wave then holds both raw record types, which for three blocks exceeds
+ * the register budget of two waves per SIMD). */
+int pf_gemm_chunk(int op, bool mixed_gate_up) { return op == PF_F16 ? (mixed_gate_up ? 64 : V2_MC) : GM; }
 
 int pf_gemm_launch(const PfGemmArgs &A, int max_tiles, int op)
 {

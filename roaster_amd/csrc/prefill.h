@@ -40,11 +40,13 @@ struct PfGemmArgs {
     float *pmax;                    /* [slots][inter / 16] partial max |act| (fp16 mode) */
     float *out;                     /* [slots x H]: down products */
     int H, I;
+    int chunk;                      /* rows per tile of the tile list (pf_gemm_chunk) */
     int dn_nt;                      /* down GEMM: output tiles per workgroup (set by the launcher) */
 };
 
-/* Rows per tile the GEMMs of operand mode op expect in the tile list. */
-int pf_gemm_chunk(int op);
+/* Rows per tile the GEMMs of operand mode op expect in the tile list;
+ * mixed_gate_up: the gate and up matrices of some group differ in type. */
+int pf_gemm_chunk(int op, bool mixed_gate_up);
 
 /* Launch the gate/up and down GEMMs over up to max_tiles tiles.  op: PF_F16,
  * PF_SPLIT or PF_BF16 (gemm.h).  0 or ROASTER_EDEVICE. */

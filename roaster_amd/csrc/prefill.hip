@@ -364,7 +364,8 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     if (E > 256) return rt_fail(ROASTER_EINVAL, "roaster_moe_prefill: at most 256 routed experts");
     const int op = opt.precision == ROASTER_PREC_F16 ? PF_F16 : opt.precision == ROASTER_PREC_SPLIT ? PF_SPLIT : PF_BF16;
     const size_t TT = (size_t)T, slots = 9 * TT;
-    const int chunk = pf_gemm_chunk(op);
+    const LayerGeo &LG = t->geo[layer];
+    const int chunk = pf_gemm_chunk(op, LG.q6[0] != LG.q6[1] || LG.sh_q6[0] != LG.sh_q6[1]);
     const int max_tiles = (int)((8 * TT + chunk - 1) / chunk + E + (TT + chunk - 1) / chunk);
 
     /* workspace */
@@ -416,7 +417,6 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     PfPlanArgs pa;
     pa.L = L;
     pa.TL = t->tlayers_h[layer];
-    const LayerGeo &LG = t->geo[layer];
     pa.eb_g = LG.eb[0]; pa.eb_u = LG.eb[1]; pa.eb_d = LG.eb[2];
     pa.teb_g = LG.teb[0]; pa.teb_u = LG.teb[1]; pa.teb_d = LG.teb[2];
     pa.q6g = LG.q6[0]; pa.q6u = LG.q6[1]; pa.q6d = LG.q6[2];
@@ -446,6 +446,7 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     ga.pmax = op == PF_F16 ? (float *)(ws + o_pmax) : nullptr;
     ga.out = (float *)(ws + o_ed);
     ga.H = H; ga.I = I;
+    ga.chunk = chunk;
     if (int rc = pf_gemm_launch(ga, max_tiles, op)) return rc;
 
     hipLaunchKernelGGL(pf_combine_kernel, dim3(T), dim3(256), 0, R.stream, (const float *)ga.out,

@@ -39,6 +39,7 @@ typedef uint32_t gu32x4 __attribute__((ext_vector_type(4)));
 typedef gu32x4 __attribute__((aligned(2))) gu32x4_a2;
 typedef uint32_t gu32x2 __attribute__((ext_vector_type(2)));
 typedef gu32x2 __attribute__((aligned(2))) gu32x2_a2;
+typedef uint32_t gu32x3 __attribute__((ext_vector_type(3)));
 typedef float gf32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint4 gld_u4(const void *p)          /* 16-byte aligned */
@@ -50,6 +51,11 @@ __device__ __forceinline__ uint4 gld_u4a2(const void *p)        /* 2-byte aligne
 {
     const gu32x4 v = *(const GAS gu32x4_a2 *)p;
     return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint3 gld_u3(const void *p)           /* 16-byte aligned, 12 bytes read */
+{
+    const gu32x3 v = *(const GAS gu32x3 *)p;
+    return make_uint3(v.x, v.y, v.z);
 }
 __device__ __forceinline__ uint2 gld_u2(const void *p)           /* 8-byte aligned */
 {

@@ -175,21 +175,20 @@ __global__ void tile_repack_kernel(const uint8_t *src, uint8_t *dst, size_t src_
         const int kb = (int)(tt % nkb), g = (int)(tt / nkb);
         const uint8_t *blk = src + m * src_mat + ((size_t)(TL_ROWS * g + n) * nkb + kb) * bb;
         uint8_t *tile = dst + m * dst_mat + tt * TL_BYTES(q6);
-        uint32_t rec[27];
+        uint32_t rec[28];
         if (q6) {
             for (int i = 0; i < 16; i++) rec[i] = rd32(blk + 4 * (16 * h + i));
             for (int i = 0; i < 8; i++) rec[16 + i] = rd32(blk + 128 + 4 * (8 * h + i));
             rec[24] = rd32(blk + 192 + 8 * h);
             rec[25] = rd32(blk + 196 + 8 * h);
             rec[26] = blk[208] | (blk[209] << 8);
+            rec[27] = 0;
         } else {
             for (int i = 0; i < 4; i++) rec[i] = rd32(blk + 4 * i);
             for (int i = 0; i < 16; i++) rec[4 + i] = rd32(blk + 16 + 4 * (16 * h + i));
         }
         const int nq = 4 * TL_SLICES(q6);
         for (int q = 0; q < nq; q++) *(uint32_t *)(tile + 1024 * (q / 4) + 16 * l + 4 * (q % 4)) = rec[q];
-        if (q6)
-            for (int q = 24; q < 27; q++) *(uint32_t *)(tile + TL_Q6_TAIL + 12 * l + 4 * (q - 24)) = rec[q];
     }
 }
 

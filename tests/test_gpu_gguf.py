@@ -1,8 +1,10 @@
 """GGUF file -> HBM expert table -> decode / prefill on the GPU.
 
-A two-layer synthetic model at the real hidden / inter sizes with 16 experts;
+A three-layer synthetic model at the real hidden / inter sizes with 16 experts;
 layer 1 flips every matrix type of layer 0 (so Q4_K down and Q6_K gate/up run
-too) and stores its router in F16.  The loaded table must hold the file's
+too) and stores its router in F16; layer 2 gives gate and up different types
+(routed Q6_K gate / Q4_K up, shared the other way round), which caps prefill
+tiles at 64 rows.  The loaded table must hold the file's
 bytes, and decode / prefill through it must match the oracle on the same
 weights (tolerance max|d|/max|y| <= 2e-3, the FFN bar; decode also <= 1e-4)."""
 import ctypes as C
@@ -18,14 +20,15 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 E, H, I = 16, 2048, 512
-TYPES = [(0, 0, 1, 0, 0, 1), (1, 1, 0, 1, 1, 0)]
+TYPES = [(0, 0, 1, 0, 0, 1), (1, 1, 0, 1, 1, 0), (1, 0, 1, 0, 1, 0)]
+NL = len(TYPES)
 TOL, TIGHT = 2e-3, 1e-4
 
 
 @pytest.fixture(scope="module")
 def loaded(tmp_path_factory):
-    log("gguf: writing a 2-layer, 16-expert model")
-    m = MoeModel(31, 2, E, H, I, TYPES, [GT_F32, GT_F16])
+    log(f"gguf: writing a {NL}-layer, {E}-expert model")
+    m = MoeModel(31, NL, E, H, I, TYPES, [GT_F32, GT_F16, GT_F32])
     path = tmp_path_factory.mktemp("gguf") / "moe.gguf"
     write_gguf(path, METADATA, m.tensors(), alignment=64)
     info = R.RoasterGgufInfo()
@@ -43,8 +46,8 @@ def oracle_layer(m, l):
 
 def test_info_and_bytes(loaded):
     m, t, info = loaded
-    assert (info.n_layers, info.n_experts, info.hidden, info.inter, info.mixed_types) == (2, E, H, I, 1)
-    for l in range(2):
+    assert (info.n_layers, info.n_experts, info.hidden, info.inter, info.mixed_types) == (NL, E, H, I, 1)
+    for l in range(NL):
         for e in (0, 5, E - 1, E):
             ptrs = [C.c_void_p() for _ in range(3)]
             R.check(R.lib().roaster_table_expert_ptrs(t, l, e, *[C.byref(p) for p in ptrs]))
@@ -55,7 +58,7 @@ def test_info_and_bytes(loaded):
                 assert np.array_equal(got, want[k]), (l, e, k)
 
 
-@pytest.mark.parametrize("layer", [0, 1])
+@pytest.mark.parametrize("layer", range(NL))
 def test_decode_from_gguf(loaded, layer):
     m, t, _ = loaded
     log(f"gguf decode layer {layer} (types {TYPES[layer]})")
@@ -78,7 +81,7 @@ def test_decode_from_gguf(loaded, layer):
     assert err <= TOL and err <= TIGHT
 
 
-@pytest.mark.parametrize("layer", [0, 1])
+@pytest.mark.parametrize("layer", range(NL))
 def test_prefill_from_gguf(loaded, layer):
     m, t, _ = loaded
     T = 200

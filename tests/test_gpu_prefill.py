@@ -107,6 +107,28 @@ def test_prefill_ragged_given_logits(cfg3, cfg3_oracle, T):
         assert rel_err(Y[t], Y_ref[t]) <= 4 * TOL, t
 
 
+@pytest.mark.parametrize("levels", [2, 5, 40])
+def test_prefill_topk_tie_stress(cfg3, levels):
+    """Logits drawn from a few values, so most tokens have ties at the 8th
+    slot (and some at every slot): ids bit-exact against the oracle for every
+    token, including rows with exactly 8 and with 9 finite logits, and rows
+    mixing -0 / +0."""
+    T = 192
+    rng = np.random.default_rng(100 + levels)
+    lg = (rng.integers(0, levels, size=(T, 256)) * 0.25 - 1.0).astype(np.float32)
+    lg[0, :] = -np.inf
+    lg[0, rng.choice(256, 8, replace=False)] = 0.5            # exactly 8 selectable
+    lg[1, :] = np.nan
+    lg[1, rng.choice(256, 9, replace=False)] = -2.0           # 9 selectable, all tied
+    lg[2, ::2] = -0.0
+    lg[2, 1::2] = 0.0                                         # -0 and +0 tie
+    lg[3, :] = rng.standard_normal(256).astype(np.float32)    # distinct values
+    X = tokens(9, T, start=3000)
+    Y, lg_out, ids, w, counts = prefill(cfg3, X, logits_in=lg)
+    np.testing.assert_array_equal(lg_out, lg)
+    check_routing(lg, ids, w, counts, 256)
+
+
 def test_prefill_token_permutation_bit_exact(cfg3):
     """A token's output does not depend on which tile or slot it lands in."""
     T = 300
