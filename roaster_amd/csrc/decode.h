@@ -40,6 +40,9 @@ struct DecPlan {
     int ids[8][8];
     float w[8][9];          /* routing weights, [8] = sigmoid(shared gate logit) */
     int pad1[2];
+    const uint8_t *dsl[8][9];   /* down matrix of token t's slot k (8 = shared), NULL when unselected */
+    int dq6k[9];                /* type of slot k's down matrix (the same for every token) */
+    int pad2[3];
 };
 static_assert(sizeof(DecPlan) % 16 == 0, "DecPlan is copied in 16-byte units");
 

@@ -15,9 +15,11 @@
  *       union of the tokens' experts as an "active expert" plan (built
  *       identically in every workgroup; workgroup 0 publishes it), and every
  *       routed expert's gate/up rows: eh = silu(g) * u  (model.c:1122-1126).
- *   D   down rows: each workgroup owns 8 output rows for all active experts
- *       and combines them in the reference order
- *       y = sum_{k=0..7} w_k d_k + sigmoid(s) d_shared  (model.c:1139-1144).
+ *   D   down rows: each workgroup owns one token and a block of output rows
+ *       (4, or 8 with several tokens) for that token's nine slots, with their
+ *       SiLU*up vectors staged in LDS, and combines them in the reference
+ *       order y = sum_{k=0..7} w_k d_k + sigmoid(s) d_shared
+ *       (model.c:1139-1144).
  * Every wave issues all loads of its task set before consuming any (one
  * memory round trip per dependency instead of one per loop iteration).
  *
@@ -36,10 +38,11 @@
 
 #define DT 256                        /* threads per workgroup */
 #define DW (DT / 64)                  /* waves per workgroup */
-#ifndef GU_PF
-#define GU_PF 2                       /* tasks in flight per wave */
-#endif
-#define D_ROWS 4                      /* output rows per down workgroup */
+#define GU_PF 2                       /* tasks in flight per wave, one token */
+#define GU_PF_B 4                     /* the same with several tokens (activations from LDS) */
+#define D_ROWS 4                      /* output rows per down workgroup, one token */
+#define D_ROWS_B 8                    /* the same with several tokens (one workgroup per token) */
+#define D_MAXR 8
 #ifndef D_PF
 #define D_PF 4                        /* down tasks in flight per wave */
 #endif
@@ -62,6 +65,19 @@ extern "C" int roaster_phase_ts(unsigned long long *out)
 #define PHASE_TS(k, i) do { } while (0)
 #endif
 
+/* This thread's wave index, as a wave-uniform (scalar) value: branches on it
+ * are scalar branches, not exec-masked regions. */
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+/* A pointer every lane of the wave holds (read from LDS), as a scalar value. */
+__device__ __forceinline__ const uint8_t *uniform_ptr(const uint8_t *p)
+{
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return (const uint8_t *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
 
 __device__ __forceinline__ int first_of(int begin, int w, int n)
@@ -71,21 +87,55 @@ __device__ __forceinline__ int first_of(int begin, int w, int n)
 
 /* Copy n16 16-byte units global -> LDS, 8 units per thread per round: all
  * loads of a round are issued before its first store, so a round costs one
- * memory round trip (one round covers 32 KB). */
+ * memory round trip (one round covers 32 KB).  Loads and stores are
+ * unconditional, of units clamped to the last one (lanes past the end load
+ * and store that unit again, the same value), so the compiler neither sinks a
+ * load into a guarded store nor places a wait before the loads are issued:
+ * the first round shares a round trip with whatever the caller issued just
+ * before. */
 __device__ __forceinline__ void block_copy16(void *dst, const void *src, int n16)
 {
     for (int base = 0; base < n16; base += 8 * DT) {
         uint4 v[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int i = base + threadIdx.x + k * DT;
-            v[k] = i < n16 ? ((const uint4 *)src)[i] : make_uint4(0u, 0u, 0u, 0u);
-        }
+        for (int k = 0; k < 8; k++) v[k] = ((const uint4 *)src)[min(base + (int)threadIdx.x + k * DT, n16 - 1)];
+#pragma unroll
+        for (int k = 0; k < 8; k++) ((uint4 *)dst)[min(base + (int)threadIdx.x + k * DT, n16 - 1)] = v[k];
+    }
+}
+
+/* Storage position of 16-byte unit u of the gate/up kernel's activations in
+ * LDS: bits 4..6 of u are folded into bits 0, 1 and 3 (an involution that
+ * keeps every run of 16 units in place).  The 16 lanes of one ds_read_b128
+ * pass read units 64 lb + 16 g + 4 h + i of a Q4_K row chunk (qdot.h lane
+ * layout): stored plainly they share 2 of the 16 bank groups (8-way
+ * conflicts), swizzled they cover all 16 (Q6_K chunks: 2 lanes per group). */
+__device__ __forceinline__ int xsw(int u) { return u ^ ((u >> 4) & 3) ^ (((u >> 6) & 1) << 3); }
+
+/* block_copy16 with units below nsw stored at xsw(unit). */
+__device__ __forceinline__ void block_copy16_sw(void *dst, const void *src, int n16, int nsw)
+{
+    for (int base = 0; base < n16; base += 8 * DT) {
+        uint4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = ((const uint4 *)src)[min(base + (int)threadIdx.x + k * DT, n16 - 1)];
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const int i = base + threadIdx.x + k * DT;
-            if (i < n16) ((uint4 *)dst)[i] = v[k];
+            const int i = min(base + (int)threadIdx.x + k * DT, n16 - 1);
+            ((uint4 *)dst)[i < nsw ? xsw(i) : i] = v[k];
         }
+    }
+}
+
+/* The 16 activations at float offset off (a multiple of 16) of an LDS copy,
+ * stored plainly or swizzled. */
+template <bool SW>
+__device__ __forceinline__ void load_x16(const float *xn, int off, float4 (&x)[4])
+{
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int u = (off >> 2) + i;
+        x[i] = ((const float4 *)xn)[SW ? xsw(u) : u];
     }
 }
 
@@ -93,30 +143,56 @@ __device__ __forceinline__ void block_copy16(void *dst, const void *src, int n16
  * RMSNorm follows kernels.c:584-605: x * (1/sqrt(mean(x^2) + eps)) * w. */
 __device__ void block_norm(const DecArgs &A, int l, float *xn, float *xsum, float (*red)[RMAX_B], float *inv_rms)
 {
-    const int H = A.H, B = A.B;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int H = A.H, B = A.B;                 /* H <= 8 * DT */
+    const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
+    /* the norm weights of this thread's columns, loaded with h (one round trip) */
+    const float *nw = A.do_norm && A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * H : NULL;
+    float wcol[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) wcol[k] = nw ? nw[min(tid + k * DT, H - 1)] : 1.0f;
     block_copy16(xn, A.h, B * H / 4);
     __syncthreads();
     if (A.do_norm) {
-        for (int t = 0; t < B; t++) {
-            float ss = 0.0f;
-            for (int i = tid; i < H; i += DT) { const float v = xn[t * H + i]; ss = fmaf(v, v, ss); }
-            ss = group_sum<64>(ss);
-            if (lane == 0) red[wv][t] = ss;
+        /* sums of squares of every token first, then their reductions: the
+         * tokens' reduction chains are independent and interleave */
+        float ss[RMAX_B];
+#pragma unroll
+        for (int t = 0; t < RMAX_B; t++) {
+            ss[t] = 0.0f;
+            if (t < B) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const int i = tid + k * DT;
+                    if (i < H) {
+                        const float v = xn[t * H + i];
+                        ss[t] = fmaf(v, v, ss[t]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < RMAX_B; t++) {
+            if (t < B) {
+                ss[t] = group_sum<64>(ss[t]);
+                if (lane == 0) red[wv][t] = ss[t];
+            }
         }
         __syncthreads();
         if (tid < B) {
-            float ss = 0.0f;
-            for (int w = 0; w < DW; w++) ss += red[w][tid];
-            inv_rms[tid] = 1.0f / sqrtf(ss / (float)H + A.eps);
+            float s2 = 0.0f;
+            for (int w = 0; w < DW; w++) s2 += red[w][tid];
+            inv_rms[tid] = 1.0f / sqrtf(s2 / (float)H + A.eps);
         }
         __syncthreads();
-        const float *nw = A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * H : NULL;
         for (int t = 0; t < B; t++) {
             const float inv = inv_rms[t];
-            for (int i = tid; i < H; i += DT) {
-                const float v = xn[t * H + i] * inv;
-                xn[t * H + i] = nw ? v * nw[i] : v;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i = tid + k * DT;
+                if (i < H) {
+                    const float v = xn[t * H + i] * inv;
+                    xn[t * H + i] = nw ? v * wcol[k] : v;
+                }
             }
         }
         __syncthreads();
@@ -125,18 +201,23 @@ __device__ void block_norm(const DecArgs &A, int l, float *xn, float *xsum, floa
     __syncthreads();
 }
 
+/* The lane's chunks of gate row j and up row j.  Lanes past the row's last
+ * super-block (lb >= nb) load the last one again: loads stay unconditional
+ * (a lane-dependent guard would make them exec-masked, with a wait after
+ * each), and those lanes' products are never used. */
 template <bool G6, bool U6>
 __device__ __forceinline__ QChunk2 load_gu_pair(const uint8_t *g, const uint8_t *u, int j, int nb, int lb, int c)
 {
+    const int lbc = lb < nb ? lb : nb - 1;
     QChunk2 r;
-    r.g = q_load<G6>(g + ((size_t)j * nb + lb) * (G6 ? RQ6K_BYTES : RQ4K_BYTES), c);
-    r.u = q_load<U6>(u + ((size_t)j * nb + lb) * (U6 ? RQ6K_BYTES : RQ4K_BYTES), c);
+    r.g = q_load<G6>(g + ((size_t)j * nb + lbc) * (G6 ? RQ6K_BYTES : RQ4K_BYTES), c);
+    r.u = q_load<U6>(u + ((size_t)j * nb + lbc) * (U6 ? RQ6K_BYTES : RQ4K_BYTES), c);
     return r;
 }
 
 /* eh[p][j] = silu(gate_j . x_t) * (up_j . x_t) for the (t, slot) pairs p of one
  * expert, given the lane's chunks of gate row j and up row j. */
-template <bool G6, bool U6>
+template <bool G6, bool U6, bool SW>
 __device__ __forceinline__ void gu_row(const DecArgs &A, int j, const QChunk2 &ch, int ntok, const int *tk,
                                        const float *xn, const float *xsum)
 {
@@ -146,11 +227,16 @@ __device__ __forceinline__ void gu_row(const DecArgs &A, int j, const QChunk2 &c
     const int ua = lb * RQK + q_run_a<U6>(c), ub = ua + q_run_b_off<U6>();
     for (int i = 0; i < ntok; i++) {
         const int p = tk[i], t = p / 9;
-        const float *x = xn + t * H, *xs = xsum + t * (H / 16);
+        const float *xs = xsum + t * (H / 16);
         float pg = 0.0f, pu = 0.0f;
         if (lb < nb) {
-            pg = q_chunk_dot<G6>(ch.g, c, x + ga, x + gb, xs[ga >> 4], xs[gb >> 4]);
-            pu = q_chunk_dot<U6>(ch.u, c, x + ua, x + ub, xs[ua >> 4], xs[ub >> 4]);
+            float4 x0[4], x1[4];
+            load_x16<SW>(xn, t * H + ga, x0);
+            load_x16<SW>(xn, t * H + gb, x1);
+            pg = q_chunk_dot_r<G6>(ch.g, c, x0, x1, xs[ga >> 4], xs[gb >> 4]);
+            load_x16<SW>(xn, t * H + ua, x0);
+            load_x16<SW>(xn, t * H + ub, x1);
+            pu = q_chunk_dot_r<U6>(ch.u, c, x0, x1, xs[ua >> 4], xs[ub >> 4]);
         }
         pg = group_sum<64>(pg);
         pu = group_sum<64>(pu);
@@ -170,7 +256,7 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A,
     const DecLayer L = A.layers[l];
     const int lane = threadIdx.x & 63, c = lane & 7, lb = lane >> 3;
     PHASE_TS(0, 0);
-    const int task = blockIdx.x * DW + (threadIdx.x >> 6);
+    const int task = blockIdx.x * DW + wave_id();
     const int nrouter = A.logits_in ? 0 : E;
     /* task < nrouter: router row; == nrouter: gate_inp; then shared-expert row pairs */
     const bool is_row = task <= nrouter;
@@ -184,9 +270,8 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A,
     if (is_row) {
         const float *row = task < nrouter ? L.router + (size_t)task * H : L.gate_inp;
 #pragma unroll
-        for (int m = 0; m < 8; m++)
-            if (4 * lane + 256 * m < H) w[m] = gld_f4(row + 4 * lane + 256 * m);
-    } else if (is_sh && lb < nb) {
+        for (int m = 0; m < 8; m++) w[m] = gld_f4(row + min(4 * lane + 256 * m, H - 4));   /* clamped: no masked loads */
+    } else if (is_sh) {
         if (kind == 0) ch = load_gu_pair<false, false>(L.sgate, L.sup, j, nb, lb, c);
         else if (kind == 3) ch = load_gu_pair<true, true>(L.sgate, L.sup, j, nb, lb, c);
         else if (kind == 2) ch = load_gu_pair<true, false>(L.sgate, L.sup, j, nb, lb, c);
@@ -229,10 +314,10 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A,
             }
         }
     } else if (is_sh) {
-        if (kind == 0) gu_row<false, false>(A, j, ch, B, sh_tk, xn, xsum);
-        else if (kind == 3) gu_row<true, true>(A, j, ch, B, sh_tk, xn, xsum);
-        else if (kind == 2) gu_row<true, false>(A, j, ch, B, sh_tk, xn, xsum);
-        else gu_row<false, true>(A, j, ch, B, sh_tk, xn, xsum);
+        if (kind == 0) gu_row<false, false, false>(A, j, ch, B, sh_tk, xn, xsum);
+        else if (kind == 3) gu_row<true, true, false>(A, j, ch, B, sh_tk, xn, xsum);
+        else if (kind == 2) gu_row<true, false, false>(A, j, ch, B, sh_tk, xn, xsum);
+        else gu_row<false, true, false>(A, j, ch, B, sh_tk, xn, xsum);
     }
     PHASE_TS(0, 2);
 }
@@ -245,7 +330,7 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A,
 __device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, const float (*lg4)[4], float sg,
                            unsigned long long *emask)
 {
-    const int B = A.B, E = A.E, tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    const int B = A.B, E = A.E, tid = threadIdx.x, wv = wave_id(), lane = tid & 63;
     if (tid == 0) P.err = 0;
     __syncthreads();
     for (int t = wv, r = 0; t < B; t += DW, r++) topk8_wave(lg4[r], E, P.ids[t], P.w[t], &P.err);
@@ -290,6 +375,17 @@ __device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, cons
             P.nact = nroute + 1;
         }
     }
+    /* down slot table for the down kernel */
+    for (int i = tid; i < B * 9; i += DT) {
+        const int t = i / 9, k = i % 9;
+        if (k < RTOPK) {
+            const int e = P.ids[t][k];
+            P.dsl[t][k] = e >= 0 ? L.down + (size_t)e * L.eb[2] : NULL;
+        } else {
+            P.dsl[t][k] = L.sdown;
+        }
+    }
+    if (tid < 9) P.dq6k[tid] = tid < RTOPK ? L.q6[2] : L.sq6[2];
     __syncthreads();
 }
 
@@ -304,6 +400,11 @@ __device__ void ffn_plan(const DecArgs &A, DecPlan &P)
             P.a[k].ntok = 1;
             P.a[k].tk[0] = k;
         }
+        for (int k = 0; k < 9; k++) {
+            P.dsl[0][k] = k < A.ffn_n ? A.ffn_ex[k].d : NULL;
+            P.dq6k[k] = k < A.ffn_n ? A.ffn_ex[k].dq6 : 0;
+            P.w[0][k] = 0.0f;
+        }
     }
     __syncthreads();
 }
@@ -317,41 +418,38 @@ __device__ __forceinline__ int type_run_end(const DecPlan &P, int a0, int a_end,
 }
 
 /* Gate/up tasks q = a*I + j for q in [q0, q1), all with types (G6, U6).  Each
- * wave loads the chunks of GU_PF tasks, then computes them.  With one token
- * (decode batch 1 and kernel_ffn_fused) the lane's activations are loaded into
- * registers once and reused by every task. */
+ * wave loads the chunks of PF tasks (GU_PF, or GU_PF_B with several tokens),
+ * then computes them.  With one token (decode batch 1 and kernel_ffn_fused)
+ * the lane's activations are loaded into registers once and reused by every
+ * task. */
 template <bool G6, bool U6, bool ONE>
 __device__ void gu_tasks(const DecArgs &A, const DecPlan &P, int q0, int q1, const float *xn, const float *xsum)
 {
     const int H = A.H, I = A.I, nb = H / RQK;
     const int lane = threadIdx.x & 63, c = lane & 7, lb = lane >> 3;
-    const int gw = blockIdx.x * DW + (threadIdx.x >> 6), nw = gridDim.x * DW;
+    const int gw = blockIdx.x * DW + wave_id(), nw = gridDim.x * DW;
     const int ga = lb * RQK + q_run_a<G6>(c), gb = ga + q_run_b_off<G6>();
     const int ua = lb * RQK + q_run_a<U6>(c), ub = ua + q_run_b_off<U6>();
     float4 xga[4], xgb[4], xua[4], xub[4];
     float sga = 0.0f, sgb = 0.0f, sua = 0.0f, sub = 0.0f;
     if (ONE && lb < nb) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            xga[i] = *(const float4 *)(xn + ga + 4 * i);
-            xgb[i] = *(const float4 *)(xn + gb + 4 * i);
-            xua[i] = *(const float4 *)(xn + ua + 4 * i);
-            xub[i] = *(const float4 *)(xn + ub + 4 * i);
-        }
+        load_x16<true>(xn, ga, xga);
+        load_x16<true>(xn, gb, xgb);
+        load_x16<true>(xn, ua, xua);
+        load_x16<true>(xn, ub, xub);
         sga = xsum[ga >> 4]; sgb = xsum[gb >> 4]; sua = xsum[ua >> 4]; sub = xsum[ub >> 4];
     }
-    for (int qs = first_of(q0, gw, nw); qs < q1; qs += nw * GU_PF) {
-        QChunk2 ch[GU_PF];
+    constexpr int PF = ONE ? GU_PF : GU_PF_B;
+    for (int qs = first_of(q0, gw, nw); qs < q1; qs += nw * PF) {
+        QChunk2 ch[PF];
 #pragma unroll
-        for (int f = 0; f < GU_PF; f++) {
-            const int q = qs + f * nw;
-            if (q < q1 && lb < nb) {
-                const DecActive &X = P.a[q / I];
-                ch[f] = load_gu_pair<G6, U6>(X.g, X.u, q % I, nb, lb, c);
-            }
+        for (int f = 0; f < PF; f++) {
+            const int q = min(qs + f * nw, q1 - 1);          /* unconditional: past q1 repeats the last task */
+            const DecActive &X = P.a[q / I];
+            ch[f] = load_gu_pair<G6, U6>(X.g, X.u, q % I, nb, lb, c);
         }
 #pragma unroll
-        for (int f = 0; f < GU_PF; f++) {
+        for (int f = 0; f < PF; f++) {
             const int q = qs + f * nw;
             if (q >= q1) break;
             const DecActive &X = P.a[q / I];
@@ -365,7 +463,7 @@ __device__ void gu_tasks(const DecArgs &A, const DecPlan &P, int q0, int q1, con
                 pu = group_sum<64>(pu);
                 if (lane == 0) A.eh[(size_t)X.tk[0] * I + q % I] = silu_mul(pg, pu);
             } else {
-                gu_row<G6, U6>(A, q % I, ch[f], X.ntok, X.tk, xn, xsum);
+                gu_row<G6, U6, true>(A, q % I, ch[f], X.ntok, X.tk, xn, xsum);
             }
         }
     }
@@ -392,9 +490,18 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int
     if (A.ffn_out) {
         ffn_plan(A, P);
         block_norm(A, l, xn, xsum, red, inv_rms);
+        for (int u = threadIdx.x; u < B * A.H / 4; u += DT) {     /* swizzle in place (xsw is an involution) */
+            const int v = xsw(u);
+            if (u < v) {
+                const float4 a = ((float4 *)xn)[u], b = ((float4 *)xn)[v];
+                ((float4 *)xn)[u] = b;
+                ((float4 *)xn)[v] = a;
+            }
+        }
+        __syncthreads();
     } else {
         /* logits of this wave's tokens and the shared-gate logits, loaded with h */
-        const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+        const int lane = threadIdx.x & 63, wv = wave_id();
         const float *lg = A.logits_in ? A.logits_in : A.logits;
         float lg4[(RMAX_B + DW - 1) / DW][4];
 #pragma unroll
@@ -406,7 +513,7 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int
         }
         const float sg = threadIdx.x < B ? A.sgate_raw[threadIdx.x] : 0.0f;
         const DecLayer L = A.layers[l];
-        block_copy16(xn, A.xn_g, B * (A.H + A.H / 16) / 4);
+        block_copy16_sw(xn, A.xn_g, B * (A.H + A.H / 16) / 4, B * A.H / 4);
         __syncthreads();
         PHASE_TS(1, 1);
         build_plan(A, L, P, lg4, sg, emask);
@@ -452,117 +559,120 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int
 
 /* ---- D: down rows + combine ----------------------------------------------- */
 
-/* Down tasks q = a*ngroups + g for q in [q0, q1) (all with type D6): rows
- * r0 + g*rpw + lane/lpr of expert a, for each of its (t, slot) pairs, into
- * dbuf[p][row - r0].  The SiLU*up inputs come from LDS (ehl, with 16-column
- * sums ehs) when they fit, else from global memory. */
-template <bool D6, bool EH_LDS>
-__device__ void down_tasks(const DecArgs &A, const DecPlan &P, int q0, int q1, float *dbuf, int ngroups,
-                           const float *ehl, const float *ehs)
+/* Down tasks of slots [k0, k1) of this workgroup's token (all of type D6):
+ * task q = (k - k0) * ngroups + g covers rows r0 + g*rpw + lane/lpr of slot
+ * k's down matrix sd[k], dotted with the slot's SiLU*up vector in LDS (ehl,
+ * with 16-column sums ehs), into dbuf[k][row - r0].  Every wave issues the
+ * loads of D_PF tasks before computing any. */
+template <bool D6>
+__device__ void down_slots(const DecArgs &A, const uint8_t *const *sd, int k0, int k1, float *dbuf, int ngroups,
+                           int dr, int r0, const float *ehl, const float *ehs, const uint8_t *fb)
 {
     const int H = A.H, I = A.I, nb = I / RQK;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wv = wave_id();
     const int lpr = lanes_per_row(nb), rpw = 64 / lpr;
     const int rw = lane / lpr, lr = lane % lpr, c = lr & 7, lb = lr >> 3;
     const size_t dbs = D6 ? RQ6K_BYTES : RQ4K_BYTES;
-    const int r0 = blockIdx.x * D_ROWS;
     const int ca = lb * RQK + q_run_a<D6>(c), cb = ca + q_run_b_off<D6>();
-    for (int qs = first_of(q0, wv, DW); qs < q1; qs += DW * D_PF) {
+    const int q1 = (k1 - k0) * ngroups;
+    for (int qs = wv; qs < q1; qs += DW * D_PF) {
+        /* loads are unconditional (a guarded load is exec-masked or branched
+         * around, and the compiler then waits before the next one): tasks past
+         * q1 repeat the last task, rows past the matrix or the block and
+         * blocks past the row read a valid chunk, an unselected slot reads fb;
+         * none of those is used */
         QChunk ch[D_PF];
 #pragma unroll
         for (int f = 0; f < D_PF; f++) {
-            const int q = qs + f * DW;
-            if (q < q1) {
-                const int a = q / ngroups, g = q % ngroups;
-                const int rl = g * rpw + rw, row = r0 + rl;
-                if (rl < D_ROWS && row < H && lb < nb)
-                    ch[f] = q_load<D6>(P.a[a].d + ((size_t)row * nb + lb) * dbs, c);
-            }
+            const int q = min(qs + f * DW, q1 - 1);
+            const int k = k0 + q / ngroups, g = q % ngroups;
+            const int row = min(r0 + g * rpw + rw, H - 1);
+            const uint8_t *m = uniform_ptr(sd[k]);
+            ch[f] = q_load<D6>((m ? m : fb) + ((size_t)row * nb + min(lb, nb - 1)) * dbs, c);
         }
 #pragma unroll
         for (int f = 0; f < D_PF; f++) {
             const int q = qs + f * DW;
             if (q >= q1) break;
-            const int a = q / ngroups, g = q % ngroups;
-            const DecActive &X = P.a[a];
+            const int k = k0 + q / ngroups, g = q % ngroups;
             const int rl = g * rpw + rw, row = r0 + rl;
-            const bool live = rl < D_ROWS && row < H && lb < nb;
-            for (int i = 0; i < X.ntok; i++) {
-                const int p = X.tk[i];
-                float part = 0.0f;
-                if (live) {
-                    if (EH_LDS) {
-                        const float *x = ehl + p * I, *xs = ehs + p * (I / 16);
-                        part = q_chunk_dot<D6>(ch[f], c, x + ca, x + cb, xs[ca >> 4], xs[cb >> 4]);
-                    } else {
-                        const float *x = A.eh + (size_t)p * I;
-                        part = q_chunk_dot<D6>(ch[f], c, x + ca, x + cb, sum16(x + ca), sum16(x + cb));
-                    }
-                }
-                part = group_sum_w(part, lpr);
-                if (live && lr == 0) dbuf[p * D_ROWS + rl] = part;
+            const bool live = rl < dr && row < H && lb < nb && uniform_ptr(sd[k]) != NULL;
+            float part = 0.0f;
+            if (live) {
+                const float *x = ehl + k * I, *xs = ehs + k * (I / 16);
+                part = q_chunk_dot<D6>(ch[f], c, x + ca, x + cb, xs[ca >> 4], xs[cb >> 4]);
             }
+            part = group_sum_w(part, lpr);
+            if (live && lr == 0) dbuf[k * D_MAXR + rl] = part;
         }
     }
 }
 
-/* SiLU*up inputs of every (t, slot) pair staged in LDS when they fit. */
-#define EH_LDS_FLOATS (18 * 1024)
-
-extern "C" __global__ void __launch_bounds__(DT, 3) dec_down_kernel(DecArgs A, int l)
+/* One workgroup per (token t, block of dr output rows): the token's nine
+ * slots (8 routed experts from the plan's ids, then the shared expert), or
+ * the n experts of kernel_ffn_fused for token 0.  The slots' SiLU*up vectors
+ * (at most 9 x 2048 floats) are staged in LDS. */
+extern "C" __global__ void __launch_bounds__(DT, 3) dec_down_kernel(DecArgs A, int l, int dr)
 {
     extern __shared__ __align__(16) float lds[];
-    __shared__ DecPlan P;
-    __shared__ float dbuf[RMAX_B * 9 * D_ROWS];
-    const int H = A.H, B = A.B, I = A.I, nb = I / RQK;
+    __shared__ float dbuf[9 * D_MAXR];
+    __shared__ const uint8_t *sd[9];
+    __shared__ float sw[9];
+    __shared__ int sq[9];
+    const int H = A.H, I = A.I, nb = I / RQK;
     const int tid = threadIdx.x;
+    const int nrb = (H + dr - 1) / dr, t = blockIdx.x / nrb, r0 = (blockIdx.x % nrb) * dr;
+    const bool ffn = A.ffn_out != NULL;
+    const int nslot = ffn ? A.ffn_n : 9;
     PHASE_TS(2, 0);
-    const int npair = A.ffn_out ? A.ffn_n : B * 9;
-    const bool eh_lds = npair * I <= EH_LDS_FLOATS;
-    float *ehl = lds, *ehs = lds + npair * I;
-    block_copy16(&P, A.plan_g, (int)(sizeof(DecPlan) / 16));
-    if (eh_lds) block_copy16(ehl, A.eh, npair * I / 4);
-    __syncthreads();
-    if (eh_lds) {
-        for (int r = tid; r < npair * (I / 16); r += DT) ehs[r] = sum16(ehl + r * 16);
-        __syncthreads();
+    float *ehl = lds, *ehs = lds + nslot * I;
+    /* slot table (published with the plan): its loads are unconditional,
+     * issued first and consumed only after the SiLU*up copy, so both share
+     * one memory round trip */
+    const int ks = min(tid, 8);
+    const uint8_t *pk = A.plan_g->dsl[t][ks];
+    const float wk = A.plan_g->w[t][ks];
+    const int qk = A.plan_g->dq6k[ks];
+    for (int i = tid; i < 9 * D_MAXR; i += DT) dbuf[i] = 0.0f;
+    block_copy16(ehl, A.eh + (size_t)(ffn ? 0 : t * 9) * I, nslot * I / 4);
+    if (tid < 9) {
+        sd[tid] = pk;
+        sw[tid] = wk;
+        sq[tid] = qk;
     }
+    __syncthreads();
+    for (int r = tid; r < nslot * (I / 16); r += DT) ehs[r] = sum16(ehl + r * 16);
+    __syncthreads();
     const int lpr = lanes_per_row(nb), rpw = 64 / lpr;
-    const int ngroups = (D_ROWS + rpw - 1) / rpw;
-    const int r0 = blockIdx.x * D_ROWS;
+    const int ngroups = (dr + rpw - 1) / rpw;
+    const uint8_t *fb = uniform_ptr(sd[nslot - 1]);     /* always set: the shared expert, or the last expert */
     PHASE_TS(2, 1);
-    for (int a0 = 0; a0 < P.nact;) {
-        const int a1 = type_run_end(P, a0, P.nact, false);
-        const int q0 = a0 * ngroups, q1 = a1 * ngroups;
-        if (eh_lds) {
-            if (P.a[a0].dq6) down_tasks<true, true>(A, P, q0, q1, dbuf, ngroups, ehl, ehs);
-            else down_tasks<false, true>(A, P, q0, q1, dbuf, ngroups, ehl, ehs);
-        } else {
-            if (P.a[a0].dq6) down_tasks<true, false>(A, P, q0, q1, dbuf, ngroups, ehl, ehs);
-            else down_tasks<false, false>(A, P, q0, q1, dbuf, ngroups, ehl, ehs);
-        }
-        a0 = a1;
+    for (int k0 = 0; k0 < nslot;) {
+        int k1 = k0 + 1;
+        while (k1 < nslot && sq[k1] == sq[k0]) k1++;
+        if (sq[k0]) down_slots<true>(A, sd, k0, k1, dbuf, ngroups, dr, r0, ehl, ehs, fb);
+        else down_slots<false>(A, sd, k0, k1, dbuf, ngroups, dr, r0, ehl, ehs, fb);
+        k0 = k1;
     }
     __syncthreads();
     PHASE_TS(2, 2);
-    if (A.ffn_out) {                    /* kernel_ffn_fused: per-expert outputs, token 0 */
-        for (int idx = tid; idx < A.ffn_n * D_ROWS; idx += DT) {
-            const int k = idx / D_ROWS, rl = idx % D_ROWS, row = r0 + rl;
-            if (row < H) A.ffn_out[(size_t)k * H + row] = dbuf[k * D_ROWS + rl];
+    if (ffn) {                          /* kernel_ffn_fused: per-expert outputs */
+        for (int idx = tid; idx < nslot * dr; idx += DT) {
+            const int k = idx / dr, rl = idx % dr, row = r0 + rl;
+            if (row < H) A.ffn_out[(size_t)k * H + row] = dbuf[k * D_MAXR + rl];
         }
     } else {
-        for (int idx = tid; idx < B * D_ROWS; idx += DT) {
-            const int t = idx / D_ROWS, rl = idx % D_ROWS, row = r0 + rl;
+        for (int rl = tid; rl < dr; rl += DT) {
+            const int row = r0 + rl;
             if (row >= H) continue;
             float y = 0.0f;
-            for (int k = 0; k < RTOPK; k++) y = fmaf(P.w[t][k], dbuf[(t * 9 + k) * D_ROWS + rl], y);
-            y = fmaf(P.w[t][8], dbuf[(t * 9 + 8) * D_ROWS + rl], y);
+            for (int k = 0; k < RTOPK; k++) y = fmaf(sw[k], dbuf[k * D_MAXR + rl], y);
+            y = fmaf(sw[8], dbuf[8 * D_MAXR + rl], y);
             if (A.y) A.y[(size_t)t * H + row] = y;
             else A.h[(size_t)t * H + row] = A.h[(size_t)t * H + row] + y;
         }
     }
     PHASE_TS(2, 3);
-    (void)l;
 }
 
 /* ---- host side ------------------------------------------------------------ */
@@ -579,9 +689,10 @@ static int launch_layer(const DecArgs &A, int l, bool with_router)
     }
     hipLaunchKernelGGL(dec_gu_kernel, dim3(2 * R.n_cu), dim3(DT), lds, R.stream, A, l);
     if (rt_check(hipGetLastError(), "gate/up launch")) return ROASTER_EDEVICE;
-    const int npair = A.ffn_out ? A.ffn_n : A.B * 9;
-    const size_t dlds = npair * A.I <= EH_LDS_FLOATS ? (size_t)npair * A.I * 4 + (size_t)npair * (A.I / 16) * 4 : 0;
-    hipLaunchKernelGGL(dec_down_kernel, dim3((A.H + D_ROWS - 1) / D_ROWS), dim3(DT), dlds, R.stream, A, l);
+    const int nslot = A.ffn_out ? A.ffn_n : 9, dr = A.B > 1 ? D_ROWS_B : D_ROWS;
+    const size_t dlds = (size_t)nslot * A.I * 4 + (size_t)nslot * (A.I / 16) * 4;
+    const int nrb = (A.H + dr - 1) / dr;
+    hipLaunchKernelGGL(dec_down_kernel, dim3(nrb * (A.ffn_out ? 1 : A.B)), dim3(DT), dlds, R.stream, A, l, dr);
     return rt_check(hipGetLastError(), "down launch") ? ROASTER_EDEVICE : 0;
 }
 
