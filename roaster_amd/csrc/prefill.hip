@@ -143,15 +143,26 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + wv;
     if (t >= A.T) return;
-    /* X row: max |x| and the shared-expert gate dot */
+    /* X row: max |x| and the shared-expert gate dot.  The row (H <= 2048: at
+     * most 8 float4 per lane) and the gate vector are loaded at once, indices
+     * clamped, and the row stays in registers for the fp16 conversion. */
     const float *x = A.X + (size_t)t * A.H;
+    float4 xv[8], gv[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int k = min(4 * lane + 256 * i, A.H - 4);
+        xv[i] = *(const float4 *)(x + k);
+        gv[i] = *(const float4 *)(A.gate_inp + k);
+    }
     float mx = 0.0f, dot = 0.0f;
-    for (int k = 4 * lane; k < A.H; k += 256) {
-        const float4 v = *(const float4 *)(x + k);
-        const float4 g = *(const float4 *)(A.gate_inp + k);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        dot = fmaf(v.x, g.x, dot); dot = fmaf(v.y, g.y, dot);
-        dot = fmaf(v.z, g.z, dot); dot = fmaf(v.w, g.w, dot);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        if (4 * lane + 256 * i < A.H) {
+            const float4 v = xv[i], g = gv[i];
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            dot = fmaf(v.x, g.x, dot); dot = fmaf(v.y, g.y, dot);
+            dot = fmaf(v.z, g.z, dot); dot = fmaf(v.w, g.w, dot);
+        }
     }
     dot = group_sum<64>(dot);
 #pragma unroll
@@ -163,13 +174,18 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
             A.xinv[t] = inv;
             A.xfwd[t] = fwd;
         }
-        if (A.x16)
-            for (int k = 4 * lane; k < A.H; k += 256) {
-                const float4 v = *(const float4 *)(x + k);
-                const f32x8 e = { v.x * inv, v.y * inv, v.z * inv, v.w * inv, 0.f, 0.f, 0.f, 0.f };
-                const uint4 c = __builtin_bit_cast(uint4, __builtin_convertvector(e, f16x8));
-                *(uint2 *)(A.x16 + (size_t)t * A.H + (k & ~255) + pf_perm_slot4(k & 255)) = make_uint2(c.x, c.y);
+        if (A.x16) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int k = 4 * lane + 256 * i;
+                if (k < A.H) {
+                    const float4 v = xv[i];
+                    const f32x8 e = { v.x * inv, v.y * inv, v.z * inv, v.w * inv, 0.f, 0.f, 0.f, 0.f };
+                    const uint4 c = __builtin_bit_cast(uint4, __builtin_convertvector(e, f16x8));
+                    *(uint2 *)(A.x16 + (size_t)t * A.H + (k & ~255) + pf_perm_slot4(k & 255)) = make_uint2(c.x, c.y);
+                }
             }
+        }
     }
     if (lane == 0) A.sg[t] = 1.0f / (1.0f + expf(-dot));
     /* logits */
@@ -210,22 +226,32 @@ extern "C" __global__ void __launch_bounds__(256) pf_bucket_kernel(const int *id
     __shared__ int wsum[4];
     const int e = blockIdx.x;
     int base = 0;
-    for (int c = 0; c < T; c += 256) {
-        const int t = c + threadIdx.x;
-        int k = -1;
-        if (t < T) {
-            const int4 a = *(const int4 *)(ids + (size_t)t * 8);
-            const int4 b = *(const int4 *)(ids + (size_t)t * 8 + 4);
-            k = a.x == e ? 0 : a.y == e ? 1 : a.z == e ? 2 : a.w == e ? 3
-              : b.x == e ? 4 : b.y == e ? 5 : b.z == e ? 6 : b.w == e ? 7 : -1;
+    /* the ids of up to 8 chunks of 256 tokens are loaded at once (indices
+     * clamped), then the chunks are ranked in token order */
+    for (int c0 = 0; c0 < T; c0 += 8 * 256) {
+        int4 a[8], b[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int t = min(c0 + 256 * j + (int)threadIdx.x, T - 1);
+            a[j] = *(const int4 *)(ids + (size_t)t * 8);
+            b[j] = *(const int4 *)(ids + (size_t)t * 8 + 4);
         }
-        int total;
-        const int r = base + block_scan_256(k >= 0 ? 1 : 0, wsum, &total);
-        if (k >= 0) {
-            list[(size_t)e * T + r] = t;
-            rank[(size_t)t * 8 + k] = r;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (c0 + 256 * j >= T) break;
+            const int t = c0 + 256 * j + threadIdx.x;
+            int k = -1;
+            if (t < T)
+                k = a[j].x == e ? 0 : a[j].y == e ? 1 : a[j].z == e ? 2 : a[j].w == e ? 3
+                  : b[j].x == e ? 4 : b[j].y == e ? 5 : b[j].z == e ? 6 : b[j].w == e ? 7 : -1;
+            int total;
+            const int r = base + block_scan_256(k >= 0 ? 1 : 0, wsum, &total);
+            if (k >= 0) {
+                list[(size_t)e * T + r] = t;
+                rank[(size_t)t * 8 + k] = r;
+            }
+            base += total;
         }
-        base += total;
     }
     if (threadIdx.x == 0) cnt[e] = base;
 }
