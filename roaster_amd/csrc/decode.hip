@@ -375,8 +375,8 @@ __device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, cons
             P.nact = nroute + 1;
         }
     }
-    /* down slot table for the down kernel */
-    for (int i = tid; i < B * 9; i += DT) {
+    /* down slot table for the down kernel (waves 1..3, beside wave 0's list) */
+    for (int i = tid - 64; i >= 0 && i < B * 9; i += DT - 64) {
         const int t = i / 9, k = i % 9;
         if (k < RTOPK) {
             const int e = P.ids[t][k];
@@ -385,7 +385,7 @@ __device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, cons
             P.dsl[t][k] = L.sdown;
         }
     }
-    if (tid < 9) P.dq6k[tid] = tid < RTOPK ? L.q6[2] : L.sq6[2];
+    if (tid >= 64 && tid < 64 + 9) P.dq6k[tid - 64] = tid - 64 < RTOPK ? L.q6[2] : L.sq6[2];
     __syncthreads();
 }
 
