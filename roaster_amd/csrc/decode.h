@@ -55,6 +55,7 @@ struct DecArgs {
     const float *norm_w;        /* [nlayers x H] or NULL */
     float eps;
     int do_norm;
+    int xswz;                   /* activations in LDS stored swizzled (H % 512 == 0: whole 128-unit blocks per row) */
     const float *logits_in;     /* [B x E] or NULL */
     float *logits;              /* [B x E] */
     float *sgate_raw;           /* [B] */

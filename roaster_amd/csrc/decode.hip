@@ -112,6 +112,10 @@ __device__ __forceinline__ void block_copy16(void *dst, const void *src, int n16
  * conflicts), swizzled they cover all 16 (Q6_K chunks: 2 lanes per group). */
 __device__ __forceinline__ int xsw(int u) { return u ^ ((u >> 4) & 3) ^ (((u >> 6) & 1) << 3); }
 
+/* Storage position of unit u: swizzled when the rows fill whole 128-unit
+ * blocks (xsw permutes within aligned blocks of 128 units), plain otherwise. */
+__device__ __forceinline__ int xpos(int u, bool swz) { return swz ? xsw(u) : u; }
+
 /* block_copy16 with units below nsw stored at xsw(unit). */
 __device__ __forceinline__ void block_copy16_sw(void *dst, const void *src, int n16, int nsw)
 {
@@ -127,45 +131,54 @@ __device__ __forceinline__ void block_copy16_sw(void *dst, const void *src, int 
     }
 }
 
-/* The 16 activations at float offset off (a multiple of 16) of an LDS copy,
- * stored plainly or swizzled. */
-template <bool SW>
-__device__ __forceinline__ void load_x16(const float *xn, int off, float4 (&x)[4])
+/* The 16 activations at float offset off (a multiple of 16) of an LDS copy. */
+__device__ __forceinline__ void load_x16(const float *xn, int off, float4 (&x)[4], bool swz)
 {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int u = (off >> 2) + i;
-        x[i] = ((const float4 *)xn)[SW ? xsw(u) : u];
-    }
+    for (int i = 0; i < 4; i++) x[i] = ((const float4 *)xn)[xpos((off >> 2) + i, swz)];
 }
 
 /* xn[t][:] (LDS) = RMSNorm(h[t]) or a copy of x, and its 16-column run sums.
  * RMSNorm follows kernels.c:584-605: x * (1/sqrt(mean(x^2) + eps)) * w. */
+/* xn[t][:] (LDS) = RMSNorm(h[t]) or a copy of x, stored at xpos (16-byte
+ * unit u of the B x H block at xsw(u) when A.xswz), and xsum[t][r] = the sum of the 16
+ * logical elements 16 r .. 16 r + 15 (plain index), added in element order.
+ * RMSNorm follows kernels.c:584-605: x * (1/sqrt(mean(x^2) + eps)) * w.  All
+ * LDS traffic is in 16-byte units (4-byte LDS accesses issue at an eighth of
+ * the rate); H <= 2048 = 2 units per thread per token. */
 __device__ void block_norm(const DecArgs &A, int l, float *xn, float *xsum, float (*red)[RMAX_B], float *inv_rms)
 {
-    const int H = A.H, B = A.B;                 /* H <= 8 * DT */
+    const int H = A.H, B = A.B, HU = H / 4;     /* 16-byte units per token */
     const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
-    /* the norm weights of this thread's columns, loaded with h (one round trip) */
+    const bool swz = A.xswz;
+    float4 *x4 = (float4 *)xn;
+    /* norm weights of this thread's storage units (logical units xsw(u)),
+     * loaded with h */
     const float *nw = A.do_norm && A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * H : NULL;
-    float wcol[8];
+    float4 wq[2];
 #pragma unroll
-    for (int k = 0; k < 8; k++) wcol[k] = nw ? nw[min(tid + k * DT, H - 1)] : 1.0f;
-    block_copy16(xn, A.h, B * H / 4);
+    for (int k = 0; k < 2; k++)
+        wq[k] = nw ? ((const float4 *)nw)[xpos(min(tid + k * DT, HU - 1), swz)] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    block_copy16_sw(xn, A.h, B * HU, swz ? B * HU : 0);
     __syncthreads();
+    PHASE_TS(0, 3);
     if (A.do_norm) {
-        /* sums of squares of every token first, then their reductions: the
-         * tokens' reduction chains are independent and interleave */
+        /* sums of squares of every token first, then their reductions (the
+         * tokens' reduction chains are independent and interleave) */
         float ss[RMAX_B];
 #pragma unroll
         for (int t = 0; t < RMAX_B; t++) {
             ss[t] = 0.0f;
             if (t < B) {
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const int i = tid + k * DT;
-                    if (i < H) {
-                        const float v = xn[t * H + i];
-                        ss[t] = fmaf(v, v, ss[t]);
+                for (int k = 0; k < 2; k++) {
+                    const int u = tid + k * DT;
+                    if (u < HU) {
+                        const float4 v = x4[t * HU + u];
+                        ss[t] = fmaf(v.x, v.x, ss[t]);
+                        ss[t] = fmaf(v.y, v.y, ss[t]);
+                        ss[t] = fmaf(v.z, v.z, ss[t]);
+                        ss[t] = fmaf(v.w, v.w, ss[t]);
                     }
                 }
             }
@@ -178,6 +191,7 @@ __device__ void block_norm(const DecArgs &A, int l, float *xn, float *xsum, floa
             }
         }
         __syncthreads();
+        PHASE_TS(0, 4);
         if (tid < B) {
             float s2 = 0.0f;
             for (int w = 0; w < DW; w++) s2 += red[w][tid];
@@ -187,17 +201,25 @@ __device__ void block_norm(const DecArgs &A, int l, float *xn, float *xsum, floa
         for (int t = 0; t < B; t++) {
             const float inv = inv_rms[t];
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const int i = tid + k * DT;
-                if (i < H) {
-                    const float v = xn[t * H + i] * inv;
-                    xn[t * H + i] = nw ? v * wcol[k] : v;
+            for (int k = 0; k < 2; k++) {
+                const int u = tid + k * DT;
+                if (u < HU) {
+                    float4 v = x4[t * HU + u];
+                    v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
+                    if (nw) { v.x *= wq[k].x; v.y *= wq[k].y; v.z *= wq[k].z; v.w *= wq[k].w; }
+                    x4[t * HU + u] = v;
                 }
             }
         }
         __syncthreads();
+        PHASE_TS(0, 5);
     }
-    for (int r = tid; r < B * (H / 16); r += DT) xsum[r] = sum16(xn + r * 16);
+    for (int r = tid; r < B * (H / 16); r += DT) {       /* the order of sum16 (qdot.h) */
+        const float4 a = x4[xpos(4 * r, swz)], b = x4[xpos(4 * r + 1, swz)];
+        const float4 c = x4[xpos(4 * r + 2, swz)], d = x4[xpos(4 * r + 3, swz)];
+        xsum[r] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)) +
+                  (((c.x + c.y) + (c.z + c.w)) + ((d.x + d.y) + (d.z + d.w)));
+    }
     __syncthreads();
 }
 
@@ -217,7 +239,7 @@ __device__ __forceinline__ QChunk2 load_gu_pair(const uint8_t *g, const uint8_t 
 
 /* eh[p][j] = silu(gate_j . x_t) * (up_j . x_t) for the (t, slot) pairs p of one
  * expert, given the lane's chunks of gate row j and up row j. */
-template <bool G6, bool U6, bool SW>
+template <bool G6, bool U6>
 __device__ __forceinline__ void gu_row(const DecArgs &A, int j, const QChunk2 &ch, int ntok, const int *tk,
                                        const float *xn, const float *xsum)
 {
@@ -231,11 +253,11 @@ __device__ __forceinline__ void gu_row(const DecArgs &A, int j, const QChunk2 &c
         float pg = 0.0f, pu = 0.0f;
         if (lb < nb) {
             float4 x0[4], x1[4];
-            load_x16<SW>(xn, t * H + ga, x0);
-            load_x16<SW>(xn, t * H + gb, x1);
+            load_x16(xn, t * H + ga, x0, A.xswz);
+            load_x16(xn, t * H + gb, x1, A.xswz);
             pg = q_chunk_dot_r<G6>(ch.g, c, x0, x1, xs[ga >> 4], xs[gb >> 4]);
-            load_x16<SW>(xn, t * H + ua, x0);
-            load_x16<SW>(xn, t * H + ub, x1);
+            load_x16(xn, t * H + ua, x0, A.xswz);
+            load_x16(xn, t * H + ub, x1, A.xswz);
             pu = q_chunk_dot_r<U6>(ch.u, c, x0, x1, xs[ua >> 4], xs[ub >> 4]);
         }
         pg = group_sum<64>(pg);
@@ -294,7 +316,7 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A,
 #pragma unroll
                 for (int t = 0; t < RMAX_B; t++) {
                     if (t < B) {
-                        const float4 x = *(const float4 *)(xn + t * H + c0);
+                        const float4 x = ((const float4 *)xn)[xpos((t * H + c0) >> 2, A.xswz)];
                         acc[t] = fmaf(w[m].x, x.x, acc[t]);
                         acc[t] = fmaf(w[m].y, x.y, acc[t]);
                         acc[t] = fmaf(w[m].z, x.z, acc[t]);
@@ -314,10 +336,10 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A,
             }
         }
     } else if (is_sh) {
-        if (kind == 0) gu_row<false, false, false>(A, j, ch, B, sh_tk, xn, xsum);
-        else if (kind == 3) gu_row<true, true, false>(A, j, ch, B, sh_tk, xn, xsum);
-        else if (kind == 2) gu_row<true, false, false>(A, j, ch, B, sh_tk, xn, xsum);
-        else gu_row<false, true, false>(A, j, ch, B, sh_tk, xn, xsum);
+        if (kind == 0) gu_row<false, false>(A, j, ch, B, sh_tk, xn, xsum);
+        else if (kind == 3) gu_row<true, true>(A, j, ch, B, sh_tk, xn, xsum);
+        else if (kind == 2) gu_row<true, false>(A, j, ch, B, sh_tk, xn, xsum);
+        else gu_row<false, true>(A, j, ch, B, sh_tk, xn, xsum);
     }
     PHASE_TS(0, 2);
 }
@@ -433,10 +455,10 @@ __device__ void gu_tasks(const DecArgs &A, const DecPlan &P, int q0, int q1, con
     float4 xga[4], xgb[4], xua[4], xub[4];
     float sga = 0.0f, sgb = 0.0f, sua = 0.0f, sub = 0.0f;
     if (ONE && lb < nb) {
-        load_x16<true>(xn, ga, xga);
-        load_x16<true>(xn, gb, xgb);
-        load_x16<true>(xn, ua, xua);
-        load_x16<true>(xn, ub, xub);
+        load_x16(xn, ga, xga, A.xswz);
+        load_x16(xn, gb, xgb, A.xswz);
+        load_x16(xn, ua, xua, A.xswz);
+        load_x16(xn, ub, xub, A.xswz);
         sga = xsum[ga >> 4]; sgb = xsum[gb >> 4]; sua = xsum[ua >> 4]; sub = xsum[ub >> 4];
     }
     constexpr int PF = ONE ? GU_PF : GU_PF_B;
@@ -463,7 +485,7 @@ __device__ void gu_tasks(const DecArgs &A, const DecPlan &P, int q0, int q1, con
                 pu = group_sum<64>(pu);
                 if (lane == 0) A.eh[(size_t)X.tk[0] * I + q % I] = silu_mul(pg, pu);
             } else {
-                gu_row<G6, U6, true>(A, q % I, ch[f], X.ntok, X.tk, xn, xsum);
+                gu_row<G6, U6>(A, q % I, ch[f], X.ntok, X.tk, xn, xsum);
             }
         }
     }
@@ -490,15 +512,6 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int
     if (A.ffn_out) {
         ffn_plan(A, P);
         block_norm(A, l, xn, xsum, red, inv_rms);
-        for (int u = threadIdx.x; u < B * A.H / 4; u += DT) {     /* swizzle in place (xsw is an involution) */
-            const int v = xsw(u);
-            if (u < v) {
-                const float4 a = ((float4 *)xn)[u], b = ((float4 *)xn)[v];
-                ((float4 *)xn)[u] = b;
-                ((float4 *)xn)[v] = a;
-            }
-        }
-        __syncthreads();
     } else {
         /* logits of this wave's tokens and the shared-gate logits, loaded with h */
         const int lane = threadIdx.x & 63, wv = wave_id();
@@ -513,7 +526,7 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int
         }
         const float sg = threadIdx.x < B ? A.sgate_raw[threadIdx.x] : 0.0f;
         const DecLayer L = A.layers[l];
-        block_copy16_sw(xn, A.xn_g, B * (A.H + A.H / 16) / 4, B * A.H / 4);
+        block_copy16(xn, A.xn_g, B * (A.H + A.H / 16) / 4);     /* published swizzled by the router kernel */
         __syncthreads();
         PHASE_TS(1, 1);
         build_plan(A, L, P, lg4, sg, emask);
@@ -698,6 +711,7 @@ static int launch_layer(const DecArgs &A, int l, bool with_router)
 
 int dec_launch(DecArgs &A)
 {
+    A.xswz = A.H % 512 == 0;
     if (A.E > 256) return rt_fail(ROASTER_EINVAL, "decode supports at most 256 routed experts");
     unsigned *ctrl = rt_ctrl();
     A.plan_g = (DecPlan *)rt_scratch(SCR_C, sizeof(DecPlan));
@@ -710,6 +724,7 @@ int dec_launch(DecArgs &A)
 
 int dec_ffn_launch(DecArgs &A)
 {
+    A.xswz = A.H % 512 == 0;
     unsigned *ctrl = rt_ctrl();
     A.plan_g = (DecPlan *)rt_scratch(SCR_C, sizeof(DecPlan));
     if (!ctrl || !A.plan_g) return ROASTER_ENOMEM;

@@ -112,17 +112,18 @@ def test_decode_reports_routing_failure(cfg2):
     assert R.lib().roaster_sync() == 0        # the error is reported once
 
 
-def oracle_stack(table, h0, n_layers, eps=1e-6):
-    """h <- h + MoE_l(RMSNorm(h)) per layer with unit norm weights, per token."""
+def oracle_stack(table, h0, n_layers, eps=1e-6, norm_w=None):
+    """h <- h + MoE_l(RMSNorm(h)) per layer, per token; norm_w [n_layers x H]
+    or None for unit norm weights."""
     B, H = h0.shape
-    ones = np.ones(H, np.float32)
     h = h0.copy()
     ids_all = np.zeros((n_layers, B, 8), np.int32)
     for l in range(n_layers):
+        nw = np.ascontiguousarray(norm_w[l]) if norm_w is not None else np.ones(H, np.float32)
         router, _ = table.router(l)
         for t in range(B):
             xn = np.empty(H, np.float32)
-            O.orc().orc_rmsnorm(xn.ctypes.data, h[t].ctypes.data, ones.ctypes.data, H, C.c_float(eps))
+            O.orc().orc_rmsnorm(xn.ctypes.data, h[t].ctypes.data, nw.ctypes.data, H, C.c_float(eps))
             lg = O.matvec_f32(router, xn)
             ids, _ = O.select_top8(lg)
             L = table.oracle_layer(l, set(ids.tolist()))
@@ -149,6 +150,31 @@ def test_decode_stack_4_layers(B):
         assert np.array_equal(ids, ids_ref)
         err = rel_err(h - h0, h_ref - h0)
         log(f"stack B={B}: max|d|/max|ffn| = {err:.3e}")
+        assert err <= TOL and err <= TIGHT
+    finally:
+        t.destroy()
+
+
+@pytest.mark.parametrize("hidden", [768, 2048])
+def test_decode_stack_norm_weights_batch8(hidden):
+    """Per-layer RMSNorm weights and 8 tokens, at a hidden size whose rows fill
+    whole 512-float blocks (activations swizzled in LDS) and at one that does
+    not (stored plainly)."""
+    B, NL = 8, 2
+    log(f"decode stack {NL} layers B={B} hidden={hidden}, norm weights")
+    t = SynthTable(5, n_layers=NL, n_experts=64, hidden=hidden)
+    try:
+        h0 = np.stack([R.synth_normal(5, R.synth_stream(0, i, 5), hidden) for i in range(B)])
+        nw = np.stack([1.0 + 0.25 * R.synth_normal(6, R.synth_stream(l, 0, 6), hidden) for l in range(NL)])
+        dh, dn = Dev(h0), Dev(np.ascontiguousarray(nw, np.float32))
+        di = Dev(nbytes=NL * B * 8 * 4, dtype=np.int32, shape=(NL, B, 8))
+        R.check(R.lib().roaster_moe_decode_stack(t.t, dh.p, B, 0, NL, dn.p, C.c_float(1e-6), di.p, None))
+        R.check(R.lib().roaster_sync())
+        h, ids = dh.get(), di.get()
+        h_ref, ids_ref = oracle_stack(t, h0, NL, norm_w=nw.astype(np.float32))
+        assert np.array_equal(ids, ids_ref)
+        err = rel_err(h - h0, h_ref - h0)
+        log(f"stack B={B} hidden={hidden}: max|d|/max|ffn| = {err:.3e}")
         assert err <= TOL and err <= TIGHT
     finally:
         t.destroy()
