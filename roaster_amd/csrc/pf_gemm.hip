@@ -202,7 +202,7 @@ __global__ void __launch_bounds__(GT) pf_down_kernel(PfGemmArgs A)
 #define V2_MC 96                  /* rows per tile */
 #define V2_LD (GK + 8)            /* LDS row stride (fp16 elements) */
 #ifndef PF_DN_NT
-#define PF_DN_NT 2                /* down output tiles per workgroup (inter <= 512) */
+#define PF_DN_NT 4                /* down output tiles per workgroup (inter <= 512) */
 #endif
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
