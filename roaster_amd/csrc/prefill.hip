@@ -325,13 +325,16 @@ extern "C" __global__ void __launch_bounds__(256) pf_combine_kernel(const float 
                                                                     float *Y, int T, int H)
 {
     const int t = blockIdx.x;
-    int id[8], sl[8];
+    int id[8], sl[8], rk[8], id0[8];
     float wt[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
+    for (int k = 0; k < 8; k++) {       /* the token's ids, weights and ranks in one round trip */
         id[k] = ids[(size_t)t * 8 + k];
         wt[k] = w[(size_t)t * 8 + k];
+        rk[k] = rank[(size_t)t * 8 + k];
     }
+#pragma unroll
+    for (int k = 0; k < 8; k++) id0[k] = id[k];
     /* ascending expert id (ids of one token are distinct; -1 = unrouted) */
 #pragma unroll
     for (int i = 1; i < 8; i++)
@@ -346,22 +349,36 @@ extern "C" __global__ void __launch_bounds__(256) pf_combine_kernel(const float 
     for (int k = 0; k < 8; k++) {
         sl[k] = -1;
         if (id[k] >= 0) {
-            int kk = 0;
+            int r = 0;
 #pragma unroll
             for (int j = 0; j < 8; j++)
-                if (ids[(size_t)t * 8 + j] == id[k]) kk = j;
-            sl[k] = off[id[k]] + rank[(size_t)t * 8 + kk];
+                if (id0[j] == id[k]) r = rk[j];
+            sl[k] = off[id[k]] + r;
         }
     }
     const float g = sg[t];
     const float *sh = ed + ((size_t)8 * T + t) * H;
-    for (int i = threadIdx.x * 4; i < H; i += 1024) {
-        const float4 s = *(const float4 *)(sh + i);
-        float4 y = make_float4(g * s.x, g * s.y, g * s.z, g * s.w);
+    /* H <= 2048: two float4 columns per thread, all 18 row loads issued
+     * before the first use (columns clamped, unrouted slots read the shared
+     * row; neither is used) */
+    float4 s4[2], d4[2][8];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        const int i = min((int)threadIdx.x * 4 + 1024 * c, H - 4);
+        s4[c] = *(const float4 *)(sh + i);
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            d4[c][k] = *(const float4 *)((sl[k] >= 0 ? ed + (size_t)sl[k] * H : sh) + i);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        const int i = threadIdx.x * 4 + 1024 * c;
+        if (i >= H) break;
+        float4 y = make_float4(g * s4[c].x, g * s4[c].y, g * s4[c].z, g * s4[c].w);
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             if (sl[k] < 0) continue;
-            const float4 d = *(const float4 *)(ed + (size_t)sl[k] * H + i);
+            const float4 d = d4[c][k];
             y.x = fmaf(wt[k], d.x, y.x);
             y.y = fmaf(wt[k], d.y, y.y);
             y.z = fmaf(wt[k], d.z, y.z);
