@@ -1,8 +1,9 @@
 /*
  * prefill.hip -- the MoE block over T tokens (model.c:1671-1791) on the GPU.
  *
- *   pf_router_kernel   logits = X . W_r^T in f32, split over K into 4 partial
- *                      sums added in fixed order (model.c:1679)
+ *   pf_router_mfma_kernel  logits = X . W_r^T in f32 on v_mfma_f32_32x32x2_f32,
+ *                      split over K into 4 partial sums added in fixed order
+ *                      by the token kernel (model.c:1679)
  *   pf_token_kernel    one wave per token: logits (+ bias), top-8 and
  *                      renormalised weights (model.c:1681-1692), the shared
  *                      expert's sigmoid gate (model.c:1707-1708), the row
@@ -66,57 +67,91 @@ __device__ int block_scan_256(int v, int *lds, int *total)
     return before + inc - v;
 }
 
-/* ---- router: part[s][t][e] = sum over k in split s of X[t][k] * W[e][k] ---- */
-#define RT_TM 32
-#define RT_TN 64
-#define RT_KC 32
+/* ---- router on MFMA: part[s][t][e] = sum over k in split s of X[t][k] W[e][k]
+ * A workgroup (4 waves) takes 32 tokens x 128 experts of K split s; wave w
+ * owns experts e0 + 32 w .. + 31 in one v_mfma_f32_32x32x2_f32 accumulator
+ * (A = X rows, B = W rows, fp32 products and sums).  The tokens' K slice is
+ * staged once in LDS (row stride klen + 4 floats: the 16 rows a ds_read_b128
+ * pass reads fall in 16 different bank groups); each wave reads its weight
+ * rows straight from global memory, one 32-wide K chunk ahead.  In a chunk,
+ * lane half h supplies k = 16 h + j to MFMA j (j = 0..15), so 16 MFMAs cover
+ * the chunk and every lane reads 16 consecutive floats of X and of W. */
+#define RM_E 128                  /* experts per workgroup */
+#define RM_T 32                   /* tokens per workgroup */
 
-extern "C" __global__ void __launch_bounds__(256) pf_router_kernel(const float *X, const float *W, float *part, int T,
-                                                                   int E, int H)
+extern "C" __global__ void __launch_bounds__(256, 2) pf_router_mfma_kernel(const float *X, const float *W, float *part,
+                                                                           int T, int E, int H)
 {
-    __shared__ float Xs[RT_KC][RT_TM + 4];
-    __shared__ float Ws[RT_KC][RT_TN + 4];
-    const int t = threadIdx.x;
-    const int n0 = blockIdx.x * RT_TN, m0 = blockIdx.y * RT_TM, s = blockIdx.z;
-    const int klen = H / RT_KSPLIT, kbeg = s * klen;
-    const int ty = t >> 4, tx = t & 15;
-    float acc[2][4] = {};
-    /* loaders: X row t/8 (32 rows), k 4*(t%8); W rows t/8 and 32 + t/8 */
-    const int xr = t >> 3, xk = 4 * (t & 7);
-    const float *xp = (m0 + xr < T) ? X + (size_t)(m0 + xr) * H + kbeg + xk : nullptr;
-    const float *wp0 = (n0 + xr < E) ? W + (size_t)(n0 + xr) * H + kbeg + xk : nullptr;
-    const float *wp1 = (n0 + 32 + xr < E) ? W + (size_t)(n0 + 32 + xr) * H + kbeg + xk : nullptr;
-    for (int k0 = 0; k0 < klen; k0 += RT_KC) {
-        const float4 a = xp ? *(const float4 *)(xp + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 b0 = wp0 ? *(const float4 *)(wp0 + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 b1 = wp1 ? *(const float4 *)(wp1 + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
-        __syncthreads();
-        Xs[xk + 0][xr] = a.x; Xs[xk + 1][xr] = a.y; Xs[xk + 2][xr] = a.z; Xs[xk + 3][xr] = a.w;
-        Ws[xk + 0][xr] = b0.x; Ws[xk + 1][xr] = b0.y; Ws[xk + 2][xr] = b0.z; Ws[xk + 3][xr] = b0.w;
-        Ws[xk + 0][32 + xr] = b1.x; Ws[xk + 1][32 + xr] = b1.y; Ws[xk + 2][32 + xr] = b1.z; Ws[xk + 3][32 + xr] = b1.w;
-        __syncthreads();
-#pragma unroll 8
-        for (int k = 0; k < RT_KC; k++) {
-            const float2 av = *(const float2 *)&Xs[k][2 * ty];
-            const float4 bv = *(const float4 *)&Ws[k][4 * tx];
-            acc[0][0] = fmaf(av.x, bv.x, acc[0][0]); acc[0][1] = fmaf(av.x, bv.y, acc[0][1]);
-            acc[0][2] = fmaf(av.x, bv.z, acc[0][2]); acc[0][3] = fmaf(av.x, bv.w, acc[0][3]);
-            acc[1][0] = fmaf(av.y, bv.x, acc[1][0]); acc[1][1] = fmaf(av.y, bv.y, acc[1][1]);
-            acc[1][2] = fmaf(av.y, bv.z, acc[1][2]); acc[1][3] = fmaf(av.y, bv.w, acc[1][3]);
-        }
+    extern __shared__ __align__(16) float xs[];         /* [RM_T][klen + 4] */
+    const int tid = threadIdx.x, l = tid & 63, h = l >> 5, n = l & 31;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = blockIdx.x * RM_T, e0 = blockIdx.y * RM_E + 32 * w, s = blockIdx.z;
+    const int klen = H / RT_KSPLIT, kbeg = s * klen, ld = klen + 4;
+    /* stage X[t0 .. t0 + 31][kbeg .. kbeg + klen) (klen <= 512: at most 16
+     * float4 per thread, all loaded before the first store; rows past T read
+     * row T - 1, pieces past the slice repeat its last one) */
+    const int q4 = klen / 4, nq = RM_T * q4;           /* float4 per row, in the slice */
+    float4 v[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const int i = min(tid + 256 * k, nq - 1), r = i / q4, c = i - r * q4;
+        v[k] = *(const float4 *)(X + (size_t)min(t0 + r, T - 1) * H + kbeg + 4 * c);
     }
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int m = m0 + 2 * ty + i;
-        if (m >= T) continue;
-        float *dst = part + ((size_t)s * T + m) * E;
+    for (int k = 0; k < 16; k++) {
+        const int i = min(tid + 256 * k, nq - 1), r = i / q4, c = i - r * q4;
+        *(float4 *)(xs + r * ld + 4 * c) = v[k];
+    }
+    __syncthreads();
+    /* this lane's weight row (clamped past E; those columns are not stored) */
+    const float *wr = W + (size_t)min(e0 + n, E - 1) * H + kbeg + 16 * h;
+    const float *xr = xs + n * ld + 16 * h;
+    f32x16 acc = (f32x16){};
+    /* weights in batches of RM_B chunks, the next batch loaded during the
+     * current one (chunk indices clamped; chunks past nch are not used) */
+    constexpr int RM_B = 4;
+    const int nch = klen / 32;
+    float4 wb[2][RM_B][4];
+    auto w_batch = [&](float4 (&dst)[RM_B][4], int c0) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int n = n0 + 4 * tx + j;
-            if (n < E) dst[n] = acc[i][j];
+        for (int j = 0; j < RM_B; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) dst[j][q] = *(const float4 *)(wr + 32 * min(c0 + j, nch - 1) + 4 * q);
+    };
+    auto compute = [&](const float4 (&src)[RM_B][4], int c0) {
+#pragma unroll
+        for (int j = 0; j < RM_B; j++) {
+            if (c0 + j >= nch) break;
+            float4 xa[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) xa[q] = *(const float4 *)(xr + 32 * (c0 + j) + 4 * q);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q].x, src[j][q].x, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q].y, src[j][q].y, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q].z, src[j][q].z, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q].w, src[j][q].w, acc, 0, 0, 0);
+            }
+        }
+    };
+    w_batch(wb[0], 0);
+    for (int c = 0; c < nch; c += 2 * RM_B) {
+        w_batch(wb[1], c + RM_B);
+        compute(wb[0], c);
+        if (c + RM_B >= nch) break;
+        w_batch(wb[0], c + 2 * RM_B);
+        compute(wb[1], c + RM_B);
+    }
+    /* D item i: token t0 + 8 (i / 4) + 4 h + i % 4, expert e0 + n */
+    if (e0 + n < E) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int m = t0 + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (m < T) part[((size_t)s * T + m) * E + e0 + n] = acc[i];
         }
     }
 }
+
 
 /* ---- per token: logits, top-8, shared gate, X row scale ------------------ */
 struct PfTokArgs {
@@ -429,8 +464,10 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     const DecLayer &L = t->layers_h[layer];
 
     if (!opt.logits_in) {
-        dim3 g((E + RT_TN - 1) / RT_TN, (T + RT_TM - 1) / RT_TM, RT_KSPLIT);
-        hipLaunchKernelGGL(pf_router_kernel, g, dim3(256), 0, R.stream, X, L.router, (float *)(ws + o_part), T, E, H);
+        dim3 g((T + RM_T - 1) / RM_T, (E + RM_E - 1) / RM_E, RT_KSPLIT);
+        const size_t xlds = (size_t)RM_T * (H / RT_KSPLIT + 4) * 4;
+        hipLaunchKernelGGL(pf_router_mfma_kernel, g, dim3(256), xlds, R.stream, X, L.router, (float *)(ws + o_part), T,
+                           E, H);
         if (rt_check(hipGetLastError(), "prefill router launch")) return ROASTER_EDEVICE;
     }
     PfTokArgs ta;

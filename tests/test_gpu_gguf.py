@@ -93,6 +93,8 @@ def test_prefill_from_gguf(loaded, layer):
     R.check(R.lib().roaster_moe_prefill(t, layer, dx.p, T, dy.p, C.byref(o)), "prefill")
     R.check(R.lib().roaster_sync(), "sync")
     Y, lg = dy.get(), dl.get()
+    lg_ref = np.stack([O.matvec_f32(m.router[layer], X[t]) for t in range(T)])   # T, E not multiples of 32
+    assert rel_err(lg, lg_ref) <= 1e-5
     rc, Y_ref, _, _, _ = oracle_layer(m, layer).prefill(X, logits_in=lg)
     assert rc == 0
     err = rel_err(Y, Y_ref)
