@@ -444,28 +444,9 @@ __device__ __forceinline__ int type_run_end(const DecPlan &P, int a0, int a_end,
  * then computes them.  With one token (decode batch 1 and kernel_ffn_fused)
  * the lane's activations are loaded into registers once and reused by every
  * task. */
-/* Warm the last-level cache with this layer's down matrices (the plan's
- * active experts): one dword per 128-byte line, spread over the grid, so that
- * the down kernel's weight loads hit the cache.  Issued after the gate/up
- * kernel's first batch of weight loads (vmcnt retires in order: issued
- * before them, the warming would delay their use), unconditionally (expert
- * slot and line clamped); the caller keeps the value in a data-dependent
- * sink so the load stays. */
-__device__ __forceinline__ uint32_t warm_down(const DecArgs &A, const DecPlan &P)
-{
-    const size_t lpe = (size_t)A.H * (A.I / RQK) * RQ6K_BYTES / 128;   /* lines per expert slot (Q6_K bound) */
-    const size_t g = (size_t)blockIdx.x * DT + threadIdx.x;
-    const int a = min((int)(g / lpe), P.nact - 1);
-    const size_t lines = (size_t)A.H * (A.I / RQK) * (P.a[a].dq6 ? RQ6K_BYTES : RQ4K_BYTES) / 128;
-    const size_t li = min(g % lpe, lines - 1);
-    return *(const GAS uint32_t *)(P.a[a].d + li * 128);
-}
-
 template <bool G6, bool U6, bool ONE>
-__device__ uint32_t gu_tasks(const DecArgs &A, const DecPlan &P, int q0, int q1, const float *xn, const float *xsum,
-                             bool do_warm)
+__device__ void gu_tasks(const DecArgs &A, const DecPlan &P, int q0, int q1, const float *xn, const float *xsum)
 {
-    uint32_t warm = 0;
     const int H = A.H, I = A.I, nb = H / RQK;
     const int lane = threadIdx.x & 63, c = lane & 7, lb = lane >> 3;
     const int gw = blockIdx.x * DW + wave_id(), nw = gridDim.x * DW;
@@ -489,10 +470,6 @@ __device__ uint32_t gu_tasks(const DecArgs &A, const DecPlan &P, int q0, int q1,
             const DecActive &X = P.a[q / I];
             ch[f] = load_gu_pair<G6, U6>(X.g, X.u, q % I, nb, lb, c);
         }
-        if (do_warm) {                  /* after the first batch of weight loads */
-            warm = warm_down(A, P);
-            do_warm = false;
-        }
 #pragma unroll
         for (int f = 0; f < PF; f++) {
             const int q = qs + f * nw;
@@ -512,16 +489,14 @@ __device__ uint32_t gu_tasks(const DecArgs &A, const DecPlan &P, int q0, int q1,
             }
         }
     }
-    if (do_warm) warm = warm_down(A, P);   /* a wave without tasks still warms its lines */
-    return warm;
 }
 
 template <bool G6, bool U6>
-__device__ __forceinline__ uint32_t gu_tasks_any(const DecArgs &A, const DecPlan &P, int q0, int q1, const float *xn,
-                                                 const float *xsum, bool do_warm)
+__device__ __forceinline__ void gu_tasks_any(const DecArgs &A, const DecPlan &P, int q0, int q1, const float *xn,
+                                             const float *xsum)
 {
-    if (A.B == 1) return gu_tasks<G6, U6, true>(A, P, q0, q1, xn, xsum, do_warm);
-    return gu_tasks<G6, U6, false>(A, P, q0, q1, xn, xsum, do_warm);
+    if (A.B == 1) gu_tasks<G6, U6, true>(A, P, q0, q1, xn, xsum);
+    else gu_tasks<G6, U6, false>(A, P, q0, q1, xn, xsum);
 }
 
 extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int l)
@@ -567,16 +542,28 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int
         }
         if (tid == 0 && P.err) atomicOr(A.err, 1);
     }
-    uint32_t warm = 0;                  /* set by the first gu_tasks call (cache warming, below) */
-    bool do_warm = !A.ffn_out;
+    /* Warm the last-level cache with this layer's down matrices (the plan's
+     * active experts): one dword per 128-byte line, spread over the grid, so
+     * that the down kernel's weight loads hit the cache.  The value is folded
+     * into a condition that is never true so the load is kept. */
+    uint32_t warm = 0;
+    if (!A.ffn_out) {
+        const size_t lpe = (size_t)A.H * (A.I / RQK) * RQ6K_BYTES / 128;   /* lines per expert slot (Q6_K bound) */
+        const size_t g = (size_t)blockIdx.x * DT + threadIdx.x;
+        const int a = (int)(g / lpe);
+        if (a < P.nact) {
+            const size_t lines = (size_t)A.H * (A.I / RQK) * (P.a[a].dq6 ? RQ6K_BYTES : RQ4K_BYTES) / 128;
+            const size_t li = g % lpe;
+            if (li < lines) warm = *(const GAS uint32_t *)(P.a[a].d + li * 128);
+        }
+    }
     for (int a0 = 0; a0 < P.nroute;) {
         const int a1 = type_run_end(P, a0, P.nroute, true);
         const int kind = (P.a[a0].gq6 ? 2 : 0) | (P.a[a0].uq6 ? 1 : 0);
-        if (kind == 0) warm ^= gu_tasks_any<false, false>(A, P, a0 * I, a1 * I, xn, xsum, do_warm);
-        else if (kind == 3) warm ^= gu_tasks_any<true, true>(A, P, a0 * I, a1 * I, xn, xsum, do_warm);
-        else if (kind == 2) warm ^= gu_tasks_any<true, false>(A, P, a0 * I, a1 * I, xn, xsum, do_warm);
-        else warm ^= gu_tasks_any<false, true>(A, P, a0 * I, a1 * I, xn, xsum, do_warm);
-        do_warm = false;
+        if (kind == 0) gu_tasks_any<false, false>(A, P, a0 * I, a1 * I, xn, xsum);
+        else if (kind == 3) gu_tasks_any<true, true>(A, P, a0 * I, a1 * I, xn, xsum);
+        else if (kind == 2) gu_tasks_any<true, false>(A, P, a0 * I, a1 * I, xn, xsum);
+        else gu_tasks_any<false, true>(A, P, a0 * I, a1 * I, xn, xsum);
         a0 = a1;
     }
     PHASE_TS(1, 3);
