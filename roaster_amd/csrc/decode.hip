@@ -46,6 +46,7 @@
 #ifndef D_PF
 #define D_PF 4                        /* down tasks in flight per wave */
 #endif
+#define LGKM_ONLY 0xC07F              /* s_waitcnt lgkmcnt(0), leaving vector-memory loads in flight */
 
 /* Opt-in phase tracing (build with -DROASTER_PHASE_TS): thread 0 of every
  * workgroup records the 100 MHz real-time counter at phase boundaries;
@@ -346,16 +347,12 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A,
 
 /* ---- GU: routing plan + routed experts' gate/up ----------------------------- */
 
-/* Active-expert plan: union of the tokens' experts in first-appearance order
- * over (t, k), then the shared expert.  Pair p = t*9 + k (k = 8: shared).
- * emask: 256 x 64-bit LDS scratch. */
-__device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, const float (*lg4)[4], float sg,
-                           unsigned long long *emask)
+/* Active-expert plan from the tokens' top-8 ids in P: union of the tokens'
+ * experts in first-appearance order over (t, k), then the shared expert.
+ * Pair p = t*9 + k (k = 8: shared).  emask: 256 x 64-bit LDS scratch. */
+__device__ __forceinline__ void plan_from_ids(const DecArgs &A, const DecLayer &L, DecPlan &P, float sg, unsigned long long *emask)
 {
-    const int B = A.B, E = A.E, tid = threadIdx.x, wv = wave_id(), lane = tid & 63;
-    if (tid == 0) P.err = 0;
-    __syncthreads();
-    for (int t = wv, r = 0; t < B; t += DW, r++) topk8_wave(lg4[r], E, P.ids[t], P.w[t], &P.err);
+    const int B = A.B, tid = threadIdx.x, wv = wave_id(), lane = tid & 63;
     if (tid < B) P.w[tid][8] = 1.0f / (1.0f + expf(-sg));
     __syncthreads();
     PHASE_TS(1, 4);
@@ -364,10 +361,10 @@ __device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, cons
         const int e = lane < n ? P.ids[lane >> 3][lane & 7] : -1;
         const bool valid = e >= 0;
         if (valid) emask[e] = 0ull;
-        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_s_waitcnt(LGKM_ONLY);
         __builtin_amdgcn_wave_barrier();
         if (valid) atomicOr(&emask[e], 1ull << lane);
-        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_s_waitcnt(LGKM_ONLY);
         __builtin_amdgcn_wave_barrier();
         const unsigned long long m = valid ? emask[e] : 0ull;
         const bool leader = valid && (__ffsll((long long)m) - 1) == lane;
@@ -409,6 +406,16 @@ __device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, cons
     }
     if (tid >= 64 && tid < 64 + 9) P.dq6k[tid - 64] = tid - 64 < RTOPK ? L.q6[2] : L.sq6[2];
     __syncthreads();
+}
+
+/* Plan of B tokens: wave w computes the top-8 of tokens w, w + 4, ... */
+__device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, const float (*lg4)[4], float sg,
+                           unsigned long long *emask)
+{
+    if (threadIdx.x == 0) P.err = 0;
+    __syncthreads();
+    for (int t = wave_id(), r = 0; t < A.B; t += DW, r++) topk8_wave(lg4[r], A.E, P.ids[t], P.w[t], &P.err);
+    plan_from_ids(A, L, P, sg, emask);
 }
 
 __device__ void ffn_plan(const DecArgs &A, DecPlan &P)
@@ -499,6 +506,135 @@ __device__ __forceinline__ void gu_tasks_any(const DecArgs &A, const DecPlan &P,
     else gu_tasks<G6, U6, false>(A, P, q0, q1, xn, xsum);
 }
 
+/* Publish the plan (workgroup 0: the plan for the down kernel, ids and
+ * weights for the caller, the routing error), then warm the last-level cache
+ * with this layer's down matrices (the plan's active experts): one dword per
+ * 128-byte line, spread over the grid, so that the down kernel's weight loads
+ * hit the cache.  Returns the loaded value, which the kernel folds into a
+ * condition that is never true so the load is kept. */
+__device__ __forceinline__ uint32_t publish_and_warm(const DecArgs &A, const DecPlan &P, int l)
+{
+    const int B = A.B, tid = threadIdx.x;
+    if (blockIdx.x == 0) {
+        for (int i = tid; i < (int)(sizeof(DecPlan) / 16); i += DT) ((uint4 *)A.plan_g)[i] = ((const uint4 *)&P)[i];
+        if (!A.ffn_out && tid < B * RTOPK) {
+            const size_t o = ((size_t)(l - A.layer0) * B + (tid >> 3)) * RTOPK + (tid & 7);
+            if (A.ids_out) A.ids_out[o] = P.ids[tid >> 3][tid & 7];
+            if (A.w_out) A.w_out[o] = P.w[tid >> 3][tid & 7];
+        }
+        if (tid == 0 && P.err) atomicOr(A.err, 1);
+    }
+    uint32_t warm = 0;
+    if (!A.ffn_out) {
+        const size_t lpe = (size_t)A.H * (A.I / RQK) * RQ6K_BYTES / 128;   /* lines per expert slot (Q6_K bound) */
+        const size_t g = (size_t)blockIdx.x * DT + tid;
+        const int a = (int)(g / lpe);
+        if (a < P.nact) {
+            const size_t lines = (size_t)A.H * (A.I / RQK) * (P.a[a].dq6 ? RQ6K_BYTES : RQ4K_BYTES) / 128;
+            const size_t li = g % lpe;
+            if (li < lines) warm = *(const GAS uint32_t *)(P.a[a].d + li * 128);
+        }
+    }
+    return warm;
+}
+
+/* Gate/up rows of every routed active expert of the plan, in runs of equal
+ * matrix types (ONE: the plan has one token).  Each kernel calls it from one
+ * place, so that it is inlined. */
+template <bool ONE>
+__device__ __forceinline__ void gu_all(const DecArgs &A, const DecPlan &P, const float *xn, const float *xsum)
+{
+    const int I = A.I;
+    for (int a0 = 0; a0 < P.nroute;) {
+        const int a1 = type_run_end(P, a0, P.nroute, true);
+        const int kind = (P.a[a0].gq6 ? 2 : 0) | (P.a[a0].uq6 ? 1 : 0);
+        if (ONE) {
+            if (kind == 0) gu_tasks<false, false, true>(A, P, a0 * I, a1 * I, xn, xsum);
+            else if (kind == 3) gu_tasks<true, true, true>(A, P, a0 * I, a1 * I, xn, xsum);
+            else if (kind == 2) gu_tasks<true, false, true>(A, P, a0 * I, a1 * I, xn, xsum);
+            else gu_tasks<false, true, true>(A, P, a0 * I, a1 * I, xn, xsum);
+        } else {
+            if (kind == 0) gu_tasks_any<false, false>(A, P, a0 * I, a1 * I, xn, xsum);
+            else if (kind == 3) gu_tasks_any<true, true>(A, P, a0 * I, a1 * I, xn, xsum);
+            else if (kind == 2) gu_tasks_any<true, false>(A, P, a0 * I, a1 * I, xn, xsum);
+            else gu_tasks_any<false, true>(A, P, a0 * I, a1 * I, xn, xsum);
+        }
+        a0 = a1;
+    }
+}
+
+/* One token (decode batch 1): every wave runs the top-8 rounds itself (the
+ * same rounds on the same logits, so the same result) and issues the loads of
+ * its GU_PF gate/up tasks as soon as the round naming the task's expert is
+ * done, so the rows' memory latency overlaps the remaining rounds and the
+ * plan.  With one token and 8 selectable logits the routed active experts
+ * are the slots in order, so task q = a*I + j is row j of slot a's expert;
+ * otherwise, or when the grid has fewer than 8*I / GU_PF waves, the preloaded
+ * rows are dropped, false is returned and the caller runs the plan's tasks
+ * through gu_all.  Wave 0 writes the ids and weights.  Routed gate / up types are the
+ * layer's (G6, U6). */
+template <bool G6, bool U6>
+__device__ __forceinline__ bool gu_one_token(const DecArgs &A, const DecLayer &L, DecPlan &P, const float lg[4],
+                                             float sg, unsigned long long *emask, const float *xn, const float *xsum,
+                                             int l, uint32_t &warm)
+{
+    const int I = A.I, nb = A.H / RQK, ntask = RTOPK * I;
+    const int lane = threadIdx.x & 63, c = lane & 7, lb = lane >> 3, wv = wave_id();
+    const int gw = blockIdx.x * DW + wv, nw = gridDim.x * DW;
+    if (threadIdx.x == 0) P.err = 0;
+    __syncthreads();
+    uint32_t key[4];
+    topk_keys(lg, A.E, key);
+    float v = -INFINITY;
+    int myid = -1, nsel = 0, ecur = 0, r = 0;
+    QChunk2 ch[GU_PF];
+#pragma unroll
+    for (int f = 0; f < GU_PF; f++) {
+        /* task f of this wave, clamped to the last task so that the load is
+         * unconditional (a wave without task f loads a row it does not use) */
+        const int q = min(gw + f * nw, ntask - 1);
+        for (; r <= q / I; r++) {
+            const int e = topk_round(key, r, v, myid);
+            nsel += e >= 0;
+            ecur = e >= 0 ? e : ecur;
+        }
+        ch[f] = load_gu_pair<G6, U6>(L.gate + (size_t)ecur * L.eb[0], L.up + (size_t)ecur * L.eb[1], q % I, nb, lb, c);
+    }
+    for (; r < RTOPK; r++) nsel += topk_round(key, r, v, myid) >= 0;
+    if (wv == 0) topk_finish(v, myid, nsel, P.ids[0], P.w[0], &P.err);
+    plan_from_ids(A, L, P, sg, emask);
+    PHASE_TS(1, 2);
+    warm = publish_and_warm(A, P, l);
+    if (P.nroute != RTOPK || GU_PF * nw < ntask) return false;      /* not every task preloaded */
+    {
+        const int ga = lb * RQK + q_run_a<G6>(c), gb = ga + q_run_b_off<G6>();
+        const int ua = lb * RQK + q_run_a<U6>(c), ub = ua + q_run_b_off<U6>();
+        float4 xga[4], xgb[4], xua[4], xub[4];
+        float sga = 0.0f, sgb = 0.0f, sua = 0.0f, sub = 0.0f;
+        if (lb < nb) {
+            load_x16(xn, ga, xga, A.xswz);
+            load_x16(xn, gb, xgb, A.xswz);
+            load_x16(xn, ua, xua, A.xswz);
+            load_x16(xn, ub, xub, A.xswz);
+            sga = xsum[ga >> 4]; sgb = xsum[gb >> 4]; sua = xsum[ua >> 4]; sub = xsum[ub >> 4];
+        }
+#pragma unroll
+        for (int f = 0; f < GU_PF; f++) {
+            const int q = gw + f * nw;
+            if (q >= ntask) break;
+            float pg = 0.0f, pu = 0.0f;
+            if (lb < nb) {
+                pg = q_chunk_dot_r<G6>(ch[f].g, c, xga, xgb, sga, sgb);
+                pu = q_chunk_dot_r<U6>(ch[f].u, c, xua, xub, sua, sub);
+            }
+            pg = group_sum<64>(pg);
+            pu = group_sum<64>(pu);
+            if (lane == 0) A.eh[(size_t)P.a[q / I].tk[0] * I + q % I] = silu_mul(pg, pu);
+        }
+    }
+    return true;
+}
+
 extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int l)
 {
     extern __shared__ __align__(16) float lds[];
@@ -506,7 +642,7 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int
     __shared__ float red[DW][RMAX_B];
     __shared__ float inv_rms[RMAX_B];
     __shared__ unsigned long long emask[256];
-    const int I = A.I, B = A.B, E = A.E;
+    const int B = A.B, E = A.E;
     float *xn = lds, *xsum = lds + B * A.H;
     PHASE_TS(1, 0);
     if (A.ffn_out) {
@@ -532,40 +668,39 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int
         build_plan(A, L, P, lg4, sg, emask);
     }
     PHASE_TS(1, 2);
-    if (blockIdx.x == 0) {
-        const int tid = threadIdx.x;
-        for (int i = tid; i < (int)(sizeof(DecPlan) / 16); i += DT) ((uint4 *)A.plan_g)[i] = ((const uint4 *)&P)[i];
-        if (!A.ffn_out && tid < B * RTOPK) {
-            const size_t o = ((size_t)(l - A.layer0) * B + (tid >> 3)) * RTOPK + (tid & 7);
-            if (A.ids_out) A.ids_out[o] = P.ids[tid >> 3][tid & 7];
-            if (A.w_out) A.w_out[o] = P.w[tid >> 3][tid & 7];
-        }
-        if (tid == 0 && P.err) atomicOr(A.err, 1);
-    }
-    /* Warm the last-level cache with this layer's down matrices (the plan's
-     * active experts): one dword per 128-byte line, spread over the grid, so
-     * that the down kernel's weight loads hit the cache.  The value is folded
-     * into a condition that is never true so the load is kept. */
+    const uint32_t warm = publish_and_warm(A, P, l);
+    gu_all<false>(A, P, xn, xsum);
+    PHASE_TS(1, 3);
+    if (warm == 0x9E3779B9u && threadIdx.x == 0) A.err[1] = (int)warm;   /* data-dependent sink, keeps the load */
+}
+
+/* The gate/up kernel for one token in the layer stack (decode batch 1): see
+ * gu_one_token. */
+extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu1_kernel(DecArgs A, int l)
+{
+    extern __shared__ __align__(16) float lds[];
+    __shared__ DecPlan P;
+    __shared__ unsigned long long emask[256];
+    const int E = A.E, lane = threadIdx.x & 63;
+    float *xn = lds, *xsum = lds + A.H;
+    PHASE_TS(1, 0);
+    const float *lg = A.logits_in ? A.logits_in : A.logits;
+    float lg4[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) lg4[i] = lane + 64 * i < E ? lg[lane + 64 * i] : -INFINITY;
+    const float sg = A.sgate_raw[0];
+    const DecLayer L = A.layers[l];
+    block_copy16(xn, A.xn_g, (A.H + A.H / 16) / 4);     /* published swizzled by the router kernel */
+    __syncthreads();
+    PHASE_TS(1, 1);
+    const int kind = (L.q6[0] ? 2 : 0) | (L.q6[1] ? 1 : 0);
     uint32_t warm = 0;
-    if (!A.ffn_out) {
-        const size_t lpe = (size_t)A.H * (A.I / RQK) * RQ6K_BYTES / 128;   /* lines per expert slot (Q6_K bound) */
-        const size_t g = (size_t)blockIdx.x * DT + threadIdx.x;
-        const int a = (int)(g / lpe);
-        if (a < P.nact) {
-            const size_t lines = (size_t)A.H * (A.I / RQK) * (P.a[a].dq6 ? RQ6K_BYTES : RQ4K_BYTES) / 128;
-            const size_t li = g % lpe;
-            if (li < lines) warm = *(const GAS uint32_t *)(P.a[a].d + li * 128);
-        }
-    }
-    for (int a0 = 0; a0 < P.nroute;) {
-        const int a1 = type_run_end(P, a0, P.nroute, true);
-        const int kind = (P.a[a0].gq6 ? 2 : 0) | (P.a[a0].uq6 ? 1 : 0);
-        if (kind == 0) gu_tasks_any<false, false>(A, P, a0 * I, a1 * I, xn, xsum);
-        else if (kind == 3) gu_tasks_any<true, true>(A, P, a0 * I, a1 * I, xn, xsum);
-        else if (kind == 2) gu_tasks_any<true, false>(A, P, a0 * I, a1 * I, xn, xsum);
-        else gu_tasks_any<false, true>(A, P, a0 * I, a1 * I, xn, xsum);
-        a0 = a1;
-    }
+    bool done;
+    if (kind == 0) done = gu_one_token<false, false>(A, L, P, lg4, sg, emask, xn, xsum, l, warm);
+    else if (kind == 3) done = gu_one_token<true, true>(A, L, P, lg4, sg, emask, xn, xsum, l, warm);
+    else if (kind == 2) done = gu_one_token<true, false>(A, L, P, lg4, sg, emask, xn, xsum, l, warm);
+    else done = gu_one_token<false, true>(A, L, P, lg4, sg, emask, xn, xsum, l, warm);
+    if (!done) gu_all<true>(A, P, xn, xsum);
     PHASE_TS(1, 3);
     if (warm == 0x9E3779B9u && threadIdx.x == 0) A.err[1] = (int)warm;   /* data-dependent sink, keeps the load */
 }
@@ -700,7 +835,8 @@ static int launch_layer(const DecArgs &A, int l, bool with_router)
         hipLaunchKernelGGL(dec_router_kernel, dim3((ntask + DW - 1) / DW), dim3(DT), lds, R.stream, A, l);
         if (rt_check(hipGetLastError(), "router launch")) return ROASTER_EDEVICE;
     }
-    hipLaunchKernelGGL(dec_gu_kernel, dim3(2 * R.n_cu), dim3(DT), lds, R.stream, A, l);
+    if (A.B == 1 && !A.ffn_out) hipLaunchKernelGGL(dec_gu1_kernel, dim3(2 * R.n_cu), dim3(DT), lds, R.stream, A, l);
+    else hipLaunchKernelGGL(dec_gu_kernel, dim3(2 * R.n_cu), dim3(DT), lds, R.stream, A, l);
     if (rt_check(hipGetLastError(), "gate/up launch")) return ROASTER_EDEVICE;
     const int nslot = A.ffn_out ? A.ffn_n : 9, dr = A.B > 1 ? D_ROWS_B : D_ROWS;
     const size_t dlds = (size_t)nslot * A.I * 4 + (size_t)nslot * (A.I / 16) * 4;

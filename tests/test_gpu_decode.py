@@ -102,14 +102,26 @@ def test_decode_given_logits_ties_and_batch(cfg2):
 
 
 def test_decode_reports_routing_failure(cfg2):
+    """Only 3 routable experts: the error is reported, and the one-token
+    kernel's fallback (the plan's 3 experts + shared) gives the same output,
+    bit for bit, as the same token inside a batch of 2."""
     x = R.synth_normal(1, 3, 2048)[None, :]
     lg = np.full((1, 256), -np.inf, np.float32)
     lg[0, :3] = 1.0
-    dx, dy, dl = Dev(x), Dev(nbytes=2048 * 4), Dev(lg)
+    dx, dy, dl = Dev(x), Dev(nbytes=2048 * 4, shape=(1, 2048)), Dev(lg)
     io = R.RoasterDecodeIO(dl.p, None, None, None)
     R.check(R.lib().roaster_moe_decode(cfg2.t, 0, dx.p, 1, dy.p, C.byref(io)))
     assert R.lib().roaster_sync() == R.EROUTE
     assert R.lib().roaster_sync() == 0        # the error is reported once
+    x2 = np.concatenate([x, R.synth_normal(2, 3, 2048)[None, :]])
+    lg2 = np.concatenate([lg, R.synth_normal(3, 3, 256)[None, :]])
+    dx2, dy2, dl2 = Dev(x2), Dev(nbytes=2 * 2048 * 4, shape=(2, 2048)), Dev(lg2)
+    io2 = R.RoasterDecodeIO(dl2.p, None, None, None)
+    R.check(R.lib().roaster_moe_decode(cfg2.t, 0, dx2.p, 2, dy2.p, C.byref(io2)))
+    assert R.lib().roaster_sync() == R.EROUTE
+    y1, y2 = dy.get(), dy2.get()
+    assert np.isfinite(y1).all()
+    np.testing.assert_array_equal(y1[0], y2[0])
 
 
 def oracle_stack(table, h0, n_layers, eps=1e-6, norm_w=None):
