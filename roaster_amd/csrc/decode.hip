@@ -563,45 +563,39 @@ __device__ __forceinline__ void gu_all(const DecArgs &A, const DecPlan &P, const
     }
 }
 
-/* One token (decode batch 1): every wave runs the top-8 rounds itself (the
- * same rounds on the same logits, so the same result) and issues the loads of
- * its GU_PF gate/up tasks as soon as the round naming the task's expert is
- * done, so the rows' memory latency overlaps the remaining rounds and the
- * plan.  With one token and 8 selectable logits the routed active experts
- * are the slots in order, so task q = a*I + j is row j of slot a's expert;
- * otherwise, or when the grid has fewer than 8*I / GU_PF waves, the preloaded
- * rows are dropped, false is returned and the caller runs the plan's tasks
- * through gu_all.  Wave 0 writes the ids and weights.  Routed gate / up types are the
- * layer's (G6, U6). */
+/* One token (decode batch 1): wave 0 ranks the top-8 (topk8_fast, a few
+ * hundred cycles where the eight reduction rounds take thousands), then every
+ * wave issues the loads of its GU_PF gate/up tasks before the plan is built,
+ * so the rows' memory latency overlaps the plan, its publication and the
+ * warming reads.  With one token and 8 selectable logits the routed active
+ * experts are the slots in order, so task q = a*I + j is row j of slot a's
+ * expert; otherwise, or when the grid has fewer than 8*I / GU_PF waves, the
+ * preloaded rows are dropped, false is returned and the caller runs the
+ * plan's tasks through gu_all.  Routed gate / up types are the layer's
+ * (G6, U6). */
 template <bool G6, bool U6>
 __device__ __forceinline__ bool gu_one_token(const DecArgs &A, const DecLayer &L, DecPlan &P, const float lg[4],
                                              float sg, unsigned long long *emask, const float *xn, const float *xsum,
-                                             int l, uint32_t &warm)
+                                             int l, uint32_t &warm, TopkScratch *ts)
 {
     const int I = A.I, nb = A.H / RQK, ntask = RTOPK * I;
     const int lane = threadIdx.x & 63, c = lane & 7, lb = lane >> 3, wv = wave_id();
     const int gw = blockIdx.x * DW + wv, nw = gridDim.x * DW;
-    if (threadIdx.x == 0) P.err = 0;
+    if (wv == 0) {
+        if (lane == 0) P.err = 0;
+        topk8_fast(lg, A.E, P.ids[0], P.w[0], &P.err, ts);
+    }
     __syncthreads();
-    uint32_t key[4];
-    topk_keys(lg, A.E, key);
-    float v = -INFINITY;
-    int myid = -1, nsel = 0, ecur = 0, r = 0;
     QChunk2 ch[GU_PF];
 #pragma unroll
     for (int f = 0; f < GU_PF; f++) {
         /* task f of this wave, clamped to the last task so that the load is
-         * unconditional (a wave without task f loads a row it does not use) */
+         * unconditional (a wave without task f loads a row it does not use);
+         * an unselected slot (id -1) loads expert 0's row */
         const int q = min(gw + f * nw, ntask - 1);
-        for (; r <= q / I; r++) {
-            const int e = topk_round(key, r, v, myid);
-            nsel += e >= 0;
-            ecur = e >= 0 ? e : ecur;
-        }
-        ch[f] = load_gu_pair<G6, U6>(L.gate + (size_t)ecur * L.eb[0], L.up + (size_t)ecur * L.eb[1], q % I, nb, lb, c);
+        const int e = max(P.ids[0][q / I], 0);
+        ch[f] = load_gu_pair<G6, U6>(L.gate + (size_t)e * L.eb[0], L.up + (size_t)e * L.eb[1], q % I, nb, lb, c);
     }
-    for (; r < RTOPK; r++) nsel += topk_round(key, r, v, myid) >= 0;
-    if (wv == 0) topk_finish(v, myid, nsel, P.ids[0], P.w[0], &P.err);
     plan_from_ids(A, L, P, sg, emask);
     PHASE_TS(1, 2);
     warm = publish_and_warm(A, P, l);
@@ -681,6 +675,7 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu1_kernel(DecArgs A, in
     extern __shared__ __align__(16) float lds[];
     __shared__ DecPlan P;
     __shared__ unsigned long long emask[256];
+    __shared__ TopkScratch ts;
     const int E = A.E, lane = threadIdx.x & 63;
     float *xn = lds, *xsum = lds + A.H;
     PHASE_TS(1, 0);
@@ -696,10 +691,10 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu1_kernel(DecArgs A, in
     const int kind = (L.q6[0] ? 2 : 0) | (L.q6[1] ? 1 : 0);
     uint32_t warm = 0;
     bool done;
-    if (kind == 0) done = gu_one_token<false, false>(A, L, P, lg4, sg, emask, xn, xsum, l, warm);
-    else if (kind == 3) done = gu_one_token<true, true>(A, L, P, lg4, sg, emask, xn, xsum, l, warm);
-    else if (kind == 2) done = gu_one_token<true, false>(A, L, P, lg4, sg, emask, xn, xsum, l, warm);
-    else done = gu_one_token<false, true>(A, L, P, lg4, sg, emask, xn, xsum, l, warm);
+    if (kind == 0) done = gu_one_token<false, false>(A, L, P, lg4, sg, emask, xn, xsum, l, warm, &ts);
+    else if (kind == 3) done = gu_one_token<true, true>(A, L, P, lg4, sg, emask, xn, xsum, l, warm, &ts);
+    else if (kind == 2) done = gu_one_token<true, false>(A, L, P, lg4, sg, emask, xn, xsum, l, warm, &ts);
+    else done = gu_one_token<false, true>(A, L, P, lg4, sg, emask, xn, xsum, l, warm, &ts);
     if (!done) gu_all<true>(A, P, xn, xsum);
     PHASE_TS(1, 3);
     if (warm == 0x9E3779B9u && threadIdx.x == 0) A.err[1] = (int)warm;   /* data-dependent sink, keeps the load */

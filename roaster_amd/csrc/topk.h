@@ -123,4 +123,81 @@ static __device__ void topk8_wave(const float v4in[4], int E, int *ids, float *w
     topk_finish(v, myid, nsel, ids, w, bad);
 }
 
+/* LDS scratch of topk8_fast, per wave. */
+struct TopkScratch {
+    unsigned long long cand[64];    /* candidates' composite keys */
+    unsigned long long slot[RTOPK]; /* slot k's composite key */
+};
+
+/* Composite key: the logit key in the high word, 255 - expert in the low
+ * word, so that a larger composite is "larger logit, then lower index". */
+__device__ __forceinline__ unsigned long long topk_ck(uint32_t key, int e)
+{
+    return ((unsigned long long)key << 32) | (uint32_t)(255 - e);
+}
+
+/* Wave-level top-8 of one token (model.c:869-897) by ranking a candidate
+ * set, the same selection as topk8_wave.  The 256 keys fall into 8 groups of
+ * 32 (the 4 keys of each 8-lane group); T = the smallest of the 8 group
+ * maxima is at most the 8th largest key, so every selected key is >= T.  The
+ * candidates (key >= T, key != 0) are compacted into LDS and each candidate's
+ * rank is the number of candidates with a larger composite key; rank r < 8
+ * fills slot r.  The rounds of topk8_wave run instead when more than 64 keys
+ * qualify (many ties at the threshold, or a group without a selectable
+ * logit).  All 64 lanes must be active; S is this wave's scratch. */
+static __device__ void topk8_fast(const float v4in[4], int E, int *ids, float *w, int *bad, TopkScratch *S)
+{
+    const int lane = threadIdx.x & 63;
+    uint32_t key[4];
+    topk_keys(v4in, E, key);
+    uint32_t g = max(max(key[0], key[1]), max(key[2], key[3]));
+    g = max(g, (uint32_t)dpp_i<DPP_XOR1>((int)g));
+    g = max(g, (uint32_t)dpp_i<DPP_XOR2>((int)g));
+    g = max(g, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)g));          /* group maximum in each 8-lane group */
+    g = min(g, (uint32_t)dpp_i<DPP_MIRROR>((int)g));              /* smaller of the row's two groups */
+    const uint32_t T = min(min((uint32_t)__builtin_amdgcn_readlane((int)g, 0), (uint32_t)__builtin_amdgcn_readlane((int)g, 16)),
+                           min((uint32_t)__builtin_amdgcn_readlane((int)g, 32), (uint32_t)__builtin_amdgcn_readlane((int)g, 48)));
+    bool c[4];
+    uint64_t b[4];
+    int n = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        c[i] = key[i] >= T && key[i] != 0u;
+        b[i] = __builtin_amdgcn_ballot_w64(c[i]);
+        n += __builtin_popcountll(b[i]);
+    }
+    if (n > 64) {                                   /* wave-uniform */
+        topk8_wave(v4in, E, ids, w, bad);
+        return;
+    }
+    int base = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b[i] >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)b[i], 0u));
+        if (c[i]) S->cand[pos] = topk_ck(key[i], lane + 64 * i);
+        base += __builtin_popcountll(b[i]);
+    }
+    if (lane < RTOPK) S->slot[lane] = 0ull;
+    __builtin_amdgcn_s_waitcnt(0xC07F);             /* lgkmcnt(0): the wave's LDS writes are done */
+    __builtin_amdgcn_wave_barrier();
+    const unsigned long long my = S->cand[lane];          /* lanes >= n read a stale entry and write nothing */
+    int rank = 0;
+    for (int j0 = 0; j0 < n; j0 += 16) {            /* 16 reads in flight, then the compares */
+        unsigned long long cj[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) cj[u] = S->cand[j0 + u];
+#pragma unroll
+        for (int u = 0; u < 16; u++) rank += (j0 + u < n && cj[u] > my) ? 1 : 0;
+    }
+    if (lane < n && rank < RTOPK) S->slot[rank] = my;
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+    const unsigned long long sk = S->slot[lane & (RTOPK - 1)];
+    const bool sel = lane < RTOPK && sk != 0ull;
+    const float v = sel ? key_logit((uint32_t)(sk >> 32)) : -INFINITY;
+    const int myid = sel ? 255 - (int)(uint32_t)sk : -1;
+    topk_finish(v, myid, min(n, RTOPK), ids, w, bad);
+}
+
 #endif
