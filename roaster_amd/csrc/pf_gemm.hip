@@ -482,29 +482,32 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
         else v4_mfma_mixed<MS, QG, QU>(acc, Xs, rg[buf], ru[buf], up, h);
         __builtin_amdgcn_sched_barrier(0);
     };
-    w_load(0, 0);
     x_load(0);
+    w_load(0, 0);
     x_store(Xb);
     __syncthreads();
     /* steady state: steps kb (raw buffer 0, activation buffer 0) and kb + 1
-     * (buffers 1), each issuing the next step's loads first */
+     * (buffers 1), each issuing the next step's loads first, activations
+     * before weights: a wave's loads complete in order, so the activation
+     * store (and with it the barrier) waits for the activation loads only,
+     * not for the next step's weights from HBM */
     int kb = 0;
     for (; kb + 2 < nkb; kb += 2) {
-        w_load(1, kb + 1);
         x_load(kb + 1);
+        w_load(1, kb + 1);
         step(0, Xb);
         x_store(Xb + V3_XBUF);
         __syncthreads();
-        w_load(0, kb + 2);
         x_load(kb + 2);
+        w_load(0, kb + 2);
         step(1, Xb + V3_XBUF);
         x_store(Xb);
         __syncthreads();
     }
     /* last one or two steps */
     if (kb + 1 < nkb) {
-        w_load(1, kb + 1);
         x_load(kb + 1);
+        w_load(1, kb + 1);
         step(0, Xb);
         x_store(Xb + V3_XBUF);
         __syncthreads();
