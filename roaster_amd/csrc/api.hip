@@ -345,6 +345,7 @@ static void fill_table_args(DecArgs &A, const RoasterTable *t)
 {
     memset(&A, 0, sizeof(A));
     A.layers = t->layers_d;
+    A.layers_h = t->layers_h.data();
     A.E = t->d.n_experts;
     A.H = (int)t->d.hidden;
     A.I = (int)t->d.inter;

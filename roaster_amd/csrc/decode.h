@@ -65,6 +65,8 @@ struct DecArgs {
     float *w_out;
     DecPlan *plan_g;            /* plan written by the gate/up kernel, read by the down kernel */
     int *err;
+    const DecLayer *layers_h;   /* host copy of layers (read by the launch code only) or NULL */
+    int d1;                     /* per launch: one-token down path, 0 off, 1 Q4_K, 2 Q6_K down matrices */
     /* kernel_ffn_fused mode */
     const DecActive *ffn_ex;    /* [n] device */
     int ffn_n;

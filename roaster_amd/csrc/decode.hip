@@ -751,6 +751,88 @@ __device__ void down_slots(const DecArgs &A, const uint8_t *const *sd, int k0, i
     }
 }
 
+/* Down rows and combine for one token when the 9 down matrices share one
+ * type D6 (A.d1, set per launch): each wave reads its tasks' slot pointers
+ * straight from the published plan and issues the weight-row loads as soon
+ * as they arrive, before the SiLU*up rows are stored to LDS, so the rows'
+ * memory latency overlaps the copy, the barriers and the run sums.  Tasks as
+ * in down_slots (q = k * ngroups + g, wave w takes q = w, w + 4, ...; the
+ * host checks that D_PF tasks per wave cover them); loads are unconditional
+ * (clamped task, row and block; an unselected slot reads the shared slot's
+ * matrix) and the copy's stores wait for the copy's loads only. */
+template <bool D6>
+__device__ __forceinline__ void down_one_token(const DecArgs &A, int dr, float *ehl, float *ehs, float *dbuf, float *sw)
+{
+    const int H = A.H, I = A.I, nb = I / RQK, tid = threadIdx.x, lane = tid & 63, wv = wave_id();
+    const int lpr = lanes_per_row(nb), rpw = 64 / lpr, ngroups = (dr + rpw - 1) / rpw, ntask = 9 * ngroups;
+    const int rw = lane / lpr, lr = lane % lpr, c = lr & 7, lb = lr >> 3;
+    const int r0 = blockIdx.x * dr;
+    const size_t dbs = D6 ? RQ6K_BYTES : RQ4K_BYTES;
+    const int ca = lb * RQK + q_run_a<D6>(c), cb = ca + q_run_b_off<D6>();
+    const DecPlan *PG = A.plan_g;
+    const uint8_t *mp[D_PF];
+#pragma unroll
+    for (int f = 0; f < D_PF; f++) mp[f] = PG->dsl[0][min(wv + f * DW, ntask - 1) / ngroups];
+    const uint8_t *fb = PG->dsl[0][8];
+    const float wk = PG->w[0][min(tid, 8)];
+    /* the SiLU*up rows: 9 x I / 4 16-byte units, 5 per thread (I <= 568), in
+     * named registers (an array here is not kept in registers across the
+     * scheduling fences) */
+    const int n16 = 9 * I / 4;
+    const uint4 *eh4 = (const uint4 *)A.eh;
+    const uint4 e0 = eh4[min(tid, n16 - 1)], e1 = eh4[min(tid + DT, n16 - 1)], e2 = eh4[min(tid + 2 * DT, n16 - 1)];
+    const uint4 e3 = eh4[min(tid + 3 * DT, n16 - 1)], e4 = eh4[min(tid + 4 * DT, n16 - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    QChunk ch[D_PF];
+#pragma unroll
+    for (int f = 0; f < D_PF; f++) {
+        const int q = min(wv + f * DW, ntask - 1), g = q % ngroups;
+        const int row = min(r0 + g * rpw + rw, H - 1);
+        const uint8_t *m = mp[f] ? mp[f] : fb;
+        ch[f] = q_load<D6>(m + ((size_t)row * nb + min(lb, nb - 1)) * dbs, c);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 *el4 = (uint4 *)ehl;
+    el4[min(tid, n16 - 1)] = e0;
+    el4[min(tid + DT, n16 - 1)] = e1;
+    el4[min(tid + 2 * DT, n16 - 1)] = e2;
+    el4[min(tid + 3 * DT, n16 - 1)] = e3;
+    el4[min(tid + 4 * DT, n16 - 1)] = e4;
+    sw[min(tid, 8)] = wk;                                   /* threads past 8 store slot 8's weight again */
+    for (int i = tid; i < 9 * D_MAXR; i += DT) dbuf[i] = 0.0f;
+    __syncthreads();
+    for (int r = tid; r < 9 * (I / 16); r += DT) ehs[r] = sum16(ehl + r * 16);
+    __syncthreads();
+    PHASE_TS(2, 1);
+#pragma unroll
+    for (int f = 0; f < D_PF; f++) {
+        const int q = wv + f * DW;
+        if (q >= ntask) break;
+        const int k = q / ngroups, g = q % ngroups;
+        const int rl = g * rpw + rw, row = r0 + rl;
+        const bool live = rl < dr && row < H && lb < nb && mp[f] != NULL;
+        float part = 0.0f;
+        if (live) {
+            const float *x = ehl + k * I, *xs = ehs + k * (I / 16);
+            part = q_chunk_dot<D6>(ch[f], c, x + ca, x + cb, xs[ca >> 4], xs[cb >> 4]);
+        }
+        part = group_sum_w(part, lpr);
+        if (live && lr == 0) dbuf[k * D_MAXR + rl] = part;
+    }
+    __syncthreads();
+    PHASE_TS(2, 2);
+    for (int rl = tid; rl < dr; rl += DT) {
+        const int row = r0 + rl;
+        if (row >= H) continue;
+        float y = 0.0f;
+        for (int k = 0; k < RTOPK; k++) y = fmaf(sw[k], dbuf[k * D_MAXR + rl], y);
+        y = fmaf(sw[8], dbuf[8 * D_MAXR + rl], y);
+        if (A.y) A.y[row] = y;
+        else A.h[row] = A.h[row] + y;
+    }
+    PHASE_TS(2, 3);
+}
+
 /* One workgroup per (token t, block of dr output rows): the token's nine
  * slots (8 routed experts from the plan's ids, then the shared expert), or
  * the n experts of kernel_ffn_fused for token 0.  The slots' SiLU*up vectors
@@ -769,6 +851,11 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_down_kernel(DecArgs A, i
     const int nslot = ffn ? A.ffn_n : 9;
     PHASE_TS(2, 0);
     float *ehl = lds, *ehs = lds + nslot * I;
+    if (A.d1) {
+        if (A.d1 == 2) down_one_token<true>(A, dr, ehl, ehs, dbuf, sw);
+        else down_one_token<false>(A, dr, ehl, ehs, dbuf, sw);
+        return;
+    }
     /* slot table (published with the plan): its loads are unconditional,
      * issued first and consumed only after the SiLU*up copy, so both share
      * one memory round trip */
@@ -821,9 +908,18 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_down_kernel(DecArgs A, i
 /* ---- host side ------------------------------------------------------------ */
 static size_t norm_lds(int B, int H) { return (size_t)B * H * 4 + (size_t)B * (H / 16) * 4; }
 
-static int launch_layer(const DecArgs &A, int l, bool with_router)
+static int launch_layer(const DecArgs &A0, int l, bool with_router)
 {
     RtState &R = rt();
+    DecArgs A = A0;
+    /* one-token down path (down_one_token): one down type for all 9 slots and
+     * every task within D_PF per wave */
+    const DecLayer *Lh = A.layers_h ? A.layers_h + l : nullptr;
+    const int rpw1 = 64 / lanes_per_row(A.I / RQK);
+    A.d1 = 0;
+    if (A.B == 1 && !A.ffn_out && Lh && Lh->q6[2] == Lh->sq6[2] && 9 * ((D_ROWS + rpw1 - 1) / rpw1) <= DW * D_PF &&
+        9 * A.I / 4 <= 5 * DT)
+        A.d1 = Lh->q6[2] ? 2 : 1;
     const size_t lds = norm_lds(A.B, A.H);
     if (with_router) {
         const int ntask = (A.logits_in ? 0 : A.E) + 1 + A.I;
