@@ -408,6 +408,49 @@ __device__ __forceinline__ void plan_from_ids(const DecArgs &A, const DecLayer &
     __syncthreads();
 }
 
+/* plan_from_ids for one token whose top-8 ids in P are visible to the whole
+ * workgroup: the selected slots (a prefix of the 8: topk fills slots in
+ * order) are the routed active experts in slot order, so lane k of wave 0
+ * writes active expert k directly; then the shared expert, and the slot table
+ * as in plan_from_ids.  Gives the same plan as plan_from_ids with B = 1. */
+__device__ __forceinline__ void plan_one_token(const DecArgs &A, const DecLayer &L, DecPlan &P, float sg)
+{
+    const int tid = threadIdx.x, wv = wave_id(), lane = tid & 63;
+    if (wv == 0) {
+        const int e = lane < RTOPK ? P.ids[0][lane] : -1;
+        const int nroute = __popcll(__ballot(e >= 0));
+        if (e >= 0) {
+            DecActive &X = P.a[lane];
+            X.g = L.gate + (size_t)e * L.eb[0];
+            X.u = L.up + (size_t)e * L.eb[1];
+            X.d = L.down + (size_t)e * L.eb[2];
+            X.gq6 = L.q6[0]; X.uq6 = L.q6[1]; X.dq6 = L.q6[2];
+            X.ntok = 1;
+            X.tk[0] = lane;                                 /* pair (token 0, slot lane) */
+        }
+        if (lane == 0) {
+            P.w[0][8] = 1.0f / (1.0f + expf(-sg));
+            DecActive &X = P.a[nroute];
+            X.g = L.sgate; X.u = L.sup; X.d = L.sdown;
+            X.gq6 = L.sq6[0]; X.uq6 = L.sq6[1]; X.dq6 = L.sq6[2];
+            X.ntok = 1;
+            X.tk[0] = 8;
+            P.nroute = nroute;
+            P.nact = nroute + 1;
+        }
+    } else if (tid < 64 + 9) {                              /* down slot table */
+        const int k = tid - 64;
+        if (k < RTOPK) {
+            const int e = P.ids[0][k];
+            P.dsl[0][k] = e >= 0 ? L.down + (size_t)e * L.eb[2] : NULL;
+        } else {
+            P.dsl[0][k] = L.sdown;
+        }
+        P.dq6k[k] = k < RTOPK ? L.q6[2] : L.sq6[2];
+    }
+    __syncthreads();
+}
+
 /* Plan of B tokens: wave w computes the top-8 of tokens w, w + 4, ... */
 __device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, const float (*lg4)[4], float sg,
                            unsigned long long *emask)
@@ -575,8 +618,8 @@ __device__ __forceinline__ void gu_all(const DecArgs &A, const DecPlan &P, const
  * (G6, U6). */
 template <bool G6, bool U6>
 __device__ __forceinline__ bool gu_one_token(const DecArgs &A, const DecLayer &L, DecPlan &P, const float lg[4],
-                                             float sg, unsigned long long *emask, const float *xn, const float *xsum,
-                                             int l, uint32_t &warm, TopkScratch *ts)
+                                             float sg, const float *xn, const float *xsum, int l, uint32_t &warm,
+                                             TopkScratch *ts)
 {
     const int I = A.I, nb = A.H / RQK, ntask = RTOPK * I;
     const int lane = threadIdx.x & 63, c = lane & 7, lb = lane >> 3, wv = wave_id();
@@ -596,7 +639,7 @@ __device__ __forceinline__ bool gu_one_token(const DecArgs &A, const DecLayer &L
         const int e = max(P.ids[0][q / I], 0);
         ch[f] = load_gu_pair<G6, U6>(L.gate + (size_t)e * L.eb[0], L.up + (size_t)e * L.eb[1], q % I, nb, lb, c);
     }
-    plan_from_ids(A, L, P, sg, emask);
+    plan_one_token(A, L, P, sg);
     PHASE_TS(1, 2);
     warm = publish_and_warm(A, P, l);
     if (P.nroute != RTOPK || GU_PF * nw < ntask) return false;      /* not every task preloaded */
@@ -674,7 +717,6 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu1_kernel(DecArgs A, in
 {
     extern __shared__ __align__(16) float lds[];
     __shared__ DecPlan P;
-    __shared__ unsigned long long emask[256];
     __shared__ TopkScratch ts;
     const int E = A.E, lane = threadIdx.x & 63;
     float *xn = lds, *xsum = lds + A.H;
@@ -691,10 +733,10 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu1_kernel(DecArgs A, in
     const int kind = (L.q6[0] ? 2 : 0) | (L.q6[1] ? 1 : 0);
     uint32_t warm = 0;
     bool done;
-    if (kind == 0) done = gu_one_token<false, false>(A, L, P, lg4, sg, emask, xn, xsum, l, warm, &ts);
-    else if (kind == 3) done = gu_one_token<true, true>(A, L, P, lg4, sg, emask, xn, xsum, l, warm, &ts);
-    else if (kind == 2) done = gu_one_token<true, false>(A, L, P, lg4, sg, emask, xn, xsum, l, warm, &ts);
-    else done = gu_one_token<false, true>(A, L, P, lg4, sg, emask, xn, xsum, l, warm, &ts);
+    if (kind == 0) done = gu_one_token<false, false>(A, L, P, lg4, sg, xn, xsum, l, warm, &ts);
+    else if (kind == 3) done = gu_one_token<true, true>(A, L, P, lg4, sg, xn, xsum, l, warm, &ts);
+    else if (kind == 2) done = gu_one_token<true, false>(A, L, P, lg4, sg, xn, xsum, l, warm, &ts);
+    else done = gu_one_token<false, true>(A, L, P, lg4, sg, xn, xsum, l, warm, &ts);
     if (!done) gu_all<true>(A, P, xn, xsum);
     PHASE_TS(1, 3);
     if (warm == 0x9E3779B9u && threadIdx.x == 0) A.err[1] = (int)warm;   /* data-dependent sink, keeps the load */
