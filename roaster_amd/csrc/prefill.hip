@@ -175,6 +175,7 @@ struct PfTokArgs {
 extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
 {
     __shared__ int bad[4];
+    __shared__ TopkScratch ts[4];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + wv;
     if (t >= A.T) return;
@@ -244,7 +245,7 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
     }
     if (lane == 0) bad[wv] = 0;
     __builtin_amdgcn_wave_barrier();
-    topk8_wave(v4, A.E, A.ids + (size_t)t * 8, A.w + (size_t)t * 8, &bad[wv]);
+    topk8_fast(v4, A.E, A.ids + (size_t)t * 8, A.w + (size_t)t * 8, &bad[wv], &ts[wv]);
     if (lane < 8) {
         if (A.ids_out) A.ids_out[(size_t)t * 8 + lane] = A.ids[(size_t)t * 8 + lane];
         if (A.w_out) A.w_out[(size_t)t * 8 + lane] = A.w[(size_t)t * 8 + lane];
