@@ -451,13 +451,15 @@ __device__ __forceinline__ void plan_one_token(const DecArgs &A, const DecLayer 
     __syncthreads();
 }
 
-/* Plan of B tokens: wave w computes the top-8 of tokens w, w + 4, ... */
+/* Plan of B tokens: wave w computes the top-8 of tokens w, w + 4, ... (ts:
+ * one scratch per wave) */
 __device__ void build_plan(const DecArgs &A, const DecLayer &L, DecPlan &P, const float (*lg4)[4], float sg,
-                           unsigned long long *emask)
+                           unsigned long long *emask, TopkScratch *ts)
 {
     if (threadIdx.x == 0) P.err = 0;
     __syncthreads();
-    for (int t = wave_id(), r = 0; t < A.B; t += DW, r++) topk8_wave(lg4[r], A.E, P.ids[t], P.w[t], &P.err);
+    for (int t = wave_id(), r = 0; t < A.B; t += DW, r++)
+        topk8_fast(lg4[r], A.E, P.ids[t], P.w[t], &P.err, &ts[wave_id()]);
     plan_from_ids(A, L, P, sg, emask);
 }
 
@@ -679,6 +681,7 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int
     __shared__ float red[DW][RMAX_B];
     __shared__ float inv_rms[RMAX_B];
     __shared__ unsigned long long emask[256];
+    __shared__ TopkScratch ts[DW];
     const int B = A.B, E = A.E;
     float *xn = lds, *xsum = lds + B * A.H;
     PHASE_TS(1, 0);
@@ -702,7 +705,7 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu_kernel(DecArgs A, int
         block_copy16(xn, A.xn_g, B * (A.H + A.H / 16) / 4);     /* published swizzled by the router kernel */
         __syncthreads();
         PHASE_TS(1, 1);
-        build_plan(A, L, P, lg4, sg, emask);
+        build_plan(A, L, P, lg4, sg, emask, ts);
     }
     PHASE_TS(1, 2);
     const uint32_t warm = publish_and_warm(A, P, l);
