@@ -815,6 +815,8 @@ __device__ __forceinline__ void down_one_token(const DecArgs &A, int dr, float *
     const size_t dbs = D6 ? RQ6K_BYTES : RQ4K_BYTES;
     const int ca = lb * RQK + q_run_a<D6>(c), cb = ca + q_run_b_off<D6>();
     const DecPlan *PG = A.plan_g;
+    /* the residual of this thread's output row (stack mode), read first */
+    const float hv = A.y ? 0.0f : A.h[min(r0 + min(tid, dr - 1), H - 1)];
     const uint8_t *mp[D_PF];
 #pragma unroll
     for (int f = 0; f < D_PF; f++) mp[f] = PG->dsl[0][min(wv + f * DW, ntask - 1) / ngroups];
@@ -873,7 +875,7 @@ __device__ __forceinline__ void down_one_token(const DecArgs &A, int dr, float *
         for (int k = 0; k < RTOPK; k++) y = fmaf(sw[k], dbuf[k * D_MAXR + rl], y);
         y = fmaf(sw[8], dbuf[8 * D_MAXR + rl], y);
         if (A.y) A.y[row] = y;
-        else A.h[row] = A.h[row] + y;
+        else A.h[row] = hv + y;                             /* rl == tid here */
     }
     PHASE_TS(2, 3);
 }
