@@ -730,8 +730,17 @@ extern "C" __global__ void __launch_bounds__(DT, 2) dec_gu1_kernel(DecArgs A, in
     for (int i = 0; i < 4; i++) lg4[i] = lane + 64 * i < E ? lg[lane + 64 * i] : -INFINITY;
     const float sg = A.sgate_raw[0];
     const DecLayer L = A.layers[l];
-    block_copy16(xn, A.xn_g, (A.H + A.H / 16) / 4);     /* published swizzled by the router kernel */
-    __syncthreads();
+    /* waves 1..3 stage the normalised input (published swizzled by the router
+     * kernel: (H + H/16) / 4 <= 3 * 192 16-byte units) while wave 0 ranks the
+     * top-8; the barrier after the ranking covers both */
+    if (wave_id() > 0) {
+        const int n16 = (A.H + A.H / 16) / 4, t3 = threadIdx.x - 64;
+        uint4 v[3];
+#pragma unroll
+        for (int k = 0; k < 3; k++) v[k] = ((const uint4 *)A.xn_g)[min(t3 + k * (DT - 64), n16 - 1)];
+#pragma unroll
+        for (int k = 0; k < 3; k++) ((uint4 *)xn)[min(t3 + k * (DT - 64), n16 - 1)] = v[k];
+    }
     PHASE_TS(1, 1);
     const int kind = (L.q6[0] ? 2 : 0) | (L.q6[1] ? 1 : 0);
     uint32_t warm = 0;
