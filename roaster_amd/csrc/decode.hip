@@ -147,20 +147,38 @@ __device__ __forceinline__ void load_x16(const float *xn, int off, float4 (&x)[4
  * RMSNorm follows kernels.c:584-605: x * (1/sqrt(mean(x^2) + eps)) * w.  All
  * LDS traffic is in 16-byte units (4-byte LDS accesses issue at an eighth of
  * the rate); H <= 2048 = 2 units per thread per token. */
+/* Norm weights of this thread's storage units (logical units xsw(u)), or
+ * NULL (then wq holds ones). */
+__device__ __forceinline__ const float *norm_weights(const DecArgs &A, int l, float4 (&wq)[2])
+{
+    const int HU = A.H / 4;
+    const float *nw = A.do_norm && A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * A.H : NULL;
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+        wq[k] = nw ? ((const float4 *)nw)[xpos(min((int)threadIdx.x + k * DT, HU - 1), A.xswz)]
+                   : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    return nw;
+}
+
+__device__ void block_norm_tail(const DecArgs &A, float *xn, float *xsum, float (*red)[RMAX_B], float *inv_rms,
+                                const float4 (&wq)[2], const float *nw);
+
 __device__ void block_norm(const DecArgs &A, int l, float *xn, float *xsum, float (*red)[RMAX_B], float *inv_rms)
+{
+    float4 wq[2];
+    const float *nw = norm_weights(A, l, wq);          /* loaded with h */
+    block_copy16_sw(xn, A.h, A.B * (A.H / 4), A.xswz ? A.B * (A.H / 4) : 0);
+    block_norm_tail(A, xn, xsum, red, inv_rms, wq, nw);
+}
+
+/* block_norm after h is stored in LDS (not yet synchronised) */
+__device__ __forceinline__ void block_norm_tail(const DecArgs &A, float *xn, float *xsum, float (*red)[RMAX_B],
+                                                float *inv_rms, const float4 (&wq)[2], const float *nw)
 {
     const int H = A.H, B = A.B, HU = H / 4;     /* 16-byte units per token */
     const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
     const bool swz = A.xswz;
     float4 *x4 = (float4 *)xn;
-    /* norm weights of this thread's storage units (logical units xsw(u)),
-     * loaded with h */
-    const float *nw = A.do_norm && A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * H : NULL;
-    float4 wq[2];
-#pragma unroll
-    for (int k = 0; k < 2; k++)
-        wq[k] = nw ? ((const float4 *)nw)[xpos(min(tid + k * DT, HU - 1), swz)] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-    block_copy16_sw(xn, A.h, B * HU, swz ? B * HU : 0);
     __syncthreads();
     PHASE_TS(0, 3);
     if (A.do_norm) {
@@ -268,7 +286,10 @@ __device__ __forceinline__ void gu_row(const DecArgs &A, int j, const QChunk2 &c
 }
 
 /* ---- R: router + shared-gate logit + shared expert gate/up ------------------ */
-extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A, int l)
+/* Router kernel body; ONE: one token (B == 1), whose h is loaded before the
+ * weights (below). */
+template <bool ONE>
+__device__ __forceinline__ void router_body(const DecArgs &A, int l)
 {
     extern __shared__ __align__(16) float lds[];
     __shared__ float red[DW][RMAX_B];
@@ -287,21 +308,50 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A,
     const bool is_sh = !is_row && j < I;
     const int kind = (L.sq6[0] ? 2 : 0) | (L.sq6[1] ? 1 : 0);
     if (threadIdx.x < B) sh_tk[threadIdx.x] = threadIdx.x * 9 + 8;
-    /* 1. weight loads first (independent of h) */
+    /* 1. h and the weights.  With several tokens the weight loads go first
+     * (independent of h) and block_norm copies h.  With one token h (2 units
+     * per thread) and the norm weights are loaded first and each branch
+     * stores h to LDS after its own weight loads, so the store waits for h
+     * only (a wave's loads complete in order) and the norm runs while the
+     * weights are in flight.  A distinct marker after each branch's stores
+     * keeps the compiler from merging them past the join (where the wait
+     * would cover the weights again). */
     float4 w[8];
     QChunk2 ch;
+    const int HU = H / 4;
+    float4 h0, h1, wq[2];
+    const float *nw = NULL;
+    if (ONE) {
+        h0 = ((const float4 *)A.h)[min((int)threadIdx.x, HU - 1)];
+        h1 = ((const float4 *)A.h)[min((int)threadIdx.x + DT, HU - 1)];
+        nw = norm_weights(A, l, wq);
+    }
+#define R_STORE_H(tag)                                                                           \
+    do {                                                                                         \
+        if (ONE) {                                                                               \
+            ((float4 *)xn)[xpos(min((int)threadIdx.x, HU - 1), A.xswz)] = h0;                    \
+            ((float4 *)xn)[xpos(min((int)threadIdx.x + DT, HU - 1), A.xswz)] = h1;               \
+            asm volatile("; h stored, " tag);                                                    \
+        }                                                                                        \
+    } while (0)
     if (is_row) {
         const float *row = task < nrouter ? L.router + (size_t)task * H : L.gate_inp;
 #pragma unroll
         for (int m = 0; m < 8; m++) w[m] = gld_f4(row + min(4 * lane + 256 * m, H - 4));   /* clamped: no masked loads */
+        R_STORE_H("router row");
     } else if (is_sh) {
         if (kind == 0) ch = load_gu_pair<false, false>(L.sgate, L.sup, j, nb, lb, c);
         else if (kind == 3) ch = load_gu_pair<true, true>(L.sgate, L.sup, j, nb, lb, c);
         else if (kind == 2) ch = load_gu_pair<true, false>(L.sgate, L.sup, j, nb, lb, c);
         else ch = load_gu_pair<false, true>(L.sgate, L.sup, j, nb, lb, c);
+        R_STORE_H("shared rows");
+    } else {
+        R_STORE_H("no task");
     }
+#undef R_STORE_H
     /* 2. normalised input into LDS; workgroup 0 publishes it for the gate/up kernel */
-    block_norm(A, l, xn, xsum, red, inv_rms);
+    if (ONE) block_norm_tail(A, xn, xsum, red, inv_rms, wq, nw);
+    else block_norm(A, l, xn, xsum, red, inv_rms);
     if (blockIdx.x == 0)
         for (int i = threadIdx.x; i < B * (H + H / 16) / 4; i += DT) ((float4 *)A.xn_g)[i] = ((const float4 *)xn)[i];
     PHASE_TS(0, 1);
@@ -344,6 +394,9 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A,
     }
     PHASE_TS(0, 2);
 }
+
+extern "C" __global__ void __launch_bounds__(DT, 3) dec_router_kernel(DecArgs A, int l) { router_body<false>(A, l); }
+extern "C" __global__ void __launch_bounds__(DT, 3) dec_router1_kernel(DecArgs A, int l) { router_body<true>(A, l); }
 
 /* ---- GU: routing plan + routed experts' gate/up ----------------------------- */
 
@@ -979,7 +1032,8 @@ static int launch_layer(const DecArgs &A0, int l, bool with_router)
     const size_t lds = norm_lds(A.B, A.H);
     if (with_router) {
         const int ntask = (A.logits_in ? 0 : A.E) + 1 + A.I;
-        hipLaunchKernelGGL(dec_router_kernel, dim3((ntask + DW - 1) / DW), dim3(DT), lds, R.stream, A, l);
+        if (A.B == 1) hipLaunchKernelGGL(dec_router1_kernel, dim3((ntask + DW - 1) / DW), dim3(DT), lds, R.stream, A, l);
+        else hipLaunchKernelGGL(dec_router_kernel, dim3((ntask + DW - 1) / DW), dim3(DT), lds, R.stream, A, l);
         if (rt_check(hipGetLastError(), "router launch")) return ROASTER_EDEVICE;
     }
     if (A.B == 1 && !A.ffn_out) hipLaunchKernelGGL(dec_gu1_kernel, dim3(2 * R.n_cu), dim3(DT), lds, R.stream, A, l);
