@@ -339,8 +339,8 @@ def dense_leg(torch, L, R, dev, stream):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on exactly one GPU: the MoE-FFN hot path is measured "
-                                   "on one MI355X; DESIGN.md describes how it would shard"}))
+        print(json.dumps({"error": "--gpus must be 1: the MoE-FFN hot path is measured on one MI355X "
+                                   "(one GPU's share of an expert-parallel layout, at its real shape)"}))
         sys.exit(2)
     import torch
     import roaster_amd as R
