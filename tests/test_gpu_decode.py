@@ -167,12 +167,14 @@ def test_decode_stack_4_layers(B):
         t.destroy()
 
 
+@pytest.mark.parametrize("B", [1, 8])
 @pytest.mark.parametrize("hidden", [768, 2048])
-def test_decode_stack_norm_weights_batch8(hidden):
-    """Per-layer RMSNorm weights and 8 tokens, at a hidden size whose rows fill
-    whole 512-float blocks (activations swizzled in LDS) and at one that does
-    not (stored plainly)."""
-    B, NL = 8, 2
+def test_decode_stack_norm_weights(hidden, B):
+    """Per-layer RMSNorm weights, one token (the one-token router, gate/up and
+    down paths) and 8 tokens, at a hidden size whose rows fill whole 512-float
+    blocks (activations swizzled in LDS) and at one that does not (stored
+    plainly)."""
+    NL = 2
     log(f"decode stack {NL} layers B={B} hidden={hidden}, norm weights")
     t = SynthTable(5, n_layers=NL, n_experts=64, hidden=hidden)
     try:
