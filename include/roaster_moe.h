@@ -52,6 +52,18 @@ int   roaster_h2d(void *dst, const void *src, size_t bytes);   /* synchronous */
 int   roaster_d2h(void *dst, const void *src, size_t bytes);   /* synchronous */
 int   roaster_memset(void *dst, int value, size_t bytes);      /* stream-ordered */
 
+/* Host weight memory behind kernels.h (kernel_vk_alloc_weights, registered
+ * regions, other host pointers) is served from HBM copies that each call
+ * brings up to date with the host bytes: written pages are found by
+ * userfaultfd write tracking where the kernel offers it (asynchronous write
+ * protection and PAGEMAP_SCAN, Linux 6.7+), else every used range is copied
+ * on each use.  ROASTER_WEIGHT_SYNC=copy in the environment forces copying.
+ * roaster_weight_tracking: enable 1 = track (where available), 0 = copy every
+ * used range on each use (memory that a device writes by DMA after pinning
+ * it), -1 = query.  Returns 1 when writes are tracked.  Needs no GPU. */
+int roaster_weight_tracking(int enable);
+int roaster_weight_sync_stats(unsigned long long *bytes_copied, int *tracking);
+
 /* ---- HBM-resident expert table (replaces weights.c's per-layer LRU cache) -- */
 typedef struct {
     int    n_layers;      /* 40 */

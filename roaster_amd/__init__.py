@@ -111,6 +111,8 @@ _SIG = {
     "roaster_h2d": (C.c_int, [_P, _P, C.c_size_t]),
     "roaster_d2h": (C.c_int, [_P, _P, C.c_size_t]),
     "roaster_memset": (C.c_int, [_P, C.c_int, C.c_size_t]),
+    "roaster_weight_tracking": (C.c_int, [C.c_int]),
+    "roaster_weight_sync_stats": (C.c_int, [C.POINTER(C.c_ulonglong), C.POINTER(C.c_int)]),
     "roaster_table_create": (_P, [C.POINTER(RoasterTableDesc)]),
     "roaster_table_create_layers": (_P, [C.POINTER(RoasterTableDesc), _P]),
     "roaster_gguf_scan": (C.c_int, [C.c_char_p, C.POINTER(RoasterGgufInfo)]),

@@ -416,7 +416,7 @@ extern "C" int roaster_moe_decode_stack(RoasterTable *t, float *h, int B, int la
     return dec_launch(A);
 }
 
-/* ---- small vector kernels (off the MoE path, kept for link compatibility) -- */
+/* ---- f32 router matvec (kernels.c:131-148) -------------------------------- */
 static int up(void *d, const void *s, size_t n)
 {
     return rt_check(hipMemcpyAsync(d, s, n, hipMemcpyHostToDevice, rt().stream), "upload");
@@ -441,45 +441,55 @@ extern "C" void kernel_matvec_f32(const float *matrix, const float *vector, floa
         fill_nan(output, rows);
 }
 
+/* ---- per-call helpers that stay on the host --------------------------------
+ * The reference runs these on the CPU (kernels.c:102-129, 584-720): each call
+ * touches a few kilobytes (one attention head, one conv state, one embedding
+ * row), less than one PCIe round trip would cost, and model.c calls some of
+ * them per head and per KV position (model.c:838, 1580).  They are plain host
+ * code of this library; nothing of the MoE path runs here. */
 extern "C" float kernel_dot_f32(const float *a, const float *b, size_t n)
 {
-    Guard g(rt_lock());
-    if (!n) return 0.0f;
-    kernel_matvec_quant_end();
-    if (rt_init_locked()) return NAN;
-    float *da = (float *)rt_scratch(SCR_IN, 2 * n * 4 + 64);
-    float *dy = (float *)rt_scratch(SCR_OUT, 64);
-    float y = NAN;
-    if (!da || !dy || up(da, a, n * 4) || up(da + n, b, n * 4) || matvec_f32_launch(da, da + n, dy, 1, n) ||
-        down_sync(&y, dy, 4))
-        return NAN;
-    return y;
+    float acc[16] = { 0 };
+    size_t i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int l = 0; l < 16; l++) acc[l] = fmaf(a[i + l], b[i + l], acc[l]);
+    for (int w = 8; w >= 1; w >>= 1)
+        for (int l = 0; l < w; l++) acc[l] += acc[l + w];
+    float s = acc[0];
+    for (; i < n; i++) s = fmaf(a[i], b[i], s);
+    return s;
 }
 
-static void norm_common(float *out, const float *in, const float *w, size_t n, float eps, int mode)
+static float sum_squares(const float *x, size_t n)
 {
-    Guard g(rt_lock());
-    if (!n) return;
-    kernel_matvec_quant_end();
-    float *d = rt_init_locked() ? NULL : (float *)rt_scratch(SCR_IN, 3 * n * 4 + 64);
-    if (!d || up(d, in, n * 4) || (mode == 0 && up(d + n, w, n * 4)) ||
-        norm_launch(d + 2 * n, d, d + n, n, eps, mode) || down_sync(out, d + 2 * n, n * 4))
-        fill_nan(out, n);
+    float acc[16] = { 0 };
+    size_t i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int l = 0; l < 16; l++) acc[l] = fmaf(x[i + l], x[i + l], acc[l]);
+    for (int w = 8; w >= 1; w >>= 1)
+        for (int l = 0; l < w; l++) acc[l] += acc[l + w];
+    float s = acc[0];
+    for (; i < n; i++) s = fmaf(x[i], x[i], s);
+    return s;
 }
 
+/* y = x * (1 / sqrt(mean(x^2) + eps)) * w   (kernels.c:584-605) */
 extern "C" void kernel_rmsnorm(float *output, const float *input, const float *weight, size_t n, float epsilon)
 {
-    norm_common(output, input, weight, n, epsilon, 0);
+    if (!n) return;
+    const float inv = 1.0f / sqrtf(sum_squares(input, n) / (float)n + epsilon);
+    for (size_t i = 0; i < n; i++) output[i] = input[i] * inv * weight[i];
 }
 
+/* y = x / sqrt(sum(x^2) + eps)   (kernels.c:607-622) */
 extern "C" void kernel_l2norm(float *output, const float *input, size_t n, float epsilon)
 {
-    norm_common(output, input, NULL, n, epsilon, 1);
+    if (!n) return;
+    const float inv = 1.0f / sqrtf(sum_squares(input, n) + epsilon);
+    for (size_t i = 0; i < n; i++) output[i] = input[i] * inv;
 }
 
-/* Scalar activations: one float in, one float out; a device round trip would
- * add nothing, so these are plain host math with the reference's formulas
- * (kernels.c:628-642). */
+/* Scalar activations with the reference's two-branch sigmoid (kernels.c:628-642). */
 extern "C" float kernel_sigmoid(float x)
 {
     if (x >= 0.0f) { float z = expf(-x); return 1.0f / (1.0f + z); }
@@ -491,37 +501,71 @@ extern "C" float kernel_silu(float x) { return x * kernel_sigmoid(x); }
 
 extern "C" void kernel_silu_array(float *x, size_t n)
 {
-    Guard g(rt_lock());
-    if (!n) return;
-    kernel_matvec_quant_end();
-    float *d = rt_init_locked() ? NULL : (float *)rt_scratch(SCR_IN, n * 4 + 64);
-    if (!d || up(d, x, n * 4) || silu_array_launch(d, n) || down_sync(x, d, n * 4)) fill_nan(x, n);
+    for (size_t i = 0; i < n; i++) x[i] = kernel_silu(x[i]);
 }
 
+static float h2f(uint16_t h)
+{
+    const uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 31, m = h & 1023;
+    uint32_t b;
+    if (e == 0) {
+        if (!m) b = s;
+        else {                                           /* subnormal: m * 2^-24 */
+            float f = ldexpf((float)m, -24);
+            memcpy(&b, &f, 4);
+            b |= s;
+        }
+    } else if (e == 31) b = s | 0x7F800000u | (m << 13);
+    else b = s | ((e + 112) << 23) | (m << 13);
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+/* One token row of a Q4_K table dequantised (kernels.c:660-690): sub-block j
+ * of a super-block has scale d*sc_j and offset dmin*m_j, the 6-bit sc / m
+ * unpacked from the 12 scale bytes (kernels.c:154-173). */
 extern "C" void kernel_embedding_row_q4_k(const void *weights, size_t token_id, float *output, size_t hidden_size)
 {
-    Guard g(rt_lock());
     if (!hidden_size) return;
-    kernel_matvec_quant_end();
-    if (hidden_size % RQK) { rt_fail(ROASTER_EINVAL, "embedding row: hidden not a multiple of 256"); fill_nan(output, hidden_size); return; }
-    const uint8_t *row = (const uint8_t *)weights + token_id * (hidden_size / RQK) * RQ4K_BYTES;
-    const uint8_t *dw = rt_init_locked() ? NULL : (const uint8_t *)rt_weight_dev(row, hidden_size / RQK * RQ4K_BYTES);
-    float *d = (float *)rt_scratch(SCR_OUT, hidden_size * 4 + 64);
-    if (!dw || !d || q4k_row_launch(dw, d, hidden_size) || down_sync(output, d, hidden_size * 4))
+    if (hidden_size % RQK) {
+        rt_fail(ROASTER_EINVAL, "embedding row: hidden not a multiple of 256");
         fill_nan(output, hidden_size);
+        return;
+    }
+    const size_t nb = hidden_size / RQK;
+    const uint8_t *row = (const uint8_t *)weights + token_id * nb * RQ4K_BYTES;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t *blk = row + b * RQ4K_BYTES;
+        uint16_t hd, hm;
+        memcpy(&hd, blk, 2);
+        memcpy(&hm, blk + 2, 2);
+        const float d = h2f(hd), dmin = h2f(hm);
+        const uint8_t *sb = blk + 4, *qs = blk + 16;
+        float *o = output + b * RQK;
+        for (int j = 0; j < 8; j++) {
+            int sc, mn;
+            if (j < 4) { sc = sb[j] & 63; mn = sb[j + 4] & 63; }
+            else { sc = (sb[j + 4] & 15) | ((sb[j - 4] >> 6) << 4); mn = (sb[j + 4] >> 4) | ((sb[j] >> 6) << 4); }
+            const float s = d * (float)sc, m = dmin * (float)mn;
+            const uint8_t *q = qs + 32 * (j / 2);
+            const int sh = (j & 1) * 4;
+            for (int i = 0; i < 32; i++) o[32 * j + i] = s * (float)((q[i] >> sh) & 15) - m;
+        }
+    }
 }
 
+/* out[c] = sum_k history[k][c] * kernel[c][k] + input[c] * kernel[c][K-1]
+ * (kernels.c:693-720): one causal step of a depthwise convolution. */
 extern "C" void kernel_conv1d_causal_f32(const float *input, const float *history, const float *kernel, float *output,
                                          size_t channels, size_t kernel_size)
 {
-    Guard g(rt_lock());
-    if (kernel_size == 0 || channels == 0) return;
-    kernel_matvec_quant_end();
-    const size_t C = channels, K = kernel_size;
-    float *d = rt_init_locked() ? NULL : (float *)rt_scratch(SCR_IN, (C + (K - 1) * C + C * K + C) * 4 + 64);
-    if (!d) { fill_nan(output, C); return; }
-    float *di = d, *dh = d + C, *dk = dh + (K - 1) * C, *dout = dk + C * K;
-    if (up(di, input, C * 4) || (K > 1 && up(dh, history, (K - 1) * C * 4)) || up(dk, kernel, C * K * 4) ||
-        conv1d_launch(di, dh, dk, dout, C, K) || down_sync(output, dout, C * 4))
-        fill_nan(output, C);
+    if (!kernel_size) return;
+    const size_t K = kernel_size;
+    for (size_t c = 0; c < channels; c++) {
+        float s = 0.0f;
+        for (size_t k = 0; k + 1 < K; k++) s += history[k * channels + c] * kernel[c * K + k];
+        s += input[c] * kernel[c * K + K - 1];
+        output[c] = s;
+    }
 }

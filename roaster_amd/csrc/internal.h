@@ -58,6 +58,16 @@ void rt_registry_clear();
 void rt_register_device_range(const void *dev, size_t bytes);   /* table allocations */
 void rt_unregister_device_range(const void *dev);
 
+/* Write tracking of host memory (wtrack.hip). */
+#include <utility>
+#include <vector>
+size_t wt_page_size();
+int wt_available();                                   /* 1 if writes can be tracked here */
+int wt_register(uintptr_t start, size_t n);           /* 0: pages of the range now tracked */
+/* Written page runs of the pages overlapping [start, start+n), re-protected
+ * in the same walk; 0 ok, -1 if the range cannot be scanned. */
+int wt_scan(uintptr_t start, size_t n, std::vector<std::pair<uintptr_t, uintptr_t>> &runs);
+
 unsigned *rt_ctrl();        /* persistent-kernel control words (device) */
 int rt_take_err();           /* sync the stream, report and clear kernel error bits */
 

@@ -20,9 +20,5 @@ int mv_tasks_for(int rows, size_t cols);
 int mv_launch(const MvJob *jobs_dev, int njobs, int ntasks);
 int silu_mul_launch(float *g, const float *u, size_t n);
 int matvec_f32_launch(const float *W, const float *x, float *y, size_t rows, size_t cols);
-int norm_launch(float *y, const float *x, const float *w, size_t n, float eps, int mode);
-int silu_array_launch(float *x, size_t n);
-int q4k_row_launch(const uint8_t *blocks, float *out, size_t n);
-int conv1d_launch(const float *in, const float *hist, const float *kern, float *out, size_t C, size_t K);
 
 #endif

@@ -157,67 +157,6 @@ __global__ void __launch_bounds__(MV_THREADS) matvec_f32_kernel(const float *W, 
     }
 }
 
-/* mode 0: rmsnorm  y = x * (1/sqrt(mean(x^2) + eps)) * w   (kernels.c:584-605)
- * mode 1: l2norm   y = x * (1/sqrt(sum(x^2) + eps))        (kernels.c:607-622)
- * One workgroup. */
-__global__ void __launch_bounds__(1024) norm_kernel(float *y, const float *x, const float *w, size_t n, float eps,
-                                                   int mode)
-{
-    __shared__ float red[16];
-    float ss = 0.0f;
-    for (size_t i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
-    ss = group_sum<64>(ss);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-    for (int i = 0; i < (int)(blockDim.x >> 6); i++) tot += red[i];
-    const float inv = mode == 0 ? 1.0f / sqrtf(tot / (float)n + eps) : 1.0f / sqrtf(tot + eps);
-    for (size_t i = threadIdx.x; i < n; i += blockDim.x) y[i] = mode == 0 ? x[i] * inv * w[i] : x[i] * inv;
-}
-
-/* kernel_silu_array: x * sigmoid(x) with the two-branch sigmoid (kernels.c:628-652). */
-__global__ void silu_array_kernel(float *x, size_t n)
-{
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        const float v = x[i];
-        float s;
-        if (v >= 0.0f) s = 1.0f / (1.0f + expf(-v));
-        else { const float z = expf(v); s = z / (1.0f + z); }
-        x[i] = v * s;
-    }
-}
-
-/* Dequantise one Q4_K row (kernel_embedding_row_q4_k, kernels.c:660-687):
- * one thread per output element. */
-__global__ void q4k_row_kernel(const uint8_t *blocks, float *out, size_t n)
-{
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        const uint8_t *blk = blocks + (i / RQK) * RQ4K_BYTES;
-        const int w = (int)(i % RQK), g = w / 64, hi = (w % 64) >= 32, k = w % 32;
-        const float d = f16_bits_to_f32(blk[0] | (blk[1] << 8)), dmin = f16_bits_to_f32(blk[2] | (blk[3] << 8));
-        const uint8_t *s = blk + 4;
-        const int j = 2 * g + hi;
-        int sc, m;
-        if (j < 4) { sc = s[j] & 63; m = s[j + 4] & 63; }
-        else { sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4); m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
-        const uint8_t q = blk[16 + 32 * g + k];
-        const int qv = hi ? (q >> 4) : (q & 15);
-        out[i] = fmaf(d * (float)sc, (float)qv, -(dmin * (float)m));
-    }
-}
-
-/* kernel_conv1d_causal_f32 (kernels.c:693-719): one thread per channel. */
-__global__ void conv1d_kernel(const float *input, const float *history, const float *kern, float *out, size_t C,
-                              size_t K)
-{
-    for (size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x; c < C; c += (size_t)gridDim.x * blockDim.x) {
-        float sum = 0.0f;
-        for (size_t k = 0; k + 1 < K; k++) sum = fmaf(history[k * C + c], kern[c * K + k], sum);
-        sum = fmaf(input[c], kern[c * K + K - 1], sum);
-        out[c] = sum;
-    }
-}
-
 /* ---- host launchers ------------------------------------------------------- */
 int mv_launch(const MvJob *jobs_dev, int njobs, int ntasks)
 {
@@ -273,35 +212,4 @@ int matvec_f32_launch(const float *W, const float *x, float *y, size_t rows, siz
     hipLaunchKernelGGL(matvec_f32_kernel, dim3((unsigned)blocks), dim3(MV_THREADS), 0, rt().stream, W, x, y, rows,
                        cols);
     return rt_check(hipGetLastError(), "matvec_f32 launch") ? ROASTER_EDEVICE : 0;
-}
-
-int norm_launch(float *y, const float *x, const float *w, size_t n, float eps, int mode)
-{
-    hipLaunchKernelGGL(norm_kernel, dim3(1), dim3(1024), 0, rt().stream, y, x, w, n, eps, mode);
-    return rt_check(hipGetLastError(), "norm launch") ? ROASTER_EDEVICE : 0;
-}
-
-int silu_array_launch(float *x, size_t n)
-{
-    int blocks = (int)((n + 255) / 256);
-    if (blocks > 4096) blocks = 4096;
-    if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(silu_array_kernel, dim3(blocks), dim3(256), 0, rt().stream, x, n);
-    return rt_check(hipGetLastError(), "silu_array launch") ? ROASTER_EDEVICE : 0;
-}
-
-int q4k_row_launch(const uint8_t *blocks, float *out, size_t n)
-{
-    int b = (int)((n + 255) / 256);
-    if (b < 1) b = 1;
-    hipLaunchKernelGGL(q4k_row_kernel, dim3(b), dim3(256), 0, rt().stream, blocks, out, n);
-    return rt_check(hipGetLastError(), "q4k_row launch") ? ROASTER_EDEVICE : 0;
-}
-
-int conv1d_launch(const float *in, const float *hist, const float *kern, float *out, size_t C, size_t K)
-{
-    int b = (int)((C + 255) / 256);
-    if (b < 1) b = 1;
-    hipLaunchKernelGGL(conv1d_kernel, dim3(b), dim3(256), 0, rt().stream, in, hist, kern, out, C, K);
-    return rt_check(hipGetLastError(), "conv1d launch") ? ROASTER_EDEVICE : 0;
 }

@@ -16,6 +16,8 @@
 #include <sys/mman.h>
 
 #include <map>
+#include <memory>
+#include <unordered_map>
 #include <utility>
 #include <vector>
 
@@ -224,24 +226,59 @@ void *rt_pinned(int slot, size_t bytes)
 }
 
 /* ---- weight registry ------------------------------------------------------
- * (1) arenas: kernel_vk_alloc_weights hands out host addresses in 256 MB
- *     anonymous mappings; each allocation has an HBM twin, uploaded whole on
- *     its first use (weights are written once by the loader, then read).
- * (2) regions: kernel_vk_register_region records a host range with an HBM
- *     twin; sub-ranges are uploaded on their first use.
- * (3) imports: any other host range, uploaded and cached per (pointer, size).
- * kernel_vk_release_host_ptr(p) forgets uploads that start at p, so rewritten
- * bytes are uploaded again on next use.                                      */
+ * Host weight addresses are served from HBM twins that always hold the host
+ * bytes as they are when a call uses them (the reference's GPU reads the host
+ * memory itself, kernels.c:1445-1475, so a write before a call is seen by that
+ * call):
+ * (1) allocs: kernel_vk_alloc_weights hands out host addresses in 256 MB
+ *     anonymous mappings; each allocation's twin sits at the same offset of
+ *     the arena's HBM block;
+ * (2) regions: kernel_vk_register_region records a host range with a twin;
+ * (3) imports: any other host range, with a twin per (pointer, size).
+ * Each use copies what changed: the used range's pages that a write-tracking
+ * scan (wtrack.hip) finds written since their last copy, or -- where tracking
+ * is unavailable -- the whole used range.  A page found written gets a new
+ * version number; every twin records per page the version it copied, so
+ * twins that share a page (adjacent imports, a region over an import) each
+ * refresh it.  Copies go through pinned staging so that the DMA engine never
+ * pins (and so never marks written) the tracked pages themselves.          */
 #define ARENA_BYTES (256ull << 20)
+static const uint32_t VER_NEVER = 0xFFFFFFFFu;
 
-struct Arena { uint8_t *host; uint8_t *dev; size_t used, size; };
-struct Alloc { size_t size; uint8_t *dev; bool uploaded; };
-struct Region { size_t size; uint8_t *dev; std::map<uintptr_t, size_t> up; };
+struct Twin {
+    size_t size;                    /* host bytes [start, start + size) */
+    uint8_t *dev;                   /* device copy of the same bytes */
+    bool tracked;                   /* pages registered for write tracking */
+    bool owns_dev;                  /* dev is this twin's own allocation */
+    std::vector<uint32_t> synced;   /* per page of the span: version copied (VER_NEVER: none) */
+};
+struct Arena { uint8_t *host; uint8_t *dev; size_t used, size; bool tracked; };
 
 static std::vector<Arena> g_arenas;
-static std::map<uintptr_t, Alloc> g_allocs;
-static std::map<uintptr_t, Region> g_regions;
-static std::map<std::pair<uintptr_t, size_t>, void *> g_imports;
+static std::map<uintptr_t, Twin> g_allocs;
+static std::map<uintptr_t, Twin> g_regions;
+static std::map<std::pair<uintptr_t, size_t>, Twin> g_imports;
+
+/* Page versions, in chunks of 512 pages; a page never found written has 0. */
+static uint32_t g_epoch;
+static std::unordered_map<uintptr_t, std::unique_ptr<uint32_t[]>> g_pver;
+static unsigned long long g_sync_bytes;
+
+static uint32_t page_ver(uintptr_t pn)
+{
+    auto it = g_pver.find(pn >> 9);
+    return it == g_pver.end() ? 0 : it->second[pn & 511];
+}
+
+static void set_page_ver(uintptr_t pn, uint32_t v)
+{
+    auto &c = g_pver[pn >> 9];
+    if (!c) {
+        c.reset(new uint32_t[512]);
+        memset(c.get(), 0, 512 * sizeof(uint32_t));
+    }
+    c[pn & 511] = v;
+}
 
 template <class M>
 static typename M::iterator find_containing(M &m, uintptr_t a)
@@ -262,50 +299,150 @@ static bool is_device_pointer(const void *p)
     return at.type == hipMemoryTypeDevice;
 }
 
+/* Host -> device copy through two pinned 8 MB buffers, ordered on the library
+ * stream (kernels launched later on it see the bytes).  Returns when the host
+ * bytes have been read. */
+static uint8_t *g_stage[2];
+static hipEvent_t g_stage_ev[2];
+static bool g_stage_busy[2];
+#define STAGE_BYTES (8u << 20)
+
+static int stage_upload(uint8_t *dst, const uint8_t *src, size_t n)
+{
+    if (!g_stage[0]) {
+        for (int b = 0; b < 2; b++) {
+            if (rt_check(hipHostMalloc((void **)&g_stage[b], STAGE_BYTES, hipHostMallocDefault), "staging hipHostMalloc") ||
+                rt_check(hipEventCreateWithFlags(&g_stage_ev[b], hipEventDisableTiming), "staging event"))
+                return ROASTER_EDEVICE;
+            g_stage_busy[b] = false;
+        }
+    }
+    static int next;
+    for (size_t off = 0; off < n; off += STAGE_BYTES) {
+        const size_t len = n - off < STAGE_BYTES ? n - off : STAGE_BYTES;
+        const int b = next;
+        next ^= 1;
+        if (g_stage_busy[b] && rt_check(hipEventSynchronize(g_stage_ev[b]), "staging wait")) return ROASTER_EDEVICE;
+        memcpy(g_stage[b], src + off, len);
+        if (rt_check(hipMemcpyAsync(dst + off, g_stage[b], len, hipMemcpyHostToDevice, g_rt.stream), "weight upload") ||
+            rt_check(hipEventRecord(g_stage_ev[b], g_rt.stream), "staging record"))
+            return ROASTER_EDEVICE;
+        g_stage_busy[b] = true;
+    }
+    g_sync_bytes += n;
+    return 0;
+}
+
+static void stage_release()
+{
+    for (int b = 0; b < 2; b++) {
+        if (!g_stage[b]) continue;
+        if (g_stage_busy[b]) (void)hipEventSynchronize(g_stage_ev[b]);
+        (void)hipEventDestroy(g_stage_ev[b]);
+        (void)hipHostFree(g_stage[b]);
+        g_stage[b] = NULL;
+        g_stage_busy[b] = false;
+    }
+}
+
+static void twin_init(Twin &T, size_t size, uint8_t *dev, bool owns, uintptr_t host, bool tracked)
+{
+    const size_t P = wt_page_size();
+    const uintptr_t p0 = host & ~(uintptr_t)(P - 1), p1 = (host + size + P - 1) & ~(uintptr_t)(P - 1);
+    T.size = size;
+    T.dev = dev;
+    T.owns_dev = owns;
+    T.tracked = tracked;
+    T.synced.assign(tracked ? (p1 - p0) / P : 0, VER_NEVER);
+}
+
+/* Make the twin hold the current host bytes of [a, a + bytes) (a inside the
+ * twin that starts at host address h). */
+static int twin_sync(Twin &T, uintptr_t h, uintptr_t a, size_t bytes)
+{
+    if (!T.tracked || !wt_available()) return stage_upload(T.dev + (a - h), (const uint8_t *)a, bytes);
+    const size_t P = wt_page_size();
+    const uintptr_t s0 = h & ~(uintptr_t)(P - 1);
+    const uintptr_t p_lo = a & ~(uintptr_t)(P - 1), p_hi = (a + bytes + P - 1) & ~(uintptr_t)(P - 1);
+    std::vector<std::pair<uintptr_t, uintptr_t>> runs;
+    if (wt_scan(p_lo, p_hi - p_lo, runs)) {
+        /* The range is no longer tracked (remapped behind the library's back):
+         * copy on every use from now on. */
+        T.tracked = false;
+        T.synced.clear();
+        return stage_upload(T.dev + (a - h), (const uint8_t *)a, bytes);
+    }
+    if (!runs.empty()) {
+        ++g_epoch;
+        for (auto &r : runs)
+            for (uintptr_t pg = r.first; pg < r.second; pg += P) set_page_ver(pg / P, g_epoch);
+    }
+    /* Whole pages (clipped to the twin): the scan re-protected them, so this
+     * twin must now hold all of each, not only the part inside [a, a+bytes). */
+    uintptr_t run0 = 0, run1 = 0;
+    for (uintptr_t pg = p_lo; pg < p_hi; pg += P) {
+        uint32_t &s = T.synced[(pg - s0) / P];
+        const uint32_t v = page_ver(pg / P);
+        const bool stale = s == VER_NEVER || v > s;
+        if (stale) {
+            s = v;
+            const uintptr_t lo = pg > h ? pg : h, hi = pg + P < h + T.size ? pg + P : h + T.size;
+            if (run1 == lo) run1 = hi;
+            else {
+                if (run1 > run0 && stage_upload(T.dev + (run0 - h), (const uint8_t *)run0, run1 - run0)) return ROASTER_EDEVICE;
+                run0 = lo;
+                run1 = hi;
+            }
+        }
+    }
+    if (run1 > run0 && stage_upload(T.dev + (run0 - h), (const uint8_t *)run0, run1 - run0)) return ROASTER_EDEVICE;
+    return 0;
+}
+
 const void *rt_weight_dev(const void *ptr, size_t bytes)
 {
     if (!ptr) { rt_fail(ROASTER_EINVAL, "NULL weight pointer"); return NULL; }
-    uintptr_t a = (uintptr_t)ptr;
+    const uintptr_t a = (uintptr_t)ptr;
     auto al = find_containing(g_allocs, a);
     if (al != g_allocs.end()) {
-        Alloc &A = al->second;
-        if (a + bytes > al->first + A.size) { rt_fail(ROASTER_EINVAL, "weight range overruns its allocation"); return NULL; }
-        if (!A.uploaded) {
-            if (rt_check(hipMemcpy(A.dev, (const void *)al->first, A.size, hipMemcpyHostToDevice), "weight upload"))
-                return NULL;
-            A.uploaded = true;
-        }
-        return A.dev + (a - al->first);
+        Twin &T = al->second;
+        if (a + bytes > al->first + T.size) { rt_fail(ROASTER_EINVAL, "weight range overruns its allocation"); return NULL; }
+        if (twin_sync(T, al->first, a, bytes)) return NULL;
+        return T.dev + (a - al->first);
     }
     auto rg = find_containing(g_regions, a);
     if (rg != g_regions.end()) {
-        Region &R = rg->second;
-        if (a + bytes > rg->first + R.size) { rt_fail(ROASTER_EINVAL, "weight range overruns its region"); return NULL; }
-        auto u = R.up.find(a);
-        if (u == R.up.end() || u->second < bytes) {
-            if (rt_check(hipMemcpy(R.dev + (a - rg->first), ptr, bytes, hipMemcpyHostToDevice), "region upload"))
-                return NULL;
-            R.up[a] = bytes;
-        }
-        return R.dev + (a - rg->first);
+        Twin &T = rg->second;
+        if (a + bytes > rg->first + T.size) { rt_fail(ROASTER_EINVAL, "weight range overruns its region"); return NULL; }
+        if (twin_sync(T, rg->first, a, bytes)) return NULL;
+        return T.dev + (a - rg->first);
     }
     if (is_device_pointer(ptr)) return ptr;
     auto key = std::make_pair(a, bytes);
     auto im = g_imports.find(key);
-    if (im != g_imports.end()) return im->second;
-    void *d = NULL;
-    if (rt_check(hipMalloc(&d, bytes + RT_TAIL_PAD), "import hipMalloc")) return NULL;
-    if (rt_check(hipMemcpy(d, ptr, bytes, hipMemcpyHostToDevice), "import upload")) { (void)hipFree(d); return NULL; }
-    g_imports[key] = d;
-    return d;
+    if (im == g_imports.end()) {
+        void *d = NULL;
+        if (rt_check(hipMalloc(&d, bytes + RT_TAIL_PAD), "import hipMalloc")) return NULL;
+        Twin T;
+        twin_init(T, bytes, (uint8_t *)d, true, a, wt_register(a, bytes) == 0);
+        im = g_imports.emplace(key, std::move(T)).first;
+    }
+    if (twin_sync(im->second, a, a, bytes)) return NULL;
+    return im->second.dev;
+}
+
+static void free_twin(Twin &T)
+{
+    if (T.owns_dev && T.dev) (void)hipFree(T.dev);
+    T.dev = NULL;
 }
 
 void rt_registry_clear()
 {
     (void)hipDeviceSynchronize();
-    for (auto &kv : g_imports) (void)hipFree(kv.second);
+    for (auto &kv : g_imports) free_twin(kv.second);
     g_imports.clear();
-    for (auto &kv : g_regions) (void)hipFree(kv.second.dev);
+    for (auto &kv : g_regions) free_twin(kv.second);
     g_regions.clear();
     g_allocs.clear();
     for (auto &ar : g_arenas) {
@@ -313,6 +450,8 @@ void rt_registry_clear()
         munmap(ar.host, ar.size);
     }
     g_arenas.clear();
+    g_pver.clear();
+    stage_release();
 }
 
 /* kernels.h:103 -- 4 KB-aligned bump allocation from 256 MB blocks (kernels.c:1445-1537);
@@ -336,17 +475,18 @@ extern "C" void *kernel_vk_alloc_weights(size_t size, size_t *granted)
             rt_fail(ROASTER_ENOMEM, "HBM arena of %zu bytes unavailable", asz);
             return NULL;
         }
+        /* Base pages keep write tracking at 4 KB granularity. */
+        (void)madvise(na.host, asz, MADV_NOHUGEPAGE);
+        na.tracked = wt_register((uintptr_t)na.host, asz) == 0;
         na.used = 0;
         na.size = asz;
         g_arenas.push_back(na);
         ar = &g_arenas.back();
     }
     uint8_t *h = ar->host + ar->used;
-    Alloc A;
-    A.size = need;
-    A.dev = ar->dev + ar->used;
-    A.uploaded = false;
-    g_allocs[(uintptr_t)h] = A;
+    Twin T;
+    twin_init(T, need, ar->dev + ar->used, false, (uintptr_t)h, ar->tracked);
+    g_allocs.emplace((uintptr_t)h, std::move(T));
     ar->used += need;
     if (granted) *granted = need;
     return h;
@@ -364,36 +504,59 @@ extern "C" int kernel_vk_free_weights(void *ptr)
     return kernel_vk_owns_weights(ptr);
 }
 
+/* kernels.c:1431-1443: one twin for a whole host range (weights.c:527-529
+ * registers its expert-cache slab); ranges inside it are then served from it. */
 extern "C" int kernel_vk_register_region(const void *ptr, size_t size)
 {
     std::lock_guard<std::recursive_mutex> g(g_lock);
     if (!ptr || !size || rt_init_locked()) return 0;
     if (find_containing(g_regions, (uintptr_t)ptr) != g_regions.end()) return 1;
-    Region R;
-    R.size = size;
-    R.dev = NULL;
-    if (hipMalloc((void **)&R.dev, size + RT_TAIL_PAD) != hipSuccess) { (void)hipGetLastError(); return 0; }
-    g_regions[(uintptr_t)ptr] = R;
+    uint8_t *dev = NULL;
+    if (hipMalloc((void **)&dev, size + RT_TAIL_PAD) != hipSuccess) { (void)hipGetLastError(); return 0; }
+    Twin T;
+    twin_init(T, size, dev, true, (uintptr_t)ptr, wt_register((uintptr_t)ptr, size) == 0);
+    g_regions.emplace((uintptr_t)ptr, std::move(T));
     return 1;
 }
 
+/* kernels.c:1402-1429: drop every import and region that starts at ptr (the
+ * caller is about to free that memory; weights.c:333-339).  Imports that lie
+ * inside a dropped region go with it.  Arena memory is the library's own and
+ * is released at shutdown only. */
 extern "C" void kernel_vk_release_host_ptr(const void *ptr)
 {
     std::lock_guard<std::recursive_mutex> g(g_lock);
-    uintptr_t a = (uintptr_t)ptr;
+    if (!ptr) return;
+    const uintptr_t a = (uintptr_t)ptr;
+    uintptr_t lo = a, hi = a + 1;
+    auto rg = g_regions.find(a);
+    if (rg != g_regions.end()) hi = a + rg->second.size;
+    bool synced = false;
     for (auto it = g_imports.begin(); it != g_imports.end();) {
-        if (it->first.first == a) {
-            (void)hipStreamSynchronize(g_rt.stream);
-            (void)hipFree(it->second);
+        const uintptr_t s = it->first.first;
+        if (s == a || (s >= lo && s + it->first.second <= hi)) {
+            if (!synced) { (void)hipStreamSynchronize(g_rt.stream); synced = true; }
+            free_twin(it->second);
             it = g_imports.erase(it);
         } else {
             ++it;
         }
     }
-    auto al = g_allocs.find(a);
-    if (al != g_allocs.end()) al->second.uploaded = false;
-    auto rg = find_containing(g_regions, a);
-    if (rg != g_regions.end()) rg->second.up.erase(a);
+    if (rg != g_regions.end()) {
+        if (!synced) (void)hipStreamSynchronize(g_rt.stream);
+        free_twin(rg->second);
+        g_regions.erase(rg);
+    }
+}
+
+/* Bytes copied host -> HBM by the registry since load, and whether writes are
+ * tracked (1) or every used range is copied on each use (0). */
+extern "C" int roaster_weight_sync_stats(unsigned long long *bytes_copied, int *tracking)
+{
+    std::lock_guard<std::recursive_mutex> g(g_lock);
+    if (bytes_copied) *bytes_copied = g_sync_bytes;
+    if (tracking) *tracking = wt_available();
+    return 0;
 }
 
 extern "C" void kernel_vk_trim_scratch(void)

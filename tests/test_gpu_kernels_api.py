@@ -134,32 +134,15 @@ def test_ffn_fused_nine_experts():
     assert R.lib().kernel_ffn_fused(fx, 9, x.ctypes.data, 500, 2048) == 0      # multiples of 256
 
 
-def test_small_vector_kernels():
-    log("small vector kernels")
-    L = R.lib()
+def test_router_matvec_f32():
+    """kernel_matvec_f32 (the router product, kernels.c:131-148) on the GPU."""
+    log("matvec_f32")
     x = R.synth_normal(3, R.synth_stream(0, 0, 5), 2048)
-    w = (R.synth_normal(3, R.synth_stream(0, 1, 6), 2048, 0.1) + np.float32(1)).astype(np.float32)
-    y = np.empty(2048, np.float32)
-    L.kernel_rmsnorm(y.ctypes.data, x.ctypes.data, w.ctypes.data, 2048, C.c_float(1e-6))
-    ref = np.empty(2048, np.float32)
-    O.orc().orc_rmsnorm(ref.ctypes.data, x.ctypes.data, w.ctypes.data, 2048, C.c_float(1e-6))
-    assert rel_err(y, ref) <= 1e-6
-    a = R.synth_normal(4, 1, 1000)
-    b = R.synth_normal(4, 2, 1000)
-    assert abs(L.kernel_dot_f32(a.ctypes.data, b.ctypes.data, 1000) - float(a.astype(np.float64) @ b)) < 1e-4
     Wf = R.synth_normal(4, 3, 64 * 2048).reshape(64, 2048)
     yy = np.empty(64, np.float32)
-    L.kernel_matvec_f32(Wf.ctypes.data, x.ctypes.data, yy.ctypes.data, 64, 2048)
+    R.lib().kernel_matvec_f32(Wf.ctypes.data, x.ctypes.data, yy.ctypes.data, 64, 2048)
     assert rel_err(yy, O.matvec_f32(Wf, x)) <= 1e-5
-    s = x.copy()
-    L.kernel_silu_array(s.ctypes.data, 2048)
-    ref = x.astype(np.float64) / (1 + np.exp(-x.astype(np.float64)))
-    assert rel_err(s, ref) <= 1e-6
-    emb = R.synth_q4k(5, 1, 3 * 8)
-    row = np.empty(2048, np.float32)
-    L.kernel_embedding_row_q4_k(alloc_w(emb), 2, row.ctypes.data, 2048)
-    ref = np.empty(2048, np.float32)
-    for k in range(8):
-        blk = np.ascontiguousarray(emb[(16 + k) * 144:(17 + k) * 144])
-        O.orc().orc_dequant_q4k_block(blk.ctypes.data, ref[256 * k:].ctypes.data)
-    np.testing.assert_array_equal(row, ref)
+    Wr = R.synth_normal(1, 9, 256 * 2048, 0.02).reshape(256, 2048)
+    yr = np.empty(256, np.float32)
+    R.lib().kernel_matvec_f32(Wr.ctypes.data, x.ctypes.data, yr.ctypes.data, 256, 2048)
+    assert rel_err(yr, O.matvec_f32(Wr, x)) <= 1e-5
