@@ -160,6 +160,19 @@ int roaster_moe_decode(RoasterTable *t, int layer, const float *x, int B, float 
 int roaster_moe_decode_stack(RoasterTable *t, float *h, int B, int layer0, int n_layers,
                              const float *norm_w, float eps, int *ids_out, float *w_out);
 
+/* No counterpart in the reference: roaster_moe_decode_stack for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, kernels and
+ * results; every intermediate lives in a fixed 512 KiB device array that the
+ * library sets up in roaster_init (call it first) and keeps until the process
+ * ends, so the call itself makes no allocation.  Calls whose intermediates
+ * exceed it -- about 8 tokens x hidden 2048 x inter 1024 or more -- return
+ * ROASTER_EINVAL.  Every call on a device shares that device's array and
+ * leaves its contents behind: calls on the library stream run one after the
+ * other, but two processes' or streams' calls that overlapped would race. */
+int roaster_moe_decode_stack_noalloc(RoasterTable *t, float *h, int B, int layer0, int n_layers,
+                                     const float *norm_w, float eps, int *ids_out, float *w_out);
+
 /* ---- dense projections ---------------------------------------------------- */
 /* Y[t * rows + r] = W[r] . X[t * cols ..] for t < T (1..8): a quantised
  * [rows x cols] matrix on the device (q6: 0 = Q4_K, 1 = Q6_K, cols a multiple

@@ -132,6 +132,7 @@ _SIG = {
     "roaster_table_synth": (C.c_int, [_P, C.c_uint64, C.POINTER(RoasterSynthSpec)]),
     "roaster_moe_decode": (C.c_int, [_P, C.c_int, _P, C.c_int, _P, C.POINTER(RoasterDecodeIO)]),
     "roaster_moe_decode_stack": (C.c_int, [_P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_float, _P, _P]),
+    "roaster_moe_decode_stack_noalloc": (C.c_int, [_P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_float, _P, _P]),
     "roaster_moe_prefill": (C.c_int, [_P, C.c_int, _P, C.c_int, _P, C.POINTER(RoasterPrefillOpts)]),
 }
 

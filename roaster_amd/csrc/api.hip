@@ -416,6 +416,71 @@ extern "C" int roaster_moe_decode_stack(RoasterTable *t, float *h, int B, int la
     return dec_launch(A);
 }
 
+/* ---- the layer stack without allocation -------------------------------------
+ * roaster_moe_decode_stack_noalloc runs the kernels of roaster_moe_decode_stack
+ * with every intermediate (error word, plan, logits, shared-gate logits,
+ * SiLU*up rows, normalised input) in one file-scope device array instead of
+ * the library's grow-only scratch, so that a caller that cannot allocate
+ * device memory can call it.  In host code `scratch` names a host-side
+ * stand-in, not the device array: its device address is looked up once per
+ * device at initialisation (noalloc_setup) and only that address is used. */
+#define NOALLOC_BYTES (512u << 10)
+static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
+
+#define NOALLOC_MAX_DEV 64
+static uint8_t *g_noalloc[NOALLOC_MAX_DEV];      /* device address of `scratch` per device */
+
+int noalloc_setup(int dev)
+{
+    if (dev < 0 || dev >= NOALLOC_MAX_DEV) return rt_fail(ROASTER_EDEVICE, "device index %d out of range", dev);
+    if (g_noalloc[dev]) return 0;
+    void *p = NULL;
+    if (rt_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return ROASTER_EDEVICE;
+    g_noalloc[dev] = (uint8_t *)p;
+    rt_set_aux_err((int *)p);        /* the error word is the array's first int */
+    return 0;
+}
+
+static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+extern "C" int roaster_moe_decode_stack_noalloc(RoasterTable *t, float *h, int B, int layer0, int n_layers,
+                                                const float *norm_w, float eps, int *ids_out, float *w_out)
+{
+    Guard g(rt_lock());
+    if (rt_init_locked()) return ROASTER_EDEVICE;
+    if (!t || !h || B < 1 || B > RMAX_B || layer0 < 0 || n_layers < 1 || layer0 + n_layers > t->d.n_layers)
+        return rt_fail(ROASTER_EINVAL, "roaster_moe_decode_stack_noalloc: bad arguments");
+    uint8_t *base = g_noalloc[rt().device];
+    if (!base) return rt_fail(ROASTER_EDEVICE, "roaster_moe_decode_stack_noalloc: scratch address not set up");
+    DecArgs A;
+    fill_table_args(A, t);
+    const size_t E = (size_t)A.E, Bz = (size_t)B, H = (size_t)A.H, I = (size_t)A.I;
+    const size_t o_plan = 256, o_log = o_plan + al256(sizeof(DecPlan)), o_sg = o_log + al256(Bz * E * 4),
+                 o_eh = o_sg + al256(Bz * 4), o_xn = o_eh + al256(Bz * 9 * I * 4), end = o_xn + al256(Bz * (H + H / 16) * 4);
+    if (end > NOALLOC_BYTES)
+        return rt_fail(ROASTER_EINVAL,
+                       "roaster_moe_decode_stack_noalloc: %d tokens x hidden %zu x inter %zu x %zu experts need %zu "
+                       "scratch bytes, above the %u-byte maximum",
+                       B, H, I, E, end, NOALLOC_BYTES);
+    A.layer0 = layer0;
+    A.nlayers = n_layers;
+    A.B = B;
+    A.h = h;
+    A.y = NULL;
+    A.norm_w = norm_w;
+    A.eps = eps;
+    A.do_norm = 1;
+    A.ids_out = ids_out;
+    A.w_out = w_out;
+    A.err = (int *)base;
+    A.plan_g = (DecPlan *)(base + o_plan);
+    A.logits = (float *)(base + o_log);
+    A.sgate_raw = (float *)(base + o_sg);
+    A.eh = (float *)(base + o_eh);
+    A.xn_g = (float *)(base + o_xn);
+    return dec_launch(A);
+}
+
 /* ---- f32 router matvec (kernels.c:131-148) -------------------------------- */
 static int up(void *d, const void *s, size_t n)
 {

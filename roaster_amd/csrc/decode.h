@@ -73,7 +73,10 @@ struct DecArgs {
     float *ffn_out;             /* [n x H] or NULL */
 };
 
-int dec_launch(DecArgs &A);          /* all layers of A: 3 kernels per layer */
+/* All layers of A: 3 kernels per layer.  A.plan_g and A.err may be set by the
+ * caller (device memory of sizeof(DecPlan) and one int); when either is NULL
+ * the library's own scratch and control words are used. */
+int dec_launch(DecArgs &A);
 int dec_ffn_launch(DecArgs &A);      /* kernel_ffn_fused: gate/up + down kernels */
 
 #endif

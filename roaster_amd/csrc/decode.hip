@@ -1050,10 +1050,12 @@ int dec_launch(DecArgs &A)
 {
     A.xswz = A.H % 512 == 0;
     if (A.E > 256) return rt_fail(ROASTER_EINVAL, "decode supports at most 256 routed experts");
-    unsigned *ctrl = rt_ctrl();
-    A.plan_g = (DecPlan *)rt_scratch(SCR_C, sizeof(DecPlan));
-    if (!ctrl || !A.plan_g) return ROASTER_ENOMEM;
-    A.err = (int *)(ctrl + 16);
+    if (!A.plan_g || !A.err) {          /* caller-provided plan and error word, or the library's own */
+        unsigned *ctrl = rt_ctrl();
+        A.plan_g = (DecPlan *)rt_scratch(SCR_C, sizeof(DecPlan));
+        if (!ctrl || !A.plan_g) return ROASTER_ENOMEM;
+        A.err = (int *)(ctrl + 16);
+    }
     for (int l = A.layer0; l < A.layer0 + A.nlayers; l++)
         if (int rc = launch_layer(A, l, true)) return rc;
     return 0;

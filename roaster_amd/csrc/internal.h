@@ -70,6 +70,8 @@ int wt_scan(uintptr_t start, size_t n, std::vector<std::pair<uintptr_t, uintptr_
 
 unsigned *rt_ctrl();        /* persistent-kernel control words (device) */
 int rt_take_err();           /* sync the stream, report and clear kernel error bits */
+void rt_set_aux_err(int *dev_word);   /* a second device error word rt_take_err reports and clears */
+int noalloc_setup(int dev);  /* api.hip: device address of the allocation-free scratch array */
 
 /* Launch helpers */
 int rt_coop_grid(const void *kernel, int threads, size_t lds, int *blocks_out);

@@ -64,6 +64,9 @@ int rt_init_locked()
     g_rt.n_xcd = 8;            /* MI355X: 8 XCDs of 32 CUs */
     g_rt.hbm_bytes = p.totalGlobalMem;
     g_rt.inited = 1;
+    /* device address of the allocation-free entry point's scratch array; a
+     * failure is reported by that entry point and leaves the others working */
+    (void)noalloc_setup(dev);
     return 0;
 }
 
@@ -84,6 +87,9 @@ extern "C" void *roaster_stream(void)
  * before each launch), [16] sticky error bits (1 = routing found fewer than 8
  * finite logits, 2 = a grid barrier wait timed out), cleared when reported. */
 static unsigned *g_ctrl;
+static int *g_aux_err;      /* error word of the allocation-free entry point's scratch, or NULL */
+
+void rt_set_aux_err(int *dev_word) { g_aux_err = dev_word; }
 
 unsigned *rt_ctrl()
 {
@@ -97,12 +103,17 @@ unsigned *rt_ctrl()
 int rt_take_err()
 {
     if (rt_check(hipStreamSynchronize(g_rt.stream), "hipStreamSynchronize")) return ROASTER_EDEVICE;
-    if (!g_ctrl) return 0;
     int e = 0;
-    if (rt_check(hipMemcpy(&e, g_ctrl + 16, sizeof(int), hipMemcpyDeviceToHost), "error word readback"))
-        return ROASTER_EDEVICE;
+    int *words[2] = { g_ctrl ? (int *)(g_ctrl + 16) : NULL, g_aux_err };
+    for (int i = 0; i < 2; i++) {
+        if (!words[i]) continue;
+        int w = 0;
+        if (rt_check(hipMemcpy(&w, words[i], sizeof(int), hipMemcpyDeviceToHost), "error word readback"))
+            return ROASTER_EDEVICE;
+        if (w && rt_check(hipMemset(words[i], 0, sizeof(int)), "error word reset")) return ROASTER_EDEVICE;
+        e |= w;
+    }
     if (!e) return 0;
-    if (rt_check(hipMemset(g_ctrl + 16, 0, sizeof(int)), "error word reset")) return ROASTER_EDEVICE;
     if (e & 2) return rt_fail(ROASTER_EDEVICE, "a grid barrier timed out (workgroups not co-resident?)");
     return rt_fail(ROASTER_EROUTE, "router produced fewer than 8 finite logits for some token");
 }
