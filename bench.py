@@ -12,12 +12,16 @@ and weights are synthetic (seeded) and already in HBM when timing starts.
 Also reported in the same JSON line:
   batch8   -- 8 slots, one token each, through the same stack;
   prefill  -- the MoE block over T tokens: 2048 tokens through 4 all-Q6_K
-              layers with N(0,1) logits given (the MFMA roofline line), and 512
-              tokens through one Q4_K/Q6_K layer with the router and a
-              Zipf(1.1) per-expert logit bias;
+              layers with N(0,1) logits given (its value, MFMA roofline and CPU
+              baseline), and 512 tokens through one Q4_K/Q6_K layer with the
+              router and a Zipf(1.1) per-expert logit bias (HBM-bound roofline);
+  config1  -- one Q4_K [512 x 2048] matvec: cache-resident latency and the HBM
+              rate over 512 rotated copies;
+  config2  -- one decode MoE block: device time and isolated latency;
   dense    -- the LM head [248320 x 2048] Q6_K as a dense projection, 1 and 8
               tokens, with its HBM roofline;
-  roofline / cpu_baseline -- see below.
+  roofline / cpu_baseline -- see below; roofline.traffic is read from the
+              committed rocprofv3 counter summary profiles/traffic_per_step.md.
 Kernel times come from HIP events recorded on the library's stream.  The CPU
 baselines run the reference's own C kernels (compiled from the reference tree
 into oracle/_ref) on a bounded sample of the same workloads on this host.
@@ -66,6 +70,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill legs")
     ap.add_argument("--cpu-tokens", type=int, default=160)
     ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--legs", default="decode,prefill,config1,config2,dense",
+                    help="comma-separated legs to run (the decode headline always runs unless omitted here)")
     return ap.parse_args()
 
 
@@ -109,7 +115,40 @@ def omp_threads():
         return int(os.environ.get("OMP_NUM_THREADS", "1"))
 
 
-def cpu_baseline_decode(table_seed, n_tokens, table=None):
+def host_cpu():
+    """CPU model and the SIMD extensions the reference's CPU kernels use
+    (kernels.c picks its AVX2 / FMA / F16C paths at compile time)."""
+    model, flags = None, set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if model is None and line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                elif not flags and line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    return {"cpu_model": model, "isa": [x for x in ("avx2", "fma", "f16c") if x in flags],
+            "build": "gcc -O3 -mavx2 -mfma -mf16c -fopenmp (kernels.c CPU subset compiled from the reference tree)"}
+
+
+def profiled_traffic(workload):
+    """HBM traffic per step of `workload` from the committed counter summary
+    (profiles/traffic_per_step.md: FETCH_SIZE and WRITE_SIZE passes of
+    rocprofv3, scaled by the copy-kernel calibration stated there), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic_per_step.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) >= 3 and cells[0] == workload:
+                    return int(cells[1].replace(",", "")) + int(cells[2].replace(",", ""))
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def cpu_baseline_decode(table_seed, n_tokens, table=None, n_layers=N_LAYERS, x_stream=1000):
     """The reference's CPU decode path (kernels.c AVX2 kernels via oracle/_ref,
     composed as model.c:1059-1146 does, one thread as the reference's OpenMP
     thresholds keep it) on a bounded sample: n_tokens tokens through all 40
@@ -123,8 +162,8 @@ def cpu_baseline_decode(table_seed, n_tokens, table=None):
     routers = {}
     total = 0.0
     for tk in range(n_tokens):
-        h = R.synth_normal(table_seed, R.synth_stream(0, 1000 + tk, 5), H)
-        for l in range(N_LAYERS):
+        h = R.synth_normal(table_seed, R.synth_stream(0, x_stream + tk, 5), H)
+        for l in range(n_layers):
             if l not in routers:
                 routers[l] = R.host_router(table_seed, l, desc)
             router, gi = routers[l]
@@ -167,30 +206,34 @@ def cpu_baseline_decode(table_seed, n_tokens, table=None):
             h = (h + y).astype(np.float32)
             total += time.perf_counter() - t0
     tok_s = n_tokens / total
-    return {"value": round(tok_s, 3), "unit": "tokens/s", "cores": 1, "kind": kind,
-            "sample": f"{n_tokens} tokens x {N_LAYERS} layers of the batch-1 decode stack (router, top-8, "
-                      f"8+1 experts, combine; {total:.2f} s of CPU work), same table seed"}
+    out = {"value": round(tok_s, 3), "unit": "tokens/s", "cores": 1, "kind": kind,
+           "sample": f"{n_tokens} tokens x {n_layers} layers of the batch-1 decode stack (router, top-8, "
+                     f"8+1 experts, combine; {total:.2f} s of CPU work), same table seed",
+           "us_per_layer": round(total / (n_tokens * n_layers) * 1e6, 2)}
+    out.update(host_cpu())
+    return out
 
 
-def cpu_baseline_prefill(table, desc, seed, X, bias, ids, reps=2):
-    """The reference's CPU prefill block (model.c:1671-1791 composition over
-    its kernels.c routines via oracle/_ref: router matvec per token, moe_cpu
-    over the expert row groups -- OpenMP-parallel as kernels.c:1882 is -- and
-    moe_cpu for the shared expert) on the 512-token Zipf layer, with the
-    GPU's routing.  Gathers and the combine are outside the timed region."""
+def cpu_baseline_prefill(table, desc, seed, X, ids, layer=0, with_router=True, reps=2, label=""):
+    """The reference's CPU prefill block (model.c:1671-1791 composed over its
+    kernels.c routines via oracle/_ref: the router matvec per token when the
+    workload has one, moe_cpu over the expert row groups -- OpenMP-parallel
+    over 32-row tiles as kernels.c:1882 is -- and moe_cpu for the shared
+    expert over all T tokens) with the GPU's routing ids [T x 8].  Gathers and
+    the combine are outside the timed region."""
     import roaster_amd as R
     from oracle import oracle as O
     if not O.ref_available():
         return None
     Rf = O.ref()
     T = X.shape[0]
-    router, gi = R.host_router(seed, 0, desc)
-    mats = {e: fetch_expert(R, table, seed, 0, e, desc) for e in range(E + 1)}
+    router, gi = R.host_router(seed, layer, desc)
     groups = []
     for e in range(E):
         rows = np.nonzero((ids == e).any(axis=1))[0]
         if len(rows):
             groups.append((e, rows))
+    mats = {e: fetch_expert(R, table, seed, layer, e, desc) for e in [g[0] for g in groups] + [E]}
     n_tot = sum(len(r) for _, r in groups)
     Xg = np.ascontiguousarray(np.concatenate([X[r] for _, r in groups]))
     Dg = np.empty((n_tot, H), np.float32)
@@ -203,18 +246,22 @@ def cpu_baseline_prefill(table, desc, seed, X, bias, ids, reps=2):
     sh[0] = R.KernelMoeExpert(g.ctypes.data, u.ctypes.data, d.ctypes.data, desc.sh_q6[0], desc.sh_q6[1], desc.sh_q6[2], T)
     Ds = np.empty((T, H), np.float32)
     lg = np.empty(E, np.float32)
+    X = np.ascontiguousarray(X, np.float32)
     best = None
     for _ in range(reps):
         t0 = time.perf_counter()
-        for t in range(T):
-            Rf.kernel_matvec_f32(router.ctypes.data, X[t].ctypes.data, lg.ctypes.data, E, H)
+        if with_router:
+            for t in range(T):
+                Rf.kernel_matvec_f32(router.ctypes.data, X[t].ctypes.data, lg.ctypes.data, E, H)
         Rf.ref_moe_cpu(C.cast(sh, C.c_void_p), 1, X.ctypes.data, Ds.ctypes.data, I, H)
         Rf.ref_moe_cpu(C.cast(exs, C.c_void_p), len(groups), Xg.ctypes.data, Dg.ctypes.data, I, H)
         dt = time.perf_counter() - t0
         best = dt if best is None else min(best, dt)
-    return {"value": round(T / best, 1), "unit": "tokens/s", "cores": omp_threads(), "kind": "reference",
-            "sample": f"one {T}-token Zipf-routed Q4_K/Q6_K layer (router + {len(groups)} expert groups + shared "
-                      f"expert via the reference moe_cpu), best of {reps}: {best:.3f} s"}
+    out = {"value": round(T / best, 1), "unit": "tokens/s", "cores": omp_threads(), "kind": "reference",
+           "sample": f"one {T}-token {label} layer ({'router + ' if with_router else ''}{len(groups)} expert groups "
+                     f"+ shared expert via the reference moe_cpu), best of {reps}: {best:.3f} s"}
+    out.update(host_cpu())
+    return out
 
 
 def event_ms(torch, stream, fn, reps):
@@ -229,23 +276,27 @@ def event_ms(torch, stream, fn, reps):
 
 
 def prefill_legs(torch, L, R, dev, stream, reps, with_cpu):
-    out = {}
-    # all-Q6_K, T = 2048, 4 layers, N(0,1) logits given (no router)
+    """Prefill: config 5 (all-Q6_K, 2048 tokens x 4 layers, N(0,1) logits
+    given) is the line's prefill value with its MFMA roofline; config 3 (512
+    Zipf-routed tokens through one Q4_K/Q6_K layer with the router) is
+    HBM-bound and reported against min(MFMA peak, AI x HBM peak)."""
+    # config 5: all-Q6_K, T = 2048, 4 layers, N(0,1) logits given (no router)
     T, NL, seed = 2048, 4, 4
     desc = R.table_desc(NL, q6=(1, 1, 1), sh_q6=(1, 1, 1))
     t = L.roaster_table_create(C.byref(desc))
     assert t, R.last_error()
     try:
         R.check(L.roaster_table_synth(t, seed, None), "table_synth")
-        X = torch.from_numpy(bf16_round(np.stack([R.synth_normal(seed, R.synth_stream(0, i, 5), H)
-                                                  for i in range(T)]))).to(dev)
+        Xh5 = bf16_round(np.stack([R.synth_normal(seed, R.synth_stream(0, i, 5), H) for i in range(T)]))
+        X = torch.from_numpy(Xh5).to(dev)
         lg = [torch.from_numpy(np.stack([R.synth_normal(seed, R.synth_stream(l, i, 7), E) for i in range(T)])).to(dev)
               for l in range(NL)]
         Y = torch.empty_like(X)
         cnt = torch.empty((NL, E), dtype=torch.int32, device=dev)
+        ids0 = torch.empty((T, 8), dtype=torch.int32, device=dev)
         torch.cuda.synchronize()
-        opts = [R.RoasterPrefillOpts(R.PREC_F16, lg[l].data_ptr(), None, None, None, None, cnt[l].data_ptr())
-                for l in range(NL)]
+        opts = [R.RoasterPrefillOpts(R.PREC_F16, lg[l].data_ptr(), None, None, ids0.data_ptr() if l == 0 else None,
+                                     None, cnt[l].data_ptr()) for l in range(NL)]
 
         def run():
             for l in range(NL):
@@ -260,19 +311,35 @@ def prefill_legs(torch, L, R, dev, stream, reps, with_cpu):
         counts = cnt.cpu().numpy()
         rows = int(counts.sum()) + NL * T                     # routed rows + shared rows
         flops = rows * FFN_FLOPS_PER_ROW
-        nbytes = NL * ((int((counts > 0).sum(axis=1).mean()) + 1) * EXPERT_BYTES_Q6) + NL * (T * H * 4 * 2 + T * E * 4)
+        # algorithmic bytes: each hit expert once + shared, X read (f32) and Y written (f32), logits read
+        nbytes = sum(((int((counts[l] > 0).sum()) + 1) * EXPERT_BYTES_Q6) for l in range(NL)) \
+            + NL * (T * H * 4 * 2 + T * E * 4)
         tf = flops / (ms * 1e-3) / 1e12
-        out["all_q6k_2048x4"] = {
-            "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_pass": round(ms, 4), "layers": NL,
-            "ms_per_layer": round(ms / NL, 4), "precision": "fp16 operands (row-scaled), fp32 accumulate",
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        ai = flops / nbytes
+        tok_s = T / (ms * 1e-3)
+        out = {
+            "metric": "MoE-FFN prefill tok/s (all-Q6_K experts, 2048 tokens x 4 layers, one MI355X)",
+            "value": round(tok_s, 1), "unit": "tokens/s", "tokens_per_s": round(tok_s, 1), "tok_s": round(tok_s, 1),
+            "higher_is_better": True, "ms_per_pass": round(ms, 4), "layers": NL, "ms_per_layer": round(ms / NL, 4),
+            "dtype": "fp16 MFMA operands (activations row-scaled by powers of two), fp32 accumulation",
+            "config": {"workload": "all-Q6_K MoE prefill, 2048 tokens x 4 layers, logits ~ N(0,1) given, seed 4",
+                       "hidden": H, "inter": I, "experts": E, "top_k": 8, "shared_experts": 1},
             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "traffic": None,
-                         "kernel": "whole prefill block (7 kernels per layer)",
-                         "algorithmic_flops_per_layer": int(flops // NL)},
-            "hbm_GBps_algorithmic": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+                         "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "traffic": profiled_traffic("prefill_q6_2048_layer"),
+                         "kernel": "whole prefill block (6 kernels per layer)",
+                         "algorithmic_flops_per_layer": int(flops // NL),
+                         "algorithmic_bytes_per_layer": int(nbytes // NL), "arithmetic_intensity": round(ai, 1),
+                         "frac_of_min_peak_ai_bw": round(tf / min(MFMA_PEAK_TFLOPS, ai * HBM_PEAK_GBS / 1000), 4)},
+            "hbm_GBps_algorithmic": round(gbs, 1)}
+        if with_cpu:
+            cb = cpu_baseline_prefill(t, desc, seed, Xh5, ids0.cpu().numpy(), layer=0, with_router=False,
+                                      label="all-Q6_K (logits given)")
+            if cb:
+                out["cpu_baseline"] = cb
     finally:
         L.roaster_table_destroy(t)
-    # Q4_K/Q6_K, T = 512, router + Zipf bias, one layer
+    # config 3: Q4_K/Q6_K, T = 512, router + Zipf bias, one layer
     T, seed = 512, 2
     desc = R.table_desc(1)
     t = L.roaster_table_create(C.byref(desc))
@@ -296,15 +363,127 @@ def prefill_legs(torch, L, R, dev, stream, reps, with_cpu):
         R.check(L.roaster_sync(), "prefill warmup")
         ms = event_ms(torch, stream, run3, reps)
         R.check(L.roaster_sync(), "prefill")
+        idh = ids.cpu().numpy()
+        n_hit = len(set(idh.ravel().tolist()))
         flops = 9 * T * FFN_FLOPS_PER_ROW + T * (E + 1) * H * 2
+        nbytes = (n_hit + 1) * EXPERT_BYTES + ROUTER_BYTES + 2 * T * H * 4
+        ai = flops / nbytes
+        roof_tf = min(MFMA_PEAK_TFLOPS, ai * HBM_PEAK_GBS / 1000)
         tf = flops / (ms * 1e-3) / 1e12
+        gbs = nbytes / (ms * 1e-3) / 1e9
         leg = {"tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_layer": round(ms, 4),
-               "achieved_TFLOPs": round(tf, 2), "frac_mfma_peak": round(tf / MFMA_PEAK_TFLOPS, 4)}
+               "config": {"workload": "Q4_K/Q6_K MoE prefill, 512 tokens x 1 layer, router + Zipf(1.1) expert bias, "
+                                      "seed 2", "experts_hit": n_hit},
+               "roofline": {"bound": "hbm" if roof_tf < MFMA_PEAK_TFLOPS else "mfma", "achieved": round(gbs, 1),
+                            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(tf / roof_tf, 4),
+                            "traffic": profiled_traffic("prefill_zipf_512_layer"),
+                            "algorithmic_bytes": int(nbytes), "algorithmic_flops": int(flops),
+                            "arithmetic_intensity": round(ai, 1), "achieved_TFLOPs": round(tf, 2),
+                            "roof_TFLOPs": round(roof_tf, 1), "frac_mfma_peak": round(tf / MFMA_PEAK_TFLOPS, 4)}}
         if with_cpu:
-            cb = cpu_baseline_prefill(t, desc, seed, Xh, zipf_bias(E, seed), ids.cpu().numpy())
+            cb = cpu_baseline_prefill(t, desc, seed, Xh, idh, layer=0, with_router=True, label="Zipf-routed Q4_K/Q6_K")
             if cb:
                 leg["cpu_baseline"] = cb
         out["zipf_512x1"] = leg
+    finally:
+        L.roaster_table_destroy(t)
+    return out
+
+
+def config1_leg(torch, L, R, dev, stream, with_cpu):
+    """Config 1: one Q4_K [512 x 2048] dequant-matvec (seed 0) through
+    roaster_matvec_q on device buffers.  Back-to-back calls on one copy give
+    the cache-resident latency; calls rotating over 512 copies (302 MB, beyond
+    the 256 MB Infinity Cache) give the HBM rate.  The reference's
+    matvec_q4_cpu (kernels.c:407-432, one thread as its OpenMP threshold keeps
+    it) is timed beside it."""
+    rows, cols, ncopy = 512, 2048, 512
+    W = R.synth_q4k(0, R.synth_stream(0, 0, 0), rows * cols // 256)
+    x = R.synth_normal(0, R.synth_stream(0, 0, 5), cols)
+    dW = torch.from_numpy(np.tile(W, ncopy)).to(dev)
+    dx = torch.from_numpy(x).to(dev)
+    dy = torch.empty(rows, dtype=torch.float32, device=dev)
+    mb = W.nbytes
+
+    def one(i):
+        rc = L.roaster_matvec_q(dW.data_ptr() + i * mb, 0, dx.data_ptr(), dy.data_ptr(), rows, cols, 1)
+        if rc:
+            raise RuntimeError(R.last_error())
+
+    one(0)
+    R.check(L.roaster_sync(), "config1 warmup")
+    hot_ms = event_ms(torch, stream, lambda: one(0), 200)
+    it = iter(range(10 ** 9))
+    rot_ms = event_ms(torch, stream, lambda: one(next(it) % ncopy), 2 * ncopy)
+    # the same 512 copies as one [262144 x 2048] matrix in one launch: the kernel's streaming rate
+    dY = torch.empty(rows * ncopy, dtype=torch.float32, device=dev)
+    big = lambda: R.check(L.roaster_matvec_q(dW.data_ptr(), 0, dx.data_ptr(), dY.data_ptr(), rows * ncopy, cols, 1))
+    one_ms = event_ms(torch, stream, big, 20)
+    R.check(L.roaster_sync(), "config1")
+    nbytes = mb + cols * 4 + rows * 4
+    gbs = nbytes / (rot_ms * 1e-3) / 1e9
+    gbs_one = ncopy * mb / (one_ms * 1e-3) / 1e9
+    out = {"workload": "Q4_K [512 x 2048] matvec, seed 0", "algorithmic_bytes": int(nbytes),
+           "us_per_call_cache_resident": round(hot_ms * 1e3, 3), "us_per_call_rotating_512_copies": round(rot_ms * 1e3, 3),
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                        "kernel": "dense_mv_kernel (one launch per matvec, 512 rotated copies)"},
+           "streaming_512_copies_one_launch": {"us": round(one_ms * 1e3, 1), "GBps": round(gbs_one, 1),
+                                               "frac_hbm_peak": round(gbs_one / HBM_PEAK_GBS, 4)}}
+    if with_cpu:
+        from oracle import oracle as O
+        if O.ref_available():
+            Rf = O.ref()
+            y = np.empty(rows, np.float32)
+            n = 0
+            t0 = time.perf_counter()
+            while time.perf_counter() - t0 < 1.0:
+                Rf.ref_matvec_q4_cpu(W.ctypes.data, x.ctypes.data, y.ctypes.data, rows, cols)
+                n += 1
+            dt = (time.perf_counter() - t0) / n
+            cb = {"value": round(1e6 * dt, 2), "unit": "us per matvec", "cores": 1, "kind": "reference",
+                  "sample": f"{n} calls of matvec_q4_cpu on the same matrix (cache-resident) over 1 s",
+                  "GBps": round(nbytes / dt / 1e9, 2)}
+            cb.update(host_cpu())
+            out["cpu_baseline"] = cb
+    return out
+
+
+def config2_leg(torch, L, R, dev, stream, with_cpu):
+    """Config 2: one decode MoE block (router -> top-8 -> 8 + 1 experts ->
+    combine, seed 1) through roaster_moe_decode.  Back-to-back calls give the
+    per-block device time; single calls with a host sync around each give the
+    isolated latency.  The reference's CPU block (model.c:1059-1146 over its
+    kernels.c routines, one thread) is timed beside it."""
+    seed = 1
+    desc = R.table_desc(1)
+    t = L.roaster_table_create(C.byref(desc))
+    assert t, R.last_error()
+    try:
+        R.check(L.roaster_table_synth(t, seed, None), "table_synth")
+        x = torch.from_numpy(R.synth_normal(seed, R.synth_stream(0, 0, 5), H)).to(dev)
+        y = torch.empty_like(x)
+        torch.cuda.synchronize()
+
+        def run():
+            rc = L.roaster_moe_decode(t, 0, x.data_ptr(), 1, y.data_ptr(), None)
+            if rc:
+                raise RuntimeError(R.last_error())
+
+        run()
+        R.check(L.roaster_sync(), "config2 warmup")
+        dev_ms = event_ms(torch, stream, run, 200)
+        lat = []
+        for _ in range(50):
+            t0 = time.perf_counter()
+            run()
+            R.check(L.roaster_sync(), "config2")
+            lat.append(time.perf_counter() - t0)
+        out = {"workload": "one decode MoE block, 1 token, hidden 2048, 256 experts top-8 + shared, seed 1",
+               "us_per_block_device": round(dev_ms * 1e3, 2), "us_per_block_isolated_median": round(
+                   float(np.median(lat)) * 1e6, 1), "algorithmic_bytes": ROUTER_BYTES + 9 * EXPERT_BYTES}
+        if with_cpu:
+            out["cpu_baseline"] = cpu_baseline_decode(seed, 200, t, n_layers=1, x_stream=0)
     finally:
         L.roaster_table_destroy(t)
     return out
@@ -336,24 +515,15 @@ def dense_leg(torch, L, R, dev, stream):
     return out
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(json.dumps({"error": "--gpus must be 1: the MoE-FFN hot path is measured on one MI355X "
-                                   "(one GPU's share of an expert-parallel layout, at its real shape)"}))
-        sys.exit(2)
-    import torch
-    import roaster_amd as R
-
-    L = R.lib()
-    dev = torch.device("cuda:0")
-    torch.cuda.init()
+def decode_legs(args, torch, L, R, dev, stream):
+    """The headline: batch-`args.batch` decode through the 40-layer stack (host
+    wall clock over --steps steps, device time from HIP events), batch 8 and
+    the reference CPU decode beside it."""
     seed = 3
     desc = R.table_desc(N_LAYERS)
     t = L.roaster_table_create(C.byref(desc))
     assert t, R.last_error()
     R.check(L.roaster_table_synth(t, seed, None), "table_synth")
-    stream = torch.cuda.ExternalStream(L.roaster_stream(), device=dev)
 
     def stack_setup(B):
         h0 = torch.from_numpy(np.stack([R.synth_normal(seed, R.synth_stream(0, b, 5), H) for b in range(B)])).to(dev)
@@ -404,7 +574,7 @@ def main():
                    "experts": E, "top_k": 8, "shared_experts": 1, "layers": N_LAYERS,
                    "gate_up": "Q4_K", "down": "Q6_K", "resident_table_bytes": int(L.roaster_table_bytes(t))},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("decode_b%d_step" % B),
                      "kernel": "decode stack (router, gate/up, down kernels x 40 layers)",
                      "kernel_ms": round(kern_ms, 5), "algorithmic_bytes_per_launch": int(nbytes)},
     }
@@ -422,9 +592,34 @@ def main():
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(seed, args.cpu_tokens, t)
     L.roaster_table_destroy(t)
-    if not args.no_prefill:
+    return line
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "--gpus must be 1: the MoE-FFN hot path is measured on one MI355X "
+                                   "(one GPU's share of an expert-parallel layout, at its real shape)"}))
+        sys.exit(2)
+    import torch
+    import roaster_amd as R
+
+    L = R.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.init()
+    stream = torch.cuda.ExternalStream(L.roaster_stream(), device=dev)
+    legs = set(args.legs.split(","))
+    line = {"metric": "partial run: legs %s" % sorted(legs)}
+    if "decode" in legs:
+        line = decode_legs(args, torch, L, R, dev, stream)
+    if "prefill" in legs and not args.no_prefill:
         line["prefill"] = prefill_legs(torch, L, R, dev, stream, args.prefill_reps, not args.no_cpu)
-    line["dense"] = dense_leg(torch, L, R, dev, stream)
+    if "config1" in legs:
+        line["config1"] = config1_leg(torch, L, R, dev, stream, not args.no_cpu)
+    if "config2" in legs:
+        line["config2"] = config2_leg(torch, L, R, dev, stream, not args.no_cpu)
+    if "dense" in legs:
+        line["dense"] = dense_leg(torch, L, R, dev, stream)
     print(json.dumps(line), flush=True)
 
 
