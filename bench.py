@@ -70,6 +70,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill legs")
     ap.add_argument("--cpu-tokens", type=int, default=160)
     ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--three-kernel", action="store_true",
+                    help="decode one token's layers with three launches each instead of one (for comparison)")
     ap.add_argument("--legs", default="decode,prefill,config1,config2,dense",
                     help="comma-separated legs to run (the decode headline always runs unless omitted here)")
     return ap.parse_args()
@@ -575,7 +577,9 @@ def decode_legs(args, torch, L, R, dev, stream):
                    "gate_up": "Q4_K", "down": "Q6_K", "resident_table_bytes": int(L.roaster_table_bytes(t))},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("decode_b%d_step" % B),
-                     "kernel": "decode stack (router, gate/up, down kernels x 40 layers)",
+                     "kernel": "decode stack: %s" % ("dec_layer1_kernel, one launch per layer"
+                                                     if B == 1 and L.roaster_decode_fused_layer(-1)
+                                                     else "router, gate/up and down kernels per layer"),
                      "kernel_ms": round(kern_ms, 5), "algorithmic_bytes_per_launch": int(nbytes)},
     }
     if B == 1:
@@ -608,6 +612,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.init()
     stream = torch.cuda.ExternalStream(L.roaster_stream(), device=dev)
+    if args.three_kernel:
+        L.roaster_decode_fused_layer(0)
     legs = set(args.legs.split(","))
     line = {"metric": "partial run: legs %s" % sorted(legs)}
     if "decode" in legs:

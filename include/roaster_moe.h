@@ -160,6 +160,20 @@ int roaster_moe_decode(RoasterTable *t, int layer, const float *x, int B, float 
 int roaster_moe_decode_stack(RoasterTable *t, float *h, int B, int layer0, int n_layers,
                              const float *norm_w, float eps, int *ids_out, float *w_out);
 
+/* Decode of one token (B = 1) runs each layer as one launch (router, top-8,
+ * experts and combine in 256 workgroups that exchange values through memory)
+ * wherever the shapes allow it (experts a multiple of 32 up to 256, hidden up
+ * to 2048, inter up to 1024, a device with at least 256 CUs); otherwise, and
+ * for B > 1, as three launches.  Both give bit-identical results.
+ * roaster_decode_fused_layer: 1 = one launch where possible (default), 0 =
+ * always three, -1 = query; returns the mode in force. */
+int roaster_decode_fused_layer(int enable);
+/* Polls a one-launch layer's wait makes before it gives up (sets error bit 2,
+ * reported by roaster_sync as ROASTER_EDEVICE, and the launch ends with
+ * unusable outputs); 0 = query.  Default 2^20 (about a second); tests set it
+ * tiny to exercise that path. */
+unsigned roaster_decode_spin_limit(unsigned polls);
+
 /* No counterpart in the reference: roaster_moe_decode_stack for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  Same arguments, kernels and

@@ -133,6 +133,8 @@ _SIG = {
     "roaster_moe_decode": (C.c_int, [_P, C.c_int, _P, C.c_int, _P, C.POINTER(RoasterDecodeIO)]),
     "roaster_moe_decode_stack": (C.c_int, [_P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_float, _P, _P]),
     "roaster_moe_decode_stack_noalloc": (C.c_int, [_P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_float, _P, _P]),
+    "roaster_decode_fused_layer": (C.c_int, [C.c_int]),
+    "roaster_decode_spin_limit": (C.c_uint, [C.c_uint]),
     "roaster_moe_prefill": (C.c_int, [_P, C.c_int, _P, C.c_int, _P, C.POINTER(RoasterPrefillOpts)]),
 }
 

@@ -358,6 +358,7 @@ static int dec_scratch(DecArgs &A)
     A.sgate_raw = (float *)rt_scratch(SCR_E, B * 4);
     A.eh = (float *)rt_scratch(SCR_F, B * 9 * (size_t)A.I * 4);
     A.xn_g = (float *)rt_scratch(SCR_B, B * ((size_t)A.H + A.H / 16) * 4);
+    if (dec_layer1_ok(A.E, A.H, A.I, A.B) && !(A.xbuf = dec_xch_default(A.E, A.H, A.I))) return ROASTER_ENOMEM;
     return A.logits && A.sgate_raw && A.eh && A.xn_g ? 0 : ROASTER_ENOMEM;
 }
 
@@ -455,8 +456,10 @@ extern "C" int roaster_moe_decode_stack_noalloc(RoasterTable *t, float *h, int B
     DecArgs A;
     fill_table_args(A, t);
     const size_t E = (size_t)A.E, Bz = (size_t)B, H = (size_t)A.H, I = (size_t)A.I;
+    const bool one = dec_layer1_ok(A.E, A.H, A.I, B);
     const size_t o_plan = 256, o_log = o_plan + al256(sizeof(DecPlan)), o_sg = o_log + al256(Bz * E * 4),
-                 o_eh = o_sg + al256(Bz * 4), o_xn = o_eh + al256(Bz * 9 * I * 4), end = o_xn + al256(Bz * (H + H / 16) * 4);
+                 o_eh = o_sg + al256(Bz * 4), o_xn = o_eh + al256(Bz * 9 * I * 4), o_x = o_xn + al256(Bz * (H + H / 16) * 4),
+                 end = o_x + (one ? al256((size_t)XCH_U64(E, H, I) * 8) : 0);
     if (end > NOALLOC_BYTES)
         return rt_fail(ROASTER_EINVAL,
                        "roaster_moe_decode_stack_noalloc: %d tokens x hidden %zu x inter %zu x %zu experts need %zu "
@@ -478,6 +481,16 @@ extern "C" int roaster_moe_decode_stack_noalloc(RoasterTable *t, float *h, int B
     A.sgate_raw = (float *)(base + o_sg);
     A.eh = (float *)(base + o_eh);
     A.xn_g = (float *)(base + o_xn);
+    if (one) {
+        /* the exchange slots keep their own epoch counter; the array was
+         * zero-filled at load and is never cleared by the host, so it needs no
+         * allocation or memset here */
+        static DecXch xb[NOALLOC_MAX_DEV];
+        DecXch &X = xb[rt().device];
+        X.p = (uint64_t *)(base + o_x);
+        X.n = (size_t)XCH_U64(E, H, I);
+        A.xbuf = &X;
+    }
     return dec_launch(A);
 }
 

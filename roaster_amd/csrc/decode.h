@@ -71,12 +71,41 @@ struct DecArgs {
     const DecActive *ffn_ex;    /* [n] device */
     int ffn_n;
     float *ffn_out;             /* [n x H] or NULL */
+    /* one-launch layer (dec_layer1_kernel): exchange slots, u64 = (epoch << 32) | f32 bits */
+    uint64_t *xch;              /* [XCH_U64(E, H, I)] or NULL (then the three-kernel path runs) */
+    uint32_t epoch;             /* this launch's epoch (set per layer by the launch code) */
+    uint32_t spin;              /* polls before a wait gives up (set by the launch code) */
+    struct DecXch *xbuf;        /* host side: the buffer behind xch and its epoch counter, or NULL */
 };
+
+/* Exchange regions of the one-launch layer, in u64 slots: the E router
+ * logits, XCH_LGP slots apart (each written by one workgroup and read by all:
+ * one line each spreads the polling over memory channels), the shared
+ * expert's SiLU*up [I], each group's routed SiLU*up [8][I] and each group's
+ * routed down outputs [8][H]. */
+#define XCH_LGS(E) ((((E) + 1) + 7) & ~7)
+#define XCH_LGP 16                          /* logit slots 128 bytes apart (one per workgroup) */
+#define XCH_LG(E, H, I) 0
+#define XCH_EHS(E, H, I) (XCH_LGP * XCH_LGS(E))
+#define XCH_EHX(E, H, I) (XCH_EHS(E, H, I) + (I))
+#define XCH_DX(E, H, I) (XCH_EHX(E, H, I) + 8 * (I))
+#define XCH_U64(E, H, I) (XCH_DX(E, H, I) + 8 * (H))
+
+/* Exchange buffer of the one-launch layer: the slots and the last epoch
+ * written into them.  Epochs grow by one per launch; before the 32-bit
+ * epoch would wrap, the slots are cleared (by a fill kernel) and epochs
+ * start again at 1, so a slot never holds a later launch's epoch. */
+struct DecXch { uint64_t *p; size_t n; uint32_t epoch; };
 
 /* All layers of A: 3 kernels per layer.  A.plan_g and A.err may be set by the
  * caller (device memory of sizeof(DecPlan) and one int); when either is NULL
  * the library's own scratch and control words are used. */
 int dec_launch(DecArgs &A);
 int dec_ffn_launch(DecArgs &A);      /* kernel_ffn_fused: gate/up + down kernels */
+/* Whether one token's layers can run as one launch each (dec_layer1_kernel)
+ * for these shapes on this device. */
+bool dec_layer1_ok(int E, int H, int I, int B);
+/* The library's exchange buffer (allocated and cleared on first use). */
+DecXch *dec_xch_default(int E, int H, int I);
 
 #endif

@@ -1014,6 +1014,503 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_down_kernel(DecArgs A, i
     PHASE_TS(2, 3);
 }
 
+/* ---- one launch per layer for one token --------------------------------------
+ * dec_layer1_kernel runs a whole layer of one token (model.c:1059-1146; in
+ * stack mode with the carry h += MoE(RMSNorm(h)), model.c:1352-1358) as one
+ * launch of 256 workgroups in 8 groups of 32.  Workgroup b is in group b % 8
+ * (the dispatcher places it on XCD b % 8) at index b / 8.  Group k serves
+ * routed slot k, the k-th selected expert:
+ *   1. every workgroup normalises h (the arithmetic of block_norm_tail),
+ *      computes the shared-gate logit itself and dots router row b (b < E)
+ *      and its pairs of the shared expert's gate/up rows, and publishes the
+ *      logit and the shared SiLU*up values;
+ *   2. the E logits are gathered (read directly when the caller gives them)
+ *      and ranked: the top 8 by the composite key of topk8_fast (larger
+ *      logit, then lower index; NaN and -inf never selected), weights by
+ *      topk_finish;
+ *   3. the slot's expert: this workgroup's 1/32 of its gate/up row pairs and
+ *      of its down rows are loaded together; SiLU*up is published within the
+ *      group and gathered; the down rows are dotted and published;
+ *   4. workgroup b owns output rows [b H/256, (b + 1) H/256): it gathers the
+ *      shared SiLU*up, dots the shared expert's down rows for them (loaded in
+ *      step 1), gathers the eight slots' down outputs for them and combines
+ *      y = sum_{k=0..7} w_k d_k + sigmoid(s) d_shared in that order
+ *      (model.c:1139-1144).
+ * Exchanges are relaxed agent-scope 64-bit stores and loads of (epoch, value)
+ * slots: a slot is ready once it carries this launch's epoch, so neither
+ * fences nor cache maintenance are needed and nothing is cleared between
+ * launches.  No workgroup writes h before every workgroup has read it: an
+ * owner's rows need every group's down outputs, each group's down outputs
+ * need all 32 of its SiLU*up values, and those need the ranking, which comes
+ * after each workgroup's h (through the logits when the router runs; with
+ * given logits through the SiLU*up values, which need the normalised h).
+ * Every wait is bounded (A.spin polls); a wait that gives up sets error bit
+ * 2 and the workgroup waits for nothing else in this launch, so the launch
+ * always ends.  Sums, dot lane layouts, reductions, softmax and combine are
+ * those of the three-kernel path, so results are bit-identical to it.
+ * NPG / ND: gate/up pairs and down tasks per wave, fixed at compile time for
+ * the common shapes (then every load of a phase is issued unconditionally
+ * and each use waits for its own loads only), 0 = from the shapes at run
+ * time. */
+#define K1_T 512
+#define K1_W (K1_T / 64)
+#define K1_G 8
+#define K1_GW 32
+#define K1_NWG (K1_G * K1_GW)
+#define K1_SPIN (1u << 20)
+#define K1_MAXH 2048
+#define K1_MAXI 1024
+#define K1_MAXPG (K1_MAXI / K1_GW / K1_W)               /* gate/up pairs per wave */
+#define K1_MAXD 4                                        /* down tasks per wave */
+
+__device__ __forceinline__ void xch_put(uint64_t *p, float v, uint32_t ep)
+{
+    __hip_atomic_store(p, ((uint64_t)ep << 32) | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* The value of slot p once it carries epoch ep, polling at most spin times
+ * (dead: stop waiting). */
+__device__ __forceinline__ float xch_get(const uint64_t *p, uint32_t ep, int &dead, uint32_t spin)
+{
+    uint64_t v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned it = 0;
+    while ((uint32_t)(v >> 32) != ep && !dead) {
+        if (++it > spin) {
+            dead = 1;
+            break;
+        }
+        v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return __builtin_bit_cast(float, (uint32_t)v);
+}
+
+/* q_load with the block type chosen at run time (the type comes from the
+ * layer descriptor, so the branch is wave-uniform). */
+__device__ __forceinline__ QChunk q_load_t(int q6, const uint8_t *m, size_t row, int nb, int lb, int c)
+{
+    const int lbc = lb < nb ? lb : nb - 1;
+    return q6 ? q_load<true>(m + (row * nb + lbc) * RQ6K_BYTES, c) : q_load<false>(m + (row * nb + lbc) * RQ4K_BYTES, c);
+}
+
+__device__ __forceinline__ int q_run_a_t(int q6, int c) { return q6 ? q_run_a<true>(c) : q_run_a<false>(c); }
+
+/* silu(gate_j . x) * (up_j . x) from the lane's chunks of one gate/up row
+ * pair, x and its run sums in LDS (gu_row's arithmetic for one token). */
+__device__ __forceinline__ float k1_gu_pair(int g6, int u6, const QChunk2 &ch, const float *xn, const float *xsum,
+                                            bool swz, int nb)
+{
+    const int lane = threadIdx.x & 63, c = lane & 7, lb = lane >> 3;
+    float pg = 0.0f, pu = 0.0f;
+    if (lb < nb) {
+        const int ga = lb * RQK + q_run_a_t(g6, c), gb = ga + (g6 ? 64 : 32);
+        const int ua = lb * RQK + q_run_a_t(u6, c), ub = ua + (u6 ? 64 : 32);
+        float4 x0[4], x1[4];
+        load_x16(xn, ga, x0, swz);
+        load_x16(xn, gb, x1, swz);
+        pg = g6 ? q_chunk_dot_r<true>(ch.g, c, x0, x1, xsum[ga >> 4], xsum[gb >> 4])
+                : q_chunk_dot_r<false>(ch.g, c, x0, x1, xsum[ga >> 4], xsum[gb >> 4]);
+        load_x16(xn, ua, x0, swz);
+        load_x16(xn, ub, x1, swz);
+        pu = u6 ? q_chunk_dot_r<true>(ch.u, c, x0, x1, xsum[ua >> 4], xsum[ub >> 4])
+                : q_chunk_dot_r<false>(ch.u, c, x0, x1, xsum[ua >> 4], xsum[ub >> 4]);
+    }
+    pg = group_sum<64>(pg);
+    pu = group_sum<64>(pu);
+    return silu_mul(pg, pu);
+}
+
+/* One down row's lane partial against a SiLU*up vector in LDS (plain layout)
+ * and its run sums (down_one_token's arithmetic), reduced over the row's
+ * lpr lanes. */
+__device__ __forceinline__ float k1_down_row(int d6, const QChunk &ch, const float *eh, const float *ehs, bool live,
+                                             int lpr)
+{
+    const int lane = threadIdx.x & 63, lr = lane % lpr, c = lr & 7, lb = lr >> 3;
+    float part = 0.0f;
+    if (live) {
+        const int ca = lb * RQK + q_run_a_t(d6, c), cb = ca + (d6 ? 64 : 32);
+        part = d6 ? q_chunk_dot<true>(ch, c, eh + ca, eh + cb, ehs[ca >> 4], ehs[cb >> 4])
+                  : q_chunk_dot<false>(ch, c, eh + ca, eh + cb, ehs[ca >> 4], ehs[cb >> 4]);
+    }
+    return group_sum_w(part, lpr);
+}
+
+/* Router-row dot of one token (router_body's arithmetic): lane partials over
+ * its 8 float4 of the row, then the wave sum. */
+__device__ __forceinline__ float k1_row_dot(const float4 (&w)[8], const float4 *x4, int H, bool swz)
+{
+    const int lane = threadIdx.x & 63;
+    float acc = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        const int c0 = 4 * lane + 256 * m;
+        if (c0 < H) {
+            const float4 x = x4[xpos(c0 >> 2, swz)];
+            acc = fmaf(w[m].x, x.x, acc);
+            acc = fmaf(w[m].y, x.y, acc);
+            acc = fmaf(w[m].z, x.z, acc);
+            acc = fmaf(w[m].w, x.w, acc);
+        }
+    }
+    return group_sum<64>(acc);
+}
+
+#define K1_SYNC_DEAD()          \
+    do {                        \
+        if (dead) s_dead = 1;   \
+        __syncthreads();        \
+        dead = s_dead;          \
+    } while (0)
+
+template <int NPG, int ND, int TY>
+__device__ __forceinline__ void layer1_body(const DecArgs &A, int l)
+{
+    __shared__ __align__(16) float xn[K1_MAXH];
+    __shared__ float xsum[K1_MAXH / 16];
+    __shared__ __align__(16) float ehk[K1_MAXI];
+    __shared__ float ehks[K1_MAXI / 16];
+    __shared__ __align__(16) float ehsh[K1_MAXI];
+    __shared__ float ehshs[K1_MAXI / 16];
+    __shared__ float lg_s[256];
+    __shared__ __align__(16) unsigned long long ck_s[256];
+    __shared__ int slot_s[RTOPK];
+    __shared__ uint32_t gmax_s[8];
+    __shared__ int ncand_s;
+    __shared__ __align__(16) unsigned long long cand_s[64];
+    __shared__ int ids_s[RTOPK];
+    __shared__ float w_s[RTOPK + 1];
+    __shared__ float red_s[4];
+    __shared__ float sg_s;
+    __shared__ float dk_s[RTOPK][K1_MAXH / 256];
+    __shared__ float dsh_s[K1_MAXH / 256];
+    __shared__ int s_dead, s_err;
+
+    const int H = A.H, I = A.I, E = A.E, HU = H / 4, nbh = H / RQK, nbi = I / RQK;
+    const int tid = threadIdx.x, lane = tid & 63, wv = wave_id(), c = lane & 7, lb = lane >> 3;
+    const int grp = blockIdx.x % K1_G, gi = blockIdx.x / K1_G, gw = blockIdx.x;
+    const uint32_t ep = A.epoch;
+    const DecLayer L = A.layers[l];
+    /* matrix types: from the descriptor, or fixed by TY (bit k: routed gate,
+     * up, down, shared gate, up, down is Q6_K) so that every load of a phase
+     * is straight-line code and each use waits for its own loads only */
+    const int g6 = TY < 0 ? L.q6[0] : (TY & 1), u6 = TY < 0 ? L.q6[1] : (TY >> 1) & 1;
+    const int d6 = TY < 0 ? L.q6[2] : (TY >> 2) & 1, sg6 = TY < 0 ? L.sq6[0] : (TY >> 3) & 1;
+    const int su6 = TY < 0 ? L.sq6[1] : (TY >> 4) & 1, sd6 = TY < 0 ? L.sq6[2] : (TY >> 5) & 1;
+    const bool swz = A.xswz;
+    uint64_t *xlg = A.xch + XCH_LG(E, H, I);
+    uint64_t *xehs = A.xch + XCH_EHS(E, H, I);
+    uint64_t *xehx = A.xch + XCH_EHX(E, H, I) + (size_t)grp * I;
+    uint64_t *xdx = A.xch + XCH_DX(E, H, I);
+#ifdef ROASTER_PHASE_TS
+    unsigned long long tsv[12];
+#define K1_TS(i) asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(tsv[i]) : : "memory")
+#else
+#define K1_TS(i) ((void)0)
+#endif
+    K1_TS(0);
+    if (tid == 0) {
+        s_dead = 0;
+        s_err = 0;
+    }
+
+    /* ---- 1. loads that need nothing.  h (with the norm weights and the
+     * owned rows' residual) first; then, by wave: 0 router row gw, 1 the
+     * shared-gate vector, 2 .. 1 + SP the shared gate/up pairs, the last nsd
+     * waves the owned rows of the shared down matrix.  h is stored to LDS in
+     * each branch after its loads, so the store waits for h only (a wave's
+     * loads complete in order); a distinct marker after each store keeps the
+     * compiler from merging the stores past the join. */
+    const float4 hq = ((const float4 *)A.h)[min(tid, HU - 1)];
+    /* error bit 2 from an earlier launch that gave up: wait for nothing (read
+     * after h is requested; first needed at the first wait) */
+    int dead = (gld_u32(A.err) & 2u) != 0;
+    const float *nw = A.do_norm && A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * H : NULL;
+    const float4 wq = nw ? ((const float4 *)nw)[xpos(min(tid, HU - 1), swz)] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    const int RO = H / 256;                                  /* output rows owned */
+    const float hv = A.y ? 0.0f : A.h[gw * RO + min(tid, RO - 1)];
+    const int SP = I / 256;                                  /* shared gate/up pairs of this workgroup */
+    const int lpr = lanes_per_row(nbi), rpw = 64 / lpr, rw_ = lane / lpr, lr = lane % lpr, lbd = lr >> 3;
+    const int nsd = (RO + rpw - 1) / rpw;                    /* shared down tasks */
+    const int sdt = wv - (K1_W - nsd);
+    const bool rrow = gw < E && !A.logits_in;                /* this workgroup dots router row gw */
+    float4 rw[8];
+    QChunk2 shc;
+    QChunk sdc;
+#define K1_STORE_H(tag)                                                       \
+    do {                                                                      \
+        ((float4 *)xn)[xpos(min(tid, HU - 1), swz)] = hq;                     \
+        asm volatile("; h stored, " tag);                                     \
+    } while (0)
+    if (wv == 0 && rrow) {
+#pragma unroll
+        for (int m = 0; m < 8; m++) rw[m] = gld_f4(L.router + (size_t)gw * H + min(4 * lane + 256 * m, H - 4));
+        K1_STORE_H("router row");
+    } else if (wv == 1) {
+#pragma unroll
+        for (int m = 0; m < 8; m++) rw[m] = gld_f4(L.gate_inp + min(4 * lane + 256 * m, H - 4));
+        K1_STORE_H("shared-gate vector");
+    } else if (wv >= 2 && wv < 2 + SP) {
+        const size_t j = (size_t)gw * SP + (wv - 2);
+        shc.g = q_load_t(sg6, L.sgate, j, nbh, lb, c);
+        shc.u = q_load_t(su6, L.sup, j, nbh, lb, c);
+        K1_STORE_H("shared gate/up");
+    } else if (sdt >= 0) {
+        sdc = q_load_t(sd6, L.sdown, (size_t)min(gw * RO + sdt * rpw + rw_, H - 1), nbi, lbd, lr & 7);
+        K1_STORE_H("shared down");
+    } else {
+        K1_STORE_H("no rows");
+    }
+#undef K1_STORE_H
+
+    /* ---- 2. normalised input (block_norm_tail for one token) ------------- */
+    __syncthreads();
+    float4 *x4 = (float4 *)xn;
+    if (A.do_norm) {
+        if (tid < 256) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int u = tid + k * 256;
+                if (u < HU) {
+                    const float4 v = x4[u];
+                    ss = fmaf(v.x, v.x, ss);
+                    ss = fmaf(v.y, v.y, ss);
+                    ss = fmaf(v.z, v.z, ss);
+                    ss = fmaf(v.w, v.w, ss);
+                }
+            }
+            ss = group_sum<64>(ss);
+            if (lane == 0) red_s[wv] = ss;
+        }
+        __syncthreads();
+        float s2 = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) s2 += red_s[w];
+        const float inv = 1.0f / sqrtf(s2 / (float)H + A.eps);
+        if (tid < HU) {
+            float4 v = x4[tid];
+            v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
+            if (nw) { v.x *= wq.x; v.y *= wq.y; v.z *= wq.z; v.w *= wq.w; }
+            x4[tid] = v;
+        }
+        __syncthreads();
+    }
+    for (int r = tid; r < H / 16; r += K1_T) {
+        const float4 a = x4[xpos(4 * r, swz)], b = x4[xpos(4 * r + 1, swz)];
+        const float4 cc = x4[xpos(4 * r + 2, swz)], d = x4[xpos(4 * r + 3, swz)];
+        xsum[r] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)) +
+                  (((cc.x + cc.y) + (cc.z + cc.w)) + ((d.x + d.y) + (d.z + d.w)));
+    }
+    __syncthreads();
+    K1_TS(1);
+
+    /* ---- 3. router logit, shared-gate logit, shared SiLU*up -------------- */
+    if (wv == 0 && rrow) {
+        const float s = k1_row_dot(rw, x4, H, swz);
+        if (lane == 0) {
+            xch_put(xlg + (size_t)gw * XCH_LGP, s, ep);
+            A.logits[gw] = s;
+        }
+    } else if (wv == 1) {
+        const float s = k1_row_dot(rw, x4, H, swz);
+        if (lane == 0) sg_s = s;
+    } else if (wv >= 2 && wv < 2 + SP) {
+        const float eh = k1_gu_pair(sg6, su6, shc, xn, xsum, swz, nbh);
+        if (lane == 0) xch_put(xehs + (size_t)gw * SP + (wv - 2), eh, ep);
+    }
+    K1_TS(2);
+
+    /* ---- 4. the logits; top-8 by rank ------------------------------------ */
+    if (tid < E) lg_s[tid] = A.logits_in ? A.logits_in[tid] : xch_get(xlg + (size_t)tid * XCH_LGP, ep, dead, A.spin);
+    if (tid < RTOPK) slot_s[tid] = -1;
+    if (tid == 0) ncand_s = 0;
+    K1_SYNC_DEAD();
+    K1_TS(3);
+    /* Every selected key is at least T = the smallest of the 8 maxima of
+     * aligned groups of 32 keys (those maxima are 8 keys >= T), so only the
+     * candidates key >= T (typically 15-25) are ranked; with more than 64 of
+     * them (ties at T, or a group without a selectable logit) every key is
+     * ranked against all 256.  Either way slot r holds the key with r larger
+     * composite keys: the order of topk8_fast. */
+    uint32_t key = 0u;
+    if (tid < 256) {
+        key = tid < E ? logit_key(lg_s[tid]) : 0u;
+        uint32_t g = key;
+        g = max(g, (uint32_t)dpp_i<DPP_XOR1>((int)g));
+        g = max(g, (uint32_t)dpp_i<DPP_XOR2>((int)g));
+        g = max(g, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)g));
+        g = max(g, (uint32_t)dpp_i<DPP_MIRROR>((int)g));
+        const uint32_t glo = max((uint32_t)__builtin_amdgcn_readlane((int)g, 0), (uint32_t)__builtin_amdgcn_readlane((int)g, 16));
+        const uint32_t ghi = max((uint32_t)__builtin_amdgcn_readlane((int)g, 32), (uint32_t)__builtin_amdgcn_readlane((int)g, 48));
+        if (lane == 0) {
+            gmax_s[2 * wv] = glo;
+            gmax_s[2 * wv + 1] = ghi;
+        }
+    }
+    __syncthreads();
+    if (tid < 256) {
+        uint32_t T = gmax_s[0];
+#pragma unroll
+        for (int i = 1; i < 8; i++) T = min(T, gmax_s[i]);
+        const bool cand = key != 0u && key >= T;
+        const uint64_t bal = __ballot(cand);
+        int base = 0;
+        if (lane == 0 && bal) base = atomicAdd(&ncand_s, __popcll(bal));
+        base = __builtin_amdgcn_readfirstlane(base);
+        const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        if (cand && pos < 64) cand_s[pos] = topk_ck(key, tid);
+        ck_s[tid] = topk_ck(key, tid);
+    }
+    __syncthreads();
+    const int ncand = ncand_s;
+    if (ncand > 64) {                                   /* workgroup-uniform */
+        const int k = tid >> 1, half = tid & 1;         /* two threads per key, half the table each */
+        const unsigned long long my = ck_s[k];
+        const ulonglong2 *t2 = (const ulonglong2 *)ck_s + half * 64;
+        int rank = 0;
+#pragma unroll
+        for (int j0 = 0; j0 < 64; j0 += 16) {
+            ulonglong2 v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = t2[j0 + u];
+#pragma unroll
+            for (int u = 0; u < 16; u++) rank += (v[u].x > my ? 1 : 0) + (v[u].y > my ? 1 : 0);
+        }
+        rank += dpp_i<DPP_XOR1>(rank);
+        if (!half && k < E && (uint32_t)(my >> 32) != 0u && rank < RTOPK) slot_s[rank] = k;
+        __syncthreads();
+    } else if (wv == 0) {
+        const unsigned long long my = lane < ncand ? cand_s[lane] : 0ull;
+        int rank = 0;
+        for (int j0 = 0; j0 < ncand; j0 += 16) {
+            unsigned long long v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = cand_s[min(j0 + u, 63)];
+#pragma unroll
+            for (int u = 0; u < 16; u++) rank += (j0 + u < ncand && v[u] > my) ? 1 : 0;
+        }
+        if (lane < ncand && rank < RTOPK) slot_s[rank] = 255 - (int)(uint32_t)my;
+        __builtin_amdgcn_s_waitcnt(LGKM_ONLY);
+        __builtin_amdgcn_wave_barrier();
+    }
+    if (wv == 0) {
+        const int id = lane < RTOPK ? slot_s[lane] : -1;
+        const int nsel = __popcll(__ballot(id >= 0));       /* the ranks fill a prefix of the slots */
+        const float v = id >= 0 ? key_logit(logit_key(lg_s[id])) : -INFINITY;
+        topk_finish(v, id, nsel, ids_s, w_s, &s_err);
+        if (lane == 0) w_s[RTOPK] = 1.0f / (1.0f + expf(-sg_s));
+    }
+    __syncthreads();
+    K1_TS(4);
+    if (gw == 0) {
+        if (tid < RTOPK) {
+            const size_t o = (size_t)(l - A.layer0) * RTOPK + tid;
+            if (A.ids_out) A.ids_out[o] = ids_s[tid];
+            if (A.w_out) A.w_out[o] = w_s[tid];
+        }
+        if (tid == 0 && s_err) atomicOr(A.err, 1);
+    }
+
+    /* ---- 5. the slot's expert: gate/up pairs and down rows loaded together */
+    const int e = ids_s[grp];
+    const bool live_slot = e >= 0;
+    const size_t ee = live_slot ? (size_t)e : 0;              /* an unselected slot reads expert 0, unused */
+    const uint8_t *ge = L.gate + ee * L.eb[0], *ue = L.up + ee * L.eb[1], *de = L.down + ee * L.eb[2];
+    const int RGP = I / K1_GW, npg = NPG ? NPG : (RGP + K1_W - 1) / K1_W;
+    const int RD = H / K1_GW, ndt = (RD + rpw - 1) / rpw, nd = ND ? ND : (ndt + K1_W - 1) / K1_W;
+    constexpr int MPG = NPG ? NPG : K1_MAXPG, MD = ND ? ND : K1_MAXD;
+    QChunk2 gch[MPG];
+    QChunk dch[MD];
+#pragma unroll
+    for (int f = 0; f < MPG; f++) {
+        if (NPG || f < npg) {
+            const size_t j = (size_t)gi * RGP + min(wv + f * K1_W, RGP - 1);
+            gch[f].g = q_load_t(g6, ge, j, nbh, lb, c);
+            gch[f].u = q_load_t(u6, ue, j, nbh, lb, c);
+        }
+    }
+#pragma unroll
+    for (int f = 0; f < MD; f++) {
+        if (ND || f < nd) {
+            const int task = min(wv + f * K1_W, ndt - 1);
+            dch[f] = q_load_t(d6, de, (size_t)min(gi * RD + task * rpw + rw_, H - 1), nbi, lbd, lr & 7);
+        }
+    }
+#pragma unroll
+    for (int f = 0; f < MPG; f++) {
+        const int pj = wv + f * K1_W;
+        if ((NPG || f < npg) && pj < RGP) {
+            const float eh = k1_gu_pair(g6, u6, gch[f], xn, xsum, swz, nbh);
+            if (lane == 0) xch_put(xehx + (size_t)gi * RGP + pj, live_slot ? eh : 0.0f, ep);
+        }
+        if (f == 0) K1_TS(5);
+    }
+    K1_TS(6);
+    for (int t = tid; t < I; t += K1_T) ehk[t] = xch_get(xehx + t, ep, dead, A.spin);
+    K1_SYNC_DEAD();
+    K1_TS(7);
+    for (int r = tid; r < I / 16; r += K1_T) ehks[r] = sum16(ehk + r * 16);
+    __syncthreads();
+#pragma unroll
+    for (int f = 0; f < MD; f++) {
+        const int task = wv + f * K1_W;
+        if ((ND || f < nd) && task < ndt) {
+            const int rl = task * rpw + rw_, row = gi * RD + rl;
+            const bool live = rl < RD && lbd < nbi;
+            const float part = k1_down_row(d6, dch[f], ehk, ehks, live, lpr);
+            if (live && lr == 0) xch_put(xdx + (size_t)grp * H + row, live_slot ? part : 0.0f, ep);
+        }
+    }
+    K1_TS(8);
+
+    /* ---- 6. owned rows: shared down, the eight slots' outputs, combine ---- */
+    for (int t = tid; t < I; t += K1_T) ehsh[t] = xch_get(xehs + t, ep, dead, A.spin);
+    K1_SYNC_DEAD();
+    K1_TS(9);
+    for (int r = tid; r < I / 16; r += K1_T) ehshs[r] = sum16(ehsh + r * 16);
+    __syncthreads();
+    if (sdt >= 0) {
+        const int rl = sdt * rpw + rw_;
+        const bool live = rl < RO && lbd < nbi;
+        const float part = k1_down_row(sd6, sdc, ehsh, ehshs, live, lpr);
+        if (live && lr == 0) dsh_s[rl] = part;
+    }
+    if (tid < RTOPK * RO) {
+        const int k = tid / RO, rl = tid % RO;
+        dk_s[k][rl] = xch_get(xdx + (size_t)k * H + gw * RO + rl, ep, dead, A.spin);
+    }
+    K1_SYNC_DEAD();
+    K1_TS(10);
+    if (tid < RO) {
+        float y = 0.0f;
+#pragma unroll
+        for (int k = 0; k < RTOPK; k++) y = fmaf(w_s[k], dk_s[k][tid], y);
+        y = fmaf(w_s[RTOPK], dsh_s[tid], y);
+        const int row = gw * RO + tid;
+        if (A.y) A.y[row] = y;
+        else A.h[row] = hv + y;
+    }
+    if (tid == 0 && dead) atomicOr(A.err, 2);
+    K1_TS(11);
+#ifdef ROASTER_PHASE_TS
+    if (tid == 0)
+        for (int i = 0; i < 12; i++) g_phase_ts[i >> 3][blockIdx.x][i & 7] = tsv[i];
+#endif
+#undef K1_TS
+}
+
+extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_layer1_kernel(DecArgs A, int l) { layer1_body<0, 0, -1>(A, l); }
+/* hidden 2048, inter 512: two gate/up pairs and two down tasks per wave;
+ * gate/up Q4_K and down Q6_K, routed and shared (types 0b100100) */
+extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_layer1_2x2_kernel(DecArgs A, int l) { layer1_body<2, 2, 0x24>(A, l); }
+
+/* Clears an exchange buffer (before epochs start again at 1). */
+extern "C" __global__ void dec_xch_clear_kernel(uint64_t *p, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0ull;
+}
+
 /* ---- host side ------------------------------------------------------------ */
 static size_t norm_lds(int B, int H) { return (size_t)B * H * 4 + (size_t)B * (H / 16) * 4; }
 
@@ -1046,6 +1543,76 @@ static int launch_layer(const DecArgs &A0, int l, bool with_router)
     return rt_check(hipGetLastError(), "down launch") ? ROASTER_EDEVICE : 0;
 }
 
+static int g_layer1 = 1;            /* roaster_decode_fused_layer */
+static uint32_t g_spin = K1_SPIN;   /* roaster_decode_spin_limit */
+
+extern "C" unsigned roaster_decode_spin_limit(unsigned polls)
+{
+    std::lock_guard<std::recursive_mutex> g(rt_lock());
+    if (polls) g_spin = polls;
+    return g_spin;
+}
+
+extern "C" int roaster_decode_fused_layer(int enable)
+{
+    std::lock_guard<std::recursive_mutex> g(rt_lock());
+    if (enable == 0 || enable == 1) g_layer1 = enable;
+    return g_layer1;
+}
+
+bool dec_layer1_ok(int E, int H, int I, int B)
+{
+    return g_layer1 && B == 1 && rt().n_cu >= K1_NWG && E >= RTOPK && E <= 256 && E % K1_GW == 0 && H % RQK == 0 &&
+           H <= K1_MAXH && I % RQK == 0 && I <= K1_MAXI;
+}
+
+static DecXch g_xch;
+
+DecXch *dec_xch_default(int E, int H, int I)
+{
+    const size_t n = (size_t)XCH_U64(E, H, I);
+    if (g_xch.p && g_xch.n >= n) return &g_xch;
+    if (g_xch.p) {
+        (void)hipStreamSynchronize(rt().stream);
+        (void)hipFree(g_xch.p);
+        g_xch.p = NULL;
+        g_xch.n = 0;
+    }
+    if (rt_check(hipMalloc((void **)&g_xch.p, n * 8), "exchange buffer hipMalloc")) {
+        g_xch.p = NULL;
+        return NULL;
+    }
+    hipLaunchKernelGGL(dec_xch_clear_kernel, dim3(64), dim3(256), 0, rt().stream, g_xch.p, n);
+    if (rt_check(hipGetLastError(), "exchange buffer clear")) return NULL;
+    g_xch.n = n;
+    g_xch.epoch = 0;
+    return &g_xch;
+}
+
+/* One launch per layer (dec_layer1_kernel) on the exchange buffer A.xbuf. */
+static int launch_layer1(DecArgs &A)
+{
+    DecXch &X = *A.xbuf;
+    A.xch = X.p;
+    for (int l = A.layer0; l < A.layer0 + A.nlayers; l++) {
+        if (X.epoch == 0xFFFFFFFFu) {                 /* epochs start again on cleared slots */
+            hipLaunchKernelGGL(dec_xch_clear_kernel, dim3(64), dim3(256), 0, rt().stream, X.p, X.n);
+            if (rt_check(hipGetLastError(), "exchange buffer clear")) return ROASTER_EDEVICE;
+            X.epoch = 0;
+        }
+        A.epoch = ++X.epoch;
+        A.spin = g_spin;
+        const int nbi = A.I / RQK, rpw = 64 / lanes_per_row(nbi);
+        const int npg = (A.I / K1_GW + K1_W - 1) / K1_W, nd = ((A.H / K1_GW + rpw - 1) / rpw + K1_W - 1) / K1_W;
+        const DecLayer *Lh = A.layers_h ? A.layers_h + l : nullptr;
+        const bool ty = Lh && !Lh->q6[0] && !Lh->q6[1] && Lh->q6[2] && !Lh->sq6[0] && !Lh->sq6[1] && Lh->sq6[2];
+        if (npg == 2 && nd == 2 && ty) hipLaunchKernelGGL(dec_layer1_2x2_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A, l);
+        else hipLaunchKernelGGL(dec_layer1_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A, l);
+        if (rt_check(hipGetLastError(), "layer launch")) return ROASTER_EDEVICE;
+    }
+    return 0;
+}
+
 int dec_launch(DecArgs &A)
 {
     A.xswz = A.H % 512 == 0;
@@ -1056,6 +1623,7 @@ int dec_launch(DecArgs &A)
         if (!ctrl || !A.plan_g) return ROASTER_ENOMEM;
         A.err = (int *)(ctrl + 16);
     }
+    if (A.xbuf && !A.ffn_out && dec_layer1_ok(A.E, A.H, A.I, A.B)) return launch_layer1(A);
     for (int l = A.layer0; l < A.layer0 + A.nlayers; l++)
         if (int rc = launch_layer(A, l, true)) return rc;
     return 0;

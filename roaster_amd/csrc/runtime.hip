@@ -114,7 +114,7 @@ int rt_take_err()
         e |= w;
     }
     if (!e) return 0;
-    if (e & 2) return rt_fail(ROASTER_EDEVICE, "a grid barrier timed out (workgroups not co-resident?)");
+    if (e & 2) return rt_fail(ROASTER_EDEVICE, "a decode layer's exchange wait timed out (workgroups not all resident?)");
     return rt_fail(ROASTER_EROUTE, "router produced fewer than 8 finite logits for some token");
 }
 
