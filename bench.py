@@ -382,6 +382,7 @@ def prefill_legs(torch, L, R, dev, stream, reps, with_cpu):
                             "algorithmic_bytes": int(nbytes), "algorithmic_flops": int(flops),
                             "arithmetic_intensity": round(ai, 1), "achieved_TFLOPs": round(tf, 2),
                             "roof_TFLOPs": round(roof_tf, 1), "frac_mfma_peak": round(tf / MFMA_PEAK_TFLOPS, 4)}}
+        leg["kernels_h_moe_prefill"] = moe_prefill_hostbuf_leg(L, R, t, desc, seed, Xh, idh)
         if with_cpu:
             cb = cpu_baseline_prefill(t, desc, seed, Xh, idh, layer=0, with_router=True, label="Zipf-routed Q4_K/Q6_K")
             if cb:
@@ -390,6 +391,61 @@ def prefill_legs(torch, L, R, dev, stream, reps, with_cpu):
     finally:
         L.roaster_table_destroy(t)
     return out
+
+
+def moe_prefill_hostbuf_leg(L, R, table, desc, seed, X, ids, reps=3):
+    """The drop-in path for the same layer: the expert row groups of the
+    Zipf-routed 512 tokens through kernels.h kernel_moe_prefill on host
+    buffers, in calls of at most 32 experts as pf_moe makes them
+    (model.c:1736-1742), plus the shared expert over all tokens as one more
+    group; weights in kernel_vk_alloc_weights memory as weights.c allocates
+    them.  Host wall clock, including the X upload and D download over PCIe;
+    the first pass (weight upload into HBM) is not timed."""
+    T = X.shape[0]
+    groups = []
+    for e in range(E):
+        rows = np.nonzero((ids == e).any(axis=1))[0]
+        if len(rows):
+            groups.append((e, rows))
+    granted = C.c_size_t(0)
+    host = {}
+    for e in [g[0] for g in groups] + [E]:
+        mats = fetch_expert(R, table, seed, 0, e, desc)
+        ptrs = []
+        for a in mats:
+            p = L.kernel_vk_alloc_weights(a.nbytes, C.byref(granted))
+            assert p, R.last_error()
+            C.memmove(p, a.ctypes.data, a.nbytes)
+            ptrs.append(p)
+        host[e] = ptrs
+    calls = []
+    for c0 in range(0, len(groups), 32):
+        chunk = groups[c0:c0 + 32]
+        Xg = np.ascontiguousarray(np.concatenate([X[r] for _, r in chunk]), np.float32)
+        Dg = np.empty_like(Xg)
+        arr = (R.KernelMoeExpert * len(chunk))()
+        for i, (e, r) in enumerate(chunk):
+            g, u, d = host[e]
+            arr[i] = R.KernelMoeExpert(g, u, d, desc.q6[0], desc.q6[1], desc.q6[2], len(r))
+        calls.append((arr, len(chunk), Xg, Dg))
+    g, u, d = host[E]
+    sh = (R.KernelMoeExpert * 1)()
+    sh[0] = R.KernelMoeExpert(g, u, d, desc.sh_q6[0], desc.sh_q6[1], desc.sh_q6[2], T)
+    Xs = np.ascontiguousarray(X, np.float32)
+    calls.append((sh, 1, Xs, np.empty_like(Xs)))
+    best = None
+    for rep in range(reps + 1):
+        t0 = time.perf_counter()
+        for arr, n, Xg, Dg in calls:
+            if L.kernel_moe_prefill(arr, n, Xg.ctypes.data, Dg.ctypes.data, I, H) != 0:
+                raise RuntimeError(R.last_error())
+        dt = time.perf_counter() - t0
+        if rep:
+            best = dt if best is None else min(best, dt)
+    rows = sum(len(r) for _, r in groups) + T
+    return {"tokens_per_s": round(T / best, 1), "ms_per_layer": round(best * 1e3, 3), "calls": len(calls),
+            "expert_rows": int(rows), "precision": "split bf16 hi+lo operands, fp32 accumulation (MFMA)",
+            "note": "host wall clock incl. PCIe transfers of X and D; router and combine not included"}
 
 
 def config1_leg(torch, L, R, dev, stream, with_cpu):
@@ -492,28 +548,37 @@ def config2_leg(torch, L, R, dev, stream, with_cpu):
 
 
 def dense_leg(torch, L, R, dev, stream):
-    """The LM head as a dense Q6_K projection [248320 x 2048] (model.c:1368-1370)
-    for 1 and 8 tokens through roaster_matvec_q: device time from HIP events,
-    HBM roofline over the matrix bytes."""
-    rows, cols = 248320, 2048
-    W = R.synth_q6k(5, R.synth_stream(0, 0, 9), rows * (cols // 256))
-    dw = torch.from_numpy(W).to(dev)
-    out = {"workload": "LM head Q6_K [248320 x 2048]", "matrix_bytes": int(W.nbytes)}
-    for T in (1, 8):
-        x = torch.from_numpy(np.stack([R.synth_normal(5, R.synth_stream(0, t, 5), cols) for t in range(T)])).to(dev)
-        y = torch.empty((T, rows), dtype=torch.float32, device=dev)
+    """Dense quantised projections through roaster_matvec_q (model.c:113-121):
+    the LM head Q6_K [248320 x 2048] (model.c:1368-1370) at 1 and 8 tokens, the
+    8-token case also through the split-operand MFMA GEMM, and the attention
+    output projection Q4_K [2048 x 4096] (model.c:862) at 1 and 8 tokens.
+    Device time from HIP events, HBM roofline over the matrix bytes."""
+    out = {}
+    for name, q6, rows, cols in (("lm_head_q6k_248320x2048", 1, 248320, 2048), ("attn_out_q4k_2048x4096", 0, 2048, 4096)):
+        nb = rows * (cols // 256)
+        W = R.synth_q6k(5, R.synth_stream(0, 0, 9), nb) if q6 else R.synth_q4k(5, R.synth_stream(0, 0, 9), nb)
+        dw = torch.from_numpy(W).to(dev)
+        leg = {"matrix_bytes": int(W.nbytes)}
+        for T, mfma in ((1, False), (8, False), (8, True)):
+            x = torch.from_numpy(np.stack([R.synth_normal(5, R.synth_stream(0, t, 5), cols) for t in range(T)])).to(dev)
+            y = torch.empty((T, rows), dtype=torch.float32, device=dev)
+            old = L.roaster_dense_mfma_min_tokens(0)
+            L.roaster_dense_mfma_min_tokens(2 if mfma else 9)
 
-        def run():
-            rc = L.roaster_matvec_q(dw.data_ptr(), 1, x.data_ptr(), y.data_ptr(), rows, cols, T)
-            if rc:
-                raise RuntimeError(R.last_error())
-        run()
-        R.check(L.roaster_sync(), "dense warmup")
-        ms = event_ms(torch, stream, run, 50)
-        gbs = W.nbytes / (ms * 1e-3) / 1e9
-        out["T%d" % T] = {"us": round(ms * 1e3, 1), "tokens_per_s": round(T / (ms * 1e-3), 1),
-                          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                                       "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+            def run():
+                rc = L.roaster_matvec_q(dw.data_ptr(), q6, x.data_ptr(), y.data_ptr(), rows, cols, T)
+                if rc:
+                    raise RuntimeError(R.last_error())
+            run()
+            R.check(L.roaster_sync(), "dense warmup")
+            ms = event_ms(torch, stream, run, 50 if rows > 100000 else 200)
+            L.roaster_dense_mfma_min_tokens(old)
+            gbs = W.nbytes / (ms * 1e-3) / 1e9
+            leg["T%d%s" % (T, "_mfma" if mfma else "")] = {
+                "us": round(ms * 1e3, 2), "tokens_per_s": round(T / (ms * 1e-3), 1),
+                "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+        out[name] = leg
     return out
 
 

@@ -190,11 +190,16 @@ int roaster_moe_decode_stack_noalloc(RoasterTable *t, float *h, int B, int layer
 /* ---- dense projections ---------------------------------------------------- */
 /* Y[t * rows + r] = W[r] . X[t * cols ..] for t < T (1..8): a quantised
  * [rows x cols] matrix on the device (q6: 0 = Q4_K, 1 = Q6_K, cols a multiple
- * of 256, at most 2048) -- the projections on either side of the MoE block and
- * the LM head (model.c:795-800, 1284-1290, 1368-1370), the products
- * kernel_matvec_q4_k / _q6_k compute from host buffers.  Device pointers;
- * ordered on the library stream. */
+ * of 256, at most 4096) -- the projections on either side of the MoE block
+ * (the attention output and DeltaNet ssm_out projections have 4096 columns,
+ * model.c:862, 1344-1347) and the LM head (model.c:795-800, 1284-1290,
+ * 1368-1370), the products kernel_matvec_q4_k / _q6_k compute from host
+ * buffers.  Device pointers; ordered on the library stream. */
 int roaster_matvec_q(const void *W, int q6, const float *X, float *Y, size_t rows, size_t cols, int T);
+/* Calls of roaster_matvec_q with at least t tokens (and rows a multiple of
+ * 64) run as the split-operand MFMA GEMM instead of the dequantising matvec;
+ * t = 0 queries.  Returns the threshold in force. */
+int roaster_dense_mfma_min_tokens(int t);
 
 /* ---- prefill ------------------------------------------------------------ */
 typedef struct {

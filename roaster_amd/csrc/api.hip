@@ -11,7 +11,12 @@
 #include "internal.h"
 #include "decode.h"
 #include "matvec.h"
+#include "prefill.h"
 #include "table.h"
+
+#define PF_SPLIT_OP 1           /* gemm.h PF_SPLIT: bf16 hi + lo operands, 3 MFMAs, fp32 accumulation */
+#define GEMM_ROWS 64            /* gemm.h GM / GN: rows per tile, output rows per block */
+#define MM_MFMA_MIN_T 16        /* kernel_matmul_quant_batch jobs with at least this many tokens use MFMA */
 
 #include <math.h>
 #include <stdio.h>
@@ -159,6 +164,57 @@ static float dot_quant(int q6, const void *w, const float *x, size_t n)
 extern "C" float kernel_dot_q4_k(const void *weights, const float *x, size_t n) { return dot_quant(0, weights, x, n); }
 extern "C" float kernel_dot_q6_k(const void *weights, const float *x, size_t n) { return dot_quant(1, weights, x, n); }
 
+/* ---- grouped GEMMs on MFMA for the host-buffer entry points ------------------
+ * Tile lists and group tables for pf_gemm (prefill.h) built on the host and
+ * uploaded through pinned staging: one group per expert (or per matmul job),
+ * its rows consecutive in X, D and the intermediate buffer. */
+struct GemmWs { PfGroup *groups; PfTile *tiles; int *ntiles; int nt; };
+
+static int gemm_ws(const std::vector<PfGroup> &hg, GemmWs &W)
+{
+    std::vector<PfTile> ht;
+    for (int i = 0; i < (int)hg.size(); i++)
+        for (int m0 = 0; m0 < hg[i].n; m0 += GEMM_ROWS) ht.push_back(PfTile{ i, m0 });
+    W.nt = (int)ht.size();
+    const size_t gb = (sizeof(PfGroup) * hg.size() + 255) & ~(size_t)255, tb = (sizeof(PfTile) * ht.size() + 255) & ~(size_t)255;
+    uint8_t *dev = (uint8_t *)rt_scratch(SCR_E, gb + tb + 256);
+    uint8_t *pin = (uint8_t *)rt_pinned(2, gb + tb + 256);
+    if (!dev || !pin) return ROASTER_ENOMEM;
+    if (rt_check(hipStreamSynchronize(rt().stream), "staging wait")) return ROASTER_EDEVICE;   /* pin is reused */
+    memcpy(pin, hg.data(), sizeof(PfGroup) * hg.size());
+    memcpy(pin + gb, ht.data(), sizeof(PfTile) * ht.size());
+    memcpy(pin + gb + tb, &W.nt, sizeof(int));
+    if (rt_check(hipMemcpyAsync(dev, pin, gb + tb + 256, hipMemcpyHostToDevice, rt().stream), "tile list upload"))
+        return ROASTER_EDEVICE;
+    W.groups = (PfGroup *)dev;
+    W.tiles = (PfTile *)(dev + gb);
+    W.ntiles = (int *)(dev + gb + tb);
+    return 0;
+}
+
+/* Y[t * rows + r] = W[r] . X[t] on device buffers (rows a multiple of 64). */
+int matmul_mfma(const uint8_t *W, int q6, const float *X, float *Y, size_t rows, size_t cols, size_t T)
+{
+    std::vector<PfGroup> hg(1);
+    memset(hg.data(), 0, sizeof(PfGroup));
+    hg[0].d = W;
+    hg[0].dq6 = q6;
+    hg[0].n = (int)T;
+    GemmWs ws;
+    if (int rc = gemm_ws(hg, ws)) return rc;
+    PfGemmArgs ga;
+    memset(&ga, 0, sizeof(ga));
+    ga.groups = ws.groups;
+    ga.tiles = ws.tiles;
+    ga.ntiles = ws.ntiles;
+    ga.act = (float *)X;
+    ga.out = Y;
+    ga.H = (int)rows;
+    ga.I = (int)cols;
+    ga.chunk = GEMM_ROWS;
+    return pf_matmul_launch(ga, ws.nt);
+}
+
 /* ---- multi-token matmul ---------------------------------------------------- */
 static int mm_valid(const KernelMatmulJob *j)
 {
@@ -202,13 +258,23 @@ extern "C" int kernel_matmul_quant_batch(const KernelMatmulJob *jobs, int n)
         if (owner[i] == i &&
             rt_check(hipMemcpyAsync(dx + xoff[i], j.X, j.T * j.cols * 4, hipMemcpyHostToDevice, R.stream), "X upload"))
             return -1;
+        if (j.T >= MM_MFMA_MIN_T && j.rows % GEMM_ROWS == 0) {
+            /* split-operand MFMA GEMM (the down GEMM of the prefill path as a
+             * plain product); the job keeps a zero-task slot in the matvec launch */
+            if (matmul_mfma(W, j.is_q6 ? 1 : 0, (const float *)(dx + xoff[i]), (float *)(dy + yoff[i]), j.rows, j.cols,
+                            j.T))
+                return -1;
+            hj[i] = MvJob{ W, (const float *)(dx + xoff[i]), (float *)(dy + yoff[i]), 0, (int)j.cols, 0, j.is_q6 ? 1 : 0,
+                           tasks };
+            continue;
+        }
         hj[i] = MvJob{ W, (const float *)(dx + xoff[i]), (float *)(dy + yoff[i]), (int)j.rows, (int)j.cols, (int)j.T,
                        j.is_q6 ? 1 : 0, tasks };
         tasks += mv_tasks_for((int)j.rows, j.cols);
     }
     if (rt_check(hipMemcpyAsync(dj, hj.data(), sizeof(MvJob) * n, hipMemcpyHostToDevice, R.stream), "job upload"))
         return -1;
-    if (mv_launch(dj, n, tasks)) return -1;
+    if (tasks && mv_launch(dj, n, tasks)) return -1;
     for (int i = 0; i < n; i++)
         if (rt_check(hipMemcpyAsync(jobs[i].Y, dy + yoff[i], jobs[i].T * jobs[i].rows * 4, hipMemcpyDeviceToHost,
                                     R.stream), "Y download"))
@@ -216,7 +282,51 @@ extern "C" int kernel_matmul_quant_batch(const KernelMatmulJob *jobs, int n)
     return rt_check(hipStreamSynchronize(R.stream), "matmul sync") ? -1 : 0;
 }
 
-/* ---- prefill MoE on host buffers (kernels.c:2198-2214) -------------------- */
+/* ---- prefill MoE on host buffers (kernels.c:2198-2214) --------------------
+ * The expert row groups as the prefill path's grouped GEMMs on MFMA: gate/up
+ * with the SiLU*up epilogue, then down, in split mode (bf16 hi + lo operands,
+ * three MFMAs per product block, fp32 accumulation: about 5e-6 of max|D|,
+ * inside the 2e-4 of the reference's own test, test_kernels.c:31), reading
+ * the weights' HBM copies in their GGML layout. */
+static int moe_groups_mfma(const KernelMoeExpert *ex, int na, const float *dx, float *dd, size_t inter, size_t hidden,
+                           size_t total)
+{
+    std::vector<PfGroup> hg(na);
+    size_t row = 0;
+    for (int i = 0; i < na; i++) {
+        const KernelMoeExpert &e = ex[i];
+        PfGroup &G = hg[i];
+        memset(&G, 0, sizeof(G));
+        G.g = (const uint8_t *)rt_weight_dev(e.gate, rq_mat_bytes(e.gate_q6, inter, hidden));
+        G.u = (const uint8_t *)rt_weight_dev(e.up, rq_mat_bytes(e.up_q6, inter, hidden));
+        G.d = (const uint8_t *)rt_weight_dev(e.down, rq_mat_bytes(e.down_q6, hidden, inter));
+        if (!G.g || !G.u || !G.d) return ROASTER_EDEVICE;
+        G.gq6 = e.gate_q6 ? 1 : 0;
+        G.uq6 = e.up_q6 ? 1 : 0;
+        G.dq6 = e.down_q6 ? 1 : 0;
+        G.n = (int)e.n;
+        G.slot0 = (int)row;
+        G.tok0 = (int)row;
+        row += e.n;
+    }
+    float *act = (float *)rt_scratch(SCR_B, total * inter * 4);
+    if (!act) return ROASTER_ENOMEM;
+    GemmWs ws;
+    if (int rc = gemm_ws(hg, ws)) return rc;
+    PfGemmArgs ga;
+    memset(&ga, 0, sizeof(ga));
+    ga.groups = ws.groups;
+    ga.tiles = ws.tiles;
+    ga.ntiles = ws.ntiles;
+    ga.X = dx;
+    ga.act = act;
+    ga.out = dd;
+    ga.H = (int)hidden;
+    ga.I = (int)inter;
+    ga.chunk = GEMM_ROWS;
+    return pf_gemm_launch(ga, ws.nt, PF_SPLIT_OP);
+}
+
 int prefill_groups_device(const KernelMoeExpert *ex, int na, const float *X, float *D, size_t inter, size_t hidden,
                           size_t total);
 
@@ -239,7 +349,7 @@ extern "C" int kernel_moe_prefill(const KernelMoeExpert *ex, int count, const fl
     float *dd = (float *)rt_scratch(SCR_OUT, total * hidden * 4);
     if (!dx || !dd) return -1;
     if (rt_check(hipMemcpyAsync(dx, X, total * hidden * 4, hipMemcpyHostToDevice, R.stream), "X upload")) return -1;
-    if (prefill_groups_device(act.data(), (int)act.size(), dx, dd, inter, hidden, total)) return -1;
+    if (moe_groups_mfma(act.data(), (int)act.size(), dx, dd, inter, hidden, total)) return -1;
     if (rt_check(hipMemcpyAsync(D, dd, total * hidden * 4, hipMemcpyDeviceToHost, R.stream), "D download")) return -1;
     return rt_check(hipStreamSynchronize(R.stream), "prefill sync") ? -1 : 0;
 }

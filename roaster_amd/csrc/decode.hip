@@ -1568,6 +1568,14 @@ bool dec_layer1_ok(int E, int H, int I, int B)
 
 static DecXch g_xch;
 
+void dec_release()
+{
+    if (g_xch.p) (void)hipFree(g_xch.p);
+    g_xch.p = NULL;
+    g_xch.n = 0;
+    g_xch.epoch = 0;
+}
+
 DecXch *dec_xch_default(int E, int H, int I)
 {
     const size_t n = (size_t)XCH_U64(E, H, I);

@@ -73,7 +73,6 @@ int rt_take_err();           /* sync the stream, report and clear kernel error b
 void rt_set_aux_err(int *dev_word);   /* a second device error word rt_take_err reports and clears */
 int noalloc_setup(int dev);  /* api.hip: device address of the allocation-free scratch array */
 
-/* Launch helpers */
-int rt_coop_grid(const void *kernel, int threads, size_t lds, int *blocks_out);
+void dec_release();          /* decode.hip: frees the decode exchange buffer */
 
 #endif

@@ -70,7 +70,10 @@ __global__ void __launch_bounds__(MV_THREADS) matvec_jobs_kernel(const MvJob *jo
 #define DMV_GRID 8                         /* workgroups per CU at most */
 #endif
 
-template <bool Q6, bool ONE>
+static int g_dense_mfma_t = 9;             /* no call reaches it until measured to pay off */
+int matmul_mfma(const uint8_t *W, int q6, const float *X, float *Y, size_t rows, size_t cols, size_t T);   /* api.hip */
+
+template <bool Q6, bool ONE, int KB>
 __global__ void __launch_bounds__(MV_THREADS) dense_mv_kernel(const uint8_t *W, const float *X, float *Y, int rows,
                                                               int cols, int T)
 {
@@ -78,22 +81,32 @@ __global__ void __launch_bounds__(MV_THREADS) dense_mv_kernel(const uint8_t *W, 
     const int lane = threadIdx.x & 63;
     const int nb = cols / RQK, lpr = lanes_per_row(nb), rpw = 64 / lpr;
     const int rw = lane / lpr, lr = lane % lpr, c = lr & 7, lb = lr >> 3;
-    const bool lane_live = lb < nb;
     const size_t bs = Q6 ? RQ6K_BYTES : RQ4K_BYTES, row_bytes = (size_t)nb * bs;
-    const int ca = lb * RQK + q_run_a<Q6>(c), cb = ca + q_run_b_off<Q6>();
-    float4 xa[4], xb[4];
-    float sxa = 0.0f, sxb = 0.0f;
+    /* KB super-blocks per lane: lb, lb + 8 (rows of more than 8 blocks) */
+    bool blk_live[KB];
+    int ca[KB], cb[KB];
+#pragma unroll
+    for (int k = 0; k < KB; k++) {
+        blk_live[k] = lb + 8 * k < nb;
+        ca[k] = (lb + 8 * k) * RQK + q_run_a<Q6>(c);
+        cb[k] = ca[k] + q_run_b_off<Q6>();
+    }
+    float4 xa[KB][4], xb[KB][4];
+    float sxa[KB], sxb[KB];
     float *xsum = xs + (size_t)T * cols;
     if (ONE) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            xa[i] = lane_live ? gld_f4(X + ca + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-            xb[i] = lane_live ? gld_f4(X + cb + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int k = 0; k < KB; k++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                xa[k][i] = blk_live[k] ? gld_f4(X + ca[k] + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                xb[k][i] = blk_live[k] ? gld_f4(X + cb[k] + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            sxa[k] = ((xa[k][0].x + xa[k][0].y) + (xa[k][0].z + xa[k][0].w)) + ((xa[k][1].x + xa[k][1].y) + (xa[k][1].z + xa[k][1].w)) +
+                     (((xa[k][2].x + xa[k][2].y) + (xa[k][2].z + xa[k][2].w)) + ((xa[k][3].x + xa[k][3].y) + (xa[k][3].z + xa[k][3].w)));
+            sxb[k] = ((xb[k][0].x + xb[k][0].y) + (xb[k][0].z + xb[k][0].w)) + ((xb[k][1].x + xb[k][1].y) + (xb[k][1].z + xb[k][1].w)) +
+                     (((xb[k][2].x + xb[k][2].y) + (xb[k][2].z + xb[k][2].w)) + ((xb[k][3].x + xb[k][3].y) + (xb[k][3].z + xb[k][3].w)));
         }
-        sxa = ((xa[0].x + xa[0].y) + (xa[0].z + xa[0].w)) + ((xa[1].x + xa[1].y) + (xa[1].z + xa[1].w)) +
-              (((xa[2].x + xa[2].y) + (xa[2].z + xa[2].w)) + ((xa[3].x + xa[3].y) + (xa[3].z + xa[3].w)));
-        sxb = ((xb[0].x + xb[0].y) + (xb[0].z + xb[0].w)) + ((xb[1].x + xb[1].y) + (xb[1].z + xb[1].w)) +
-              (((xb[2].x + xb[2].y) + (xb[2].z + xb[2].w)) + ((xb[3].x + xb[3].y) + (xb[3].z + xb[3].w)));
     } else {
         for (int i = threadIdx.x; i < T * cols / 4; i += MV_THREADS) ((float4 *)xs)[i] = gld_f4(X + 4 * i);
         __syncthreads();
@@ -103,26 +116,32 @@ __global__ void __launch_bounds__(MV_THREADS) dense_mv_kernel(const uint8_t *W, 
     const int gw = blockIdx.x * (MV_THREADS / 64) + (threadIdx.x >> 6), nw = gridDim.x * (MV_THREADS / 64);
     const int npass = (rows + rpw - 1) / rpw;
     for (int p0 = gw; p0 < npass; p0 += nw * DMV_PF) {
-        QChunk ch[DMV_PF];
+        QChunk ch[DMV_PF][KB];
 #pragma unroll
         for (int f = 0; f < DMV_PF; f++) {
             const int row = (p0 + f * nw) * rpw + rw;
-            if (lane_live && row < rows) ch[f] = q_load<Q6>(W + (size_t)row * row_bytes + (size_t)lb * bs, c);
+#pragma unroll
+            for (int k = 0; k < KB; k++)
+                if (blk_live[k] && row < rows)
+                    ch[f][k] = q_load<Q6>(W + (size_t)row * row_bytes + (size_t)(lb + 8 * k) * bs, c);
         }
 #pragma unroll
         for (int f = 0; f < DMV_PF; f++) {
             const int pass = p0 + f * nw;
             if (pass >= npass) break;
             const int row = pass * rpw + rw;
-            const bool live = lane_live && row < rows;
+            const bool live = row < rows;
             for (int t = 0; t < (ONE ? 1 : T); t++) {
                 float part = 0.0f;
-                if (live) {
-                    if (ONE) {
-                        part = q_chunk_dot_r<Q6>(ch[f], c, xa, xb, sxa, sxb);
-                    } else {
-                        const float *x = xs + (size_t)t * cols, *sx = xsum + (size_t)t * (cols / 16);
-                        part = q_chunk_dot<Q6>(ch[f], c, x + ca, x + cb, sx[ca >> 4], sx[cb >> 4]);
+#pragma unroll
+                for (int k = 0; k < KB; k++) {
+                    if (live && blk_live[k]) {
+                        if (ONE) {
+                            part += q_chunk_dot_r<Q6>(ch[f][k], c, xa[k], xb[k], sxa[k], sxb[k]);
+                        } else {
+                            const float *x = xs + (size_t)t * cols, *sx = xsum + (size_t)t * (cols / 16);
+                            part += q_chunk_dot<Q6>(ch[f][k], c, x + ca[k], x + cb[k], sx[ca[k] >> 4], sx[cb[k] >> 4]);
+                        }
                     }
                 }
                 part = group_sum_w(part, lpr);
@@ -180,19 +199,41 @@ extern "C" int roaster_matvec_q(const void *W, int q6, const float *X, float *Y,
 {
     std::lock_guard<std::recursive_mutex> g(rt_lock());
     if (rt_init_locked()) return ROASTER_EDEVICE;
-    if (!W || !X || !Y || !rows || !cols || cols % RQK || cols > 2048 || T < 1 || T > 8 || rows > (size_t)INT32_MAX)
-        return rt_fail(ROASTER_EINVAL, "roaster_matvec_q: need cols a multiple of 256 and <= 2048, 1 <= T <= 8");
+    if (!W || !X || !Y || !rows || !cols || cols % RQK || cols > 4096 || T < 1 || T > 8 || rows > (size_t)INT32_MAX)
+        return rt_fail(ROASTER_EINVAL, "roaster_matvec_q: need cols a multiple of 256 and <= 4096, 1 <= T <= 8");
+    if (T >= g_dense_mfma_t && rows % 64 == 0)           /* several tokens: the split-operand MFMA GEMM */
+        return matmul_mfma((const uint8_t *)W, q6 ? 1 : 0, X, Y, rows, cols, (size_t)T);
     const int nb = (int)(cols / RQK), rpw = 64 / lanes_per_row(nb);
     const size_t npass = (rows + rpw - 1) / rpw;
     size_t blocks = (npass + 3) / 4;
     if (blocks > (size_t)DMV_GRID * rt().n_cu) blocks = (size_t)DMV_GRID * rt().n_cu;
     const size_t lds = T > 1 ? (size_t)T * cols * 4 + (size_t)T * (cols / 16) * 4 : 0;
     const dim3 gd((unsigned)blocks), bd(MV_THREADS);
-    if (q6 && T == 1) hipLaunchKernelGGL((dense_mv_kernel<true, true>), gd, bd, 0, rt().stream, (const uint8_t *)W, X, Y, (int)rows, (int)cols, T);
-    else if (q6) hipLaunchKernelGGL((dense_mv_kernel<true, false>), gd, bd, lds, rt().stream, (const uint8_t *)W, X, Y, (int)rows, (int)cols, T);
-    else if (T == 1) hipLaunchKernelGGL((dense_mv_kernel<false, true>), gd, bd, 0, rt().stream, (const uint8_t *)W, X, Y, (int)rows, (int)cols, T);
-    else hipLaunchKernelGGL((dense_mv_kernel<false, false>), gd, bd, lds, rt().stream, (const uint8_t *)W, X, Y, (int)rows, (int)cols, T);
+    const uint8_t *w = (const uint8_t *)W;
+    const int r = (int)rows, cc = (int)cols;
+#define DMV(Q6_, ONE_, KB_) hipLaunchKernelGGL((dense_mv_kernel<Q6_, ONE_, KB_>), gd, bd, ONE_ ? 0 : lds, rt().stream, w, X, Y, r, cc, T)
+    if (nb <= 8) {
+        if (q6 && T == 1) DMV(true, true, 1);
+        else if (q6) DMV(true, false, 1);
+        else if (T == 1) DMV(false, true, 1);
+        else DMV(false, false, 1);
+    } else {
+        if (q6 && T == 1) DMV(true, true, 2);
+        else if (q6) DMV(true, false, 2);
+        else if (T == 1) DMV(false, true, 2);
+        else DMV(false, false, 2);
+    }
+#undef DMV
     return rt_check(hipGetLastError(), "dense matvec launch") ? ROASTER_EDEVICE : 0;
+}
+
+/* roaster_dense_mfma_min_tokens: calls with at least this many tokens (and
+ * rows a multiple of 64) run as the split-operand MFMA GEMM; 0 = query. */
+extern "C" int roaster_dense_mfma_min_tokens(int t)
+{
+    std::lock_guard<std::recursive_mutex> g(rt_lock());
+    if (t > 0) g_dense_mfma_t = t;
+    return g_dense_mfma_t;
 }
 
 int silu_mul_launch(float *g, const float *u, size_t n)

@@ -803,6 +803,14 @@ static int launch_v1(const PfGemmArgs &A, int max_tiles)
     return rt_check(hipGetLastError(), "prefill down launch") ? ROASTER_EDEVICE : 0;
 }
 
+int pf_matmul_launch(const PfGemmArgs &A, int max_tiles)
+{
+    if (max_tiles <= 0) return 0;
+    const size_t lds = gemm_lds_bytes(PF_SPLIT);
+    hipLaunchKernelGGL(pf_down_kernel<PF_SPLIT>, dim3(max_tiles * (A.H / GN)), dim3(GT), lds, rt().stream, A);
+    return rt_check(hipGetLastError(), "matmul launch") ? ROASTER_EDEVICE : 0;
+}
+
 /* fp16 mode: up to three 32-row blocks; two when gate and up differ in type
  * (a wave then holds both raw record types, which for three blocks exceeds
  * the register budget of two waves per SIMD). */

@@ -52,4 +52,9 @@ int pf_gemm_chunk(int op, bool mixed_gate_up);
  * PF_SPLIT or PF_BF16 (gemm.h).  0 or ROASTER_EDEVICE. */
 int pf_gemm_launch(const PfGemmArgs &A, int max_tiles, int op);
 
+/* The down GEMM alone in split mode as a plain product: out[slot][r] =
+ * act[slot] . W[r] over A.I columns for A.H (a multiple of 64) rows of each
+ * group's d matrix.  0 or ROASTER_EDEVICE. */
+int pf_matmul_launch(const PfGemmArgs &A, int max_tiles);
+
 #endif

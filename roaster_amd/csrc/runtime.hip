@@ -577,11 +577,19 @@ extern "C" void kernel_vk_trim_scratch(void)
     rt_scratch_trim();
 }
 
+/* kernels.h:105 -- the reference destroys its backend here (kernels.c, called
+ * from weights.c:1171).  Everything the library holds goes: scratch, control
+ * words, the decode exchange buffer, pinned and staging buffers, the weight
+ * registry and its HBM twins, and the stream, so that nothing of the library
+ * is left for the HIP runtime to tear down at process exit.  Expert tables
+ * belong to the caller (roaster_table_destroy).  A later call initialises
+ * the library again. */
 extern "C" void kernel_vk_shutdown(void)
 {
     std::lock_guard<std::recursive_mutex> g(g_lock);
     if (!g_rt.inited) return;
     kernel_matvec_quant_end();
+    (void)hipStreamSynchronize(g_rt.stream);
     rt_scratch_trim();
     rt_registry_clear();
     for (int i = 0; i < 4; i++) {
@@ -589,14 +597,12 @@ extern "C" void kernel_vk_shutdown(void)
         g_pin[i].p = NULL;
         g_pin[i].n = 0;
     }
-}
-
-int rt_coop_grid(const void *kernel, int threads, size_t lds, int *blocks_out)
-{
-    int per_cu = 0;
-    if (rt_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds), "occupancy"))
-        return ROASTER_EDEVICE;
-    if (per_cu < 1) return rt_fail(ROASTER_EDEVICE, "kernel cannot be resident (threads %d, lds %zu)", threads, lds);
-    *blocks_out = per_cu * g_rt.n_cu;
-    return 0;
+    dec_release();
+    if (g_ctrl) {
+        (void)hipFree(g_ctrl);
+        g_ctrl = NULL;
+    }
+    (void)hipStreamDestroy(g_rt.stream);
+    g_rt.stream = NULL;
+    g_rt.inited = 0;
 }

@@ -1,7 +1,10 @@
 """Dense quantised projections on device buffers (roaster_matvec_q) against the
 oracle's matvec (kernels.c:407-432, 553-578): Q4_K / Q6_K, widths of 1..8
 super-blocks (3, 5, 6, 7 included: row lane groups rounded up to a power of
-two), 1..8 tokens, ragged row counts, and an LM-head-sized Q6_K matrix
+two) and 9..16 super-blocks (two per lane: the attention output and
+DeltaNet ssm_out projections are [2048 x 4096], model.c:862, 1344-1347), 1..8
+tokens, ragged row counts, the split-operand MFMA route for several tokens
+(roaster_dense_mfma_min_tokens), and an LM-head-sized Q6_K matrix
 [248320 x 2048] checked on sampled rows.  Tolerance: max|d|/max|y| <= 2e-5
 (fp32 accumulation in another order; the reference test allows 2e-4)."""
 import ctypes as C
@@ -32,7 +35,7 @@ def run(q6, W, X, rows, cols):
 
 
 @pytest.mark.parametrize("q6", [0, 1])
-@pytest.mark.parametrize("cols", [256, 512, 768, 1280, 1536, 2048])
+@pytest.mark.parametrize("cols", [256, 512, 768, 1280, 1536, 2048, 2304, 3328, 4096])
 @pytest.mark.parametrize("T", [1, 3, 8])
 def test_dense_matvec(q6, cols, T):
     rows = 1001
@@ -49,8 +52,28 @@ def test_dense_matvec_invalid():
     dw, dx, dy = Dev(nbytes=256), Dev(nbytes=256), Dev(nbytes=256)
     L = R.lib()
     assert L.roaster_matvec_q(dw.p, 1, dx.p, dy.p, 4, 300, 1) == R.EINVAL     # cols not a multiple of 256
-    assert L.roaster_matvec_q(dw.p, 1, dx.p, dy.p, 4, 4096, 1) == R.EINVAL    # cols > 2048
+    assert L.roaster_matvec_q(dw.p, 1, dx.p, dy.p, 4, 4352, 1) == R.EINVAL    # cols > 4096
     assert L.roaster_matvec_q(dw.p, 1, dx.p, dy.p, 4, 256, 9) == R.EINVAL     # T > 8
+
+
+@pytest.mark.parametrize("q6", [0, 1])
+@pytest.mark.parametrize("cols", [2048, 4096])
+def test_dense_mfma_route(q6, cols):
+    """8 tokens through the split-operand MFMA GEMM (threshold lowered to 2),
+    rows a multiple of 64, and 7 rows short of one (the matvec again)."""
+    L = R.lib()
+    old = L.roaster_dense_mfma_min_tokens(0)
+    L.roaster_dense_mfma_min_tokens(2)
+    try:
+        for rows in (1024, 1017):
+            W = weights(q6, rows, cols, 60 + cols)
+            X = np.stack([R.synth_normal(61, R.synth_stream(t, cols, 5), cols) for t in range(8)])
+            Y = run(q6, W, X, rows, cols)
+            for t in range(8):
+                err = rel_err(Y[t], O.matvec(q6, W, X[t], rows, cols))
+                assert err <= TOL, (rows, t, err)
+    finally:
+        L.roaster_dense_mfma_min_tokens(old)
 
 
 @pytest.mark.parametrize("q6", [0, 1])
