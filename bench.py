@@ -5,8 +5,8 @@ Headline (value): batch-1 decode through the 40-layer MoE-FFN stack -- hidden
 [512 x 2048], down Q6_K [2048 x 512], F32 router, RMSNorm (eps 1e-6) carried
 between layers -- with every expert resident in HBM (21.05 GB in the GGML layout
 the decode kernels read, plus the 22.9 GB MFMA tile-layout copy the prefill
-GEMMs read).  A step is one token through all 40 layers (one library call, 3
-kernels per layer).  Inputs
+GEMMs read).  A step is one token through all 40 layers (one library call: one
+launch for the whole stack at batch 1, three kernels per layer at batch 8).  Inputs
 and weights are synthetic (seeded) and already in HBM when timing starts.
 
 Also reported in the same JSON line:
@@ -642,7 +642,7 @@ def decode_legs(args, torch, L, R, dev, stream):
                    "gate_up": "Q4_K", "down": "Q6_K", "resident_table_bytes": int(L.roaster_table_bytes(t))},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("decode_b%d_step" % B),
-                     "kernel": "decode stack: %s" % ("dec_layer1_kernel, one launch per layer"
+                     "kernel": "decode stack: %s" % ("dec_stack1_kernel, one launch for all 40 layers"
                                                      if B == 1 and L.roaster_decode_fused_layer(-1)
                                                      else "router, gate/up and down kernels per layer"),
                      "kernel_ms": round(kern_ms, 5), "algorithmic_bytes_per_launch": int(nbytes)},

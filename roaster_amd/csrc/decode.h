@@ -21,6 +21,7 @@ struct DecLayer {
     int q6[3];                            /* routed gate / up / down: 0 = Q4_K, 1 = Q6_K */
     int sq6[3];                           /* shared expert gate / up / down */
 };
+static_assert(sizeof(DecLayer) % 16 == 0, "DecLayer is copied in 16-byte units");
 
 /* One active expert of a decode plan: its matrices and the (token, slot)
  * pairs that use it (pair p = t*9 + k, k = 8 for the shared expert). */
@@ -71,30 +72,40 @@ struct DecArgs {
     const DecActive *ffn_ex;    /* [n] device */
     int ffn_n;
     float *ffn_out;             /* [n x H] or NULL */
-    /* one-launch layer (dec_layer1_kernel): exchange slots, u64 = (epoch << 32) | f32 bits */
+    /* one-launch stack (dec_stack1_kernel): exchange slots, u64 = (epoch << 32) | f32 bits */
     uint64_t *xch;              /* [XCH_U64(E, H, I)] or NULL (then the three-kernel path runs) */
-    uint32_t epoch;             /* this launch's epoch (set per layer by the launch code) */
+    uint32_t epoch;             /* epoch of the launch's first layer (layer i: epoch + i) */
     uint32_t spin;              /* polls before a wait gives up (set by the launch code) */
+    int xl2;                    /* 1: slots read only within the writer's XCD stay in its L2 */
     struct DecXch *xbuf;        /* host side: the buffer behind xch and its epoch counter, or NULL */
 };
 
-/* Exchange regions of the one-launch layer, in u64 slots: the E router
- * logits, XCH_LGP slots apart (each written by one workgroup and read by all:
- * one line each spreads the polling over memory channels), the shared
- * expert's SiLU*up [I], each group's routed SiLU*up [8][I] and each group's
- * routed down outputs [8][H]. */
-#define XCH_LGS(E) ((((E) + 1) + 7) & ~7)
-#define XCH_LGP 16                          /* logit slots 128 bytes apart (one per workgroup) */
+/* Exchange regions of the one-launch stack, in u64 slots; every region
+ * starts on a 128-byte line.  Read across XCDs, each value by one workgroup
+ * per XCD, and each line written by one workgroup (lines shared by writers on
+ * different XCDs are slow to propagate): router logit b [256][16], workgroup
+ * b's shared-expert SiLU*up values [256][16], the 8 routed slots' down
+ * outputs [8][H] and the shared expert's, H/256 rows per workgroup,
+ * [256][16].  Then one region per XCD, written and read within it: its copies
+ * of the logits [256] and the shared SiLU*up [I], its group's routed SiLU*up
+ * [I] and its copy of the next layer's hidden state [H]. */
+#define XCH_LN 16                                   /* slots per line */
 #define XCH_LG(E, H, I) 0
-#define XCH_EHS(E, H, I) (XCH_LGP * XCH_LGS(E))
-#define XCH_EHX(E, H, I) (XCH_EHS(E, H, I) + (I))
-#define XCH_DX(E, H, I) (XCH_EHX(E, H, I) + 8 * (I))
-#define XCH_U64(E, H, I) (XCH_DX(E, H, I) + 8 * (H))
+#define XCH_EHS(E, H, I) ((size_t)256 * XCH_LN)
+#define XCH_DX(E, H, I) (XCH_EHS(E, H, I) + (size_t)256 * XCH_LN)
+#define XCH_DSH(E, H, I) (XCH_DX(E, H, I) + 8 * (size_t)(H))
+#define XCH_LOC0(E, H, I) (XCH_DSH(E, H, I) + (size_t)256 * XCH_LN)
+#define XCH_LOCN(E, H, I) ((size_t)256 + 2 * (size_t)(I) + (size_t)(H))
+#define XCH_LLG(I) ((size_t)0)
+#define XCH_LEHS(I) ((size_t)256)
+#define XCH_LEHX(I) ((size_t)256 + (size_t)(I))
+#define XCH_LH(I) ((size_t)256 + 2 * (size_t)(I))
+#define XCH_U64(E, H, I) (XCH_LOC0(E, H, I) + 8 * XCH_LOCN(E, H, I))
 
-/* Exchange buffer of the one-launch layer: the slots and the last epoch
- * written into them.  Epochs grow by one per launch; before the 32-bit
- * epoch would wrap, the slots are cleared (by a fill kernel) and epochs
- * start again at 1, so a slot never holds a later launch's epoch. */
+/* Exchange buffer of the one-launch stack: the slots and the last epoch
+ * written into them.  Epochs grow by one per layer; before the 32-bit epoch
+ * would wrap, the slots are cleared (by a fill kernel) and epochs start
+ * again at 1, so a slot never holds a later layer's epoch. */
 struct DecXch { uint64_t *p; size_t n; uint32_t epoch; };
 
 /* All layers of A: 3 kernels per layer.  A.plan_g and A.err may be set by the
@@ -102,8 +113,8 @@ struct DecXch { uint64_t *p; size_t n; uint32_t epoch; };
  * the library's own scratch and control words are used. */
 int dec_launch(DecArgs &A);
 int dec_ffn_launch(DecArgs &A);      /* kernel_ffn_fused: gate/up + down kernels */
-/* Whether one token's layers can run as one launch each (dec_layer1_kernel)
- * for these shapes on this device. */
+/* Whether one token's layers can run as one launch (dec_stack1_kernel) for
+ * these shapes on this device. */
 bool dec_layer1_ok(int E, int H, int I, int B);
 /* The library's exchange buffer (allocated and cleared on first use). */
 DecXch *dec_xch_default(int E, int H, int I);

@@ -52,7 +52,7 @@
  * workgroup records the 100 MHz real-time counter at phase boundaries;
  * roaster_phase_ts() copies the [kernel][workgroup][mark] table out. */
 #ifdef ROASTER_PHASE_TS
-__device__ unsigned long long g_phase_ts[3][1024][8];
+__device__ unsigned long long g_phase_ts[4][1024][8];
 #define PHASE_TS(k, i)                                                                      \
     do {                                                                                    \
         if (threadIdx.x == 0 && blockIdx.x < 1024)                                          \
@@ -61,6 +61,12 @@ __device__ unsigned long long g_phase_ts[3][1024][8];
 extern "C" int roaster_phase_ts(unsigned long long *out)
 {
     return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_phase_ts), sizeof(g_phase_ts));
+}
+/* one-launch stack: [last two layers][workgroup][wave 0, wave 1][mark] */
+__device__ unsigned long long g_k1_ts[2][256][2][16];
+extern "C" int roaster_phase_ts_k1(unsigned long long *out)
+{
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_k1_ts), sizeof(g_k1_ts));
 }
 #else
 #define PHASE_TS(k, i) do { } while (0)
@@ -1014,44 +1020,53 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_down_kernel(DecArgs A, i
     PHASE_TS(2, 3);
 }
 
-/* ---- one launch per layer for one token --------------------------------------
- * dec_layer1_kernel runs a whole layer of one token (model.c:1059-1146; in
- * stack mode with the carry h += MoE(RMSNorm(h)), model.c:1352-1358) as one
- * launch of 256 workgroups in 8 groups of 32.  Workgroup b is in group b % 8
- * (the dispatcher places it on XCD b % 8) at index b / 8.  Group k serves
- * routed slot k, the k-th selected expert:
- *   1. every workgroup normalises h (the arithmetic of block_norm_tail),
- *      computes the shared-gate logit itself and dots router row b (b < E)
- *      and its pairs of the shared expert's gate/up rows, and publishes the
- *      logit and the shared SiLU*up values;
- *   2. the E logits are gathered (read directly when the caller gives them)
- *      and ranked: the top 8 by the composite key of topk8_fast (larger
- *      logit, then lower index; NaN and -inf never selected), weights by
- *      topk_finish;
- *   3. the slot's expert: this workgroup's 1/32 of its gate/up row pairs and
- *      of its down rows are loaded together; SiLU*up is published within the
- *      group and gathered; the down rows are dotted and published;
- *   4. workgroup b owns output rows [b H/256, (b + 1) H/256): it gathers the
- *      shared SiLU*up, dots the shared expert's down rows for them (loaded in
- *      step 1), gathers the eight slots' down outputs for them and combines
- *      y = sum_{k=0..7} w_k d_k + sigmoid(s) d_shared in that order
- *      (model.c:1139-1144).
- * Exchanges are relaxed agent-scope 64-bit stores and loads of (epoch, value)
- * slots: a slot is ready once it carries this launch's epoch, so neither
+/* ---- one launch for one token's layer stack ----------------------------------
+ * dec_stack1_kernel runs layers [l0, l0 + n) of one token (model.c:1059-1146 per
+ * layer; in stack mode with the carry h += MoE(RMSNorm(h)), model.c:1352-1358)
+ * as ONE launch of 256 workgroups in 8 groups of 32, one group per XCD (the
+ * group is the XCD a workgroup runs on, so a group shares one L2).  Group k
+ * serves routed slot k, the k-th selected expert.  Per layer:
+ *   1. every workgroup gathers h -- the caller's buffer for the first layer,
+ *      the owners' rows of the previous layer after that -- and normalises it
+ *      (block_norm_tail's arithmetic); wave 1 dots router row b (b < E), wave
+ *      2 the shared-gate vector, waves 4.. this workgroup's pairs of the
+ *      shared expert's gate/up rows; the logit and the shared SiLU*up values
+ *      are published;
+ *   2. wave 0 gathers the E logits and ranks the top 8 (topk8_fast: larger
+ *      logit, then lower index; NaN and -inf never selected; weights by
+ *      topk_finish) while wave 3 gathers the shared SiLU*up values;
+ *   3. the slot's expert: this workgroup's 1/32 of its gate/up row pairs, and
+ *      once those have arrived its 1/32 of the down rows (a burst of about
+ *      40 KB per CU in flight completes about twice as fast as one of 64 KB);
+ *      SiLU*up is published within the group and gathered; the down rows are
+ *      dotted and published;
+ *   4. the next layer's router row, shared-gate vector, shared expert rows and
+ *      norm weights are loaded: they depend on nothing of this layer, and they
+ *      arrive while this layer's outputs are exchanged;
+ *   5. workgroup b owns output rows [b H/256, (b + 1) H/256): it dots the
+ *      shared expert's down rows for them (after step 2), gathers the eight
+ *      slots' down outputs for them, combines y = sum_{k=0..7} w_k d_k +
+ *      sigmoid(s) d_shared in that order (model.c:1139-1144) and publishes
+ *      h + y for the next layer (after the last layer: writes it, or y, to
+ *      the caller's buffer).
+ * Exchanges are 64-bit (epoch, value) slots; layer i of a launch uses epoch
+ * A.epoch + i and a slot is ready once it carries that epoch, so neither
  * fences nor cache maintenance are needed and nothing is cleared between
- * launches.  No workgroup writes h before every workgroup has read it: an
- * owner's rows need every group's down outputs, each group's down outputs
- * need all 32 of its SiLU*up values, and those need the ranking, which comes
- * after each workgroup's h (through the logits when the router runs; with
- * given logits through the SiLU*up values, which need the normalised h).
- * Every wait is bounded (A.spin polls); a wait that gives up sets error bit
- * 2 and the workgroup waits for nothing else in this launch, so the launch
- * always ends.  Sums, dot lane layouts, reductions, softmax and combine are
- * those of the three-kernel path, so results are bit-identical to it.
- * NPG / ND: gate/up pairs and down tasks per wave, fixed at compile time for
- * the common shapes (then every load of a phase is issued unconditionally
- * and each use waits for its own loads only), 0 = from the shapes at run
- * time. */
+ * launches or layers.  Slots read on other XCDs are written with agent-scope
+ * stores (through to memory); slots read only within the writer's XCD (the
+ * group's SiLU*up values) with workgroup-scope stores that stay in the shared
+ * L2, where the readers' agent-scope loads find them (0.23 us one way against
+ * 0.48 across XCDs, measured); A.xl2 = 0 writes those through to memory too.
+ * A slot is rewritten by the next layer only after every reader has read it:
+ * a workgroup publishes layer i + 1 values only after it has gathered h of
+ * layer i + 1, which needs every owner's combine of layer i, which comes after
+ * that owner's top-8 and gathers of layer i.  Every wait is bounded (A.spin
+ * polls); a wait that gives up sets error bit 2 and the workgroup waits for
+ * nothing else, so the launch always ends.  Sums, dot lane layouts,
+ * reductions, softmax and combine are those of the three-kernel path, so
+ * results are bit-identical to it.  NPG / ND: gate/up pairs and down tasks per
+ * wave fixed at compile time for the common shapes (every load of a phase then
+ * straight-line code), 0 = from the shapes at run time. */
 #define K1_T 512
 #define K1_W (K1_T / 64)
 #define K1_G 8
@@ -1062,27 +1077,85 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_down_kernel(DecArgs A, i
 #define K1_MAXI 1024
 #define K1_MAXPG (K1_MAXI / K1_GW / K1_W)               /* gate/up pairs per wave */
 #define K1_MAXD 4                                        /* down tasks per wave */
+#define K1_WR 1                                          /* wave roles: router row */
+#define K1_WGI 2                                         /* shared-gate vector */
+#define K1_WN 3                                          /* norm weights; shared SiLU*up gather */
+#define K1_WS 4                                          /* first shared gate/up pair */
+#define K1_MAXL 64                                       /* layers per launch (descriptors in LDS) */
 
+__device__ __forceinline__ uint64_t xch_word(float v, uint32_t ep)
+{
+    return ((uint64_t)ep << 32) | __builtin_bit_cast(uint32_t, v);
+}
+
+/* A slot read on other XCDs: written through to memory. */
 __device__ __forceinline__ void xch_put(uint64_t *p, float v, uint32_t ep)
 {
-    __hip_atomic_store(p, ((uint64_t)ep << 32) | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p, xch_word(v, ep), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* A slot read only on the writer's XCD: kept in the shared L2 (l2), else as
+ * xch_put. */
+__device__ __forceinline__ void xch_put_xcd(uint64_t *p, float v, uint32_t ep, bool l2)
+{
+    if (l2) __hip_atomic_store(p, xch_word(v, ep), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else xch_put(p, v, ep);
+}
+
+__device__ __forceinline__ uint64_t xch_load(const uint64_t *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* The value of slot p once it carries epoch ep, polling at most spin times
  * (dead: stop waiting). */
-__device__ __forceinline__ float xch_get(const uint64_t *p, uint32_t ep, int &dead, uint32_t spin)
+__device__ __forceinline__ float xch_wait(const uint64_t *p, uint64_t v, uint32_t ep, int &dead, uint32_t spin)
 {
-    uint64_t v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     unsigned it = 0;
     while ((uint32_t)(v >> 32) != ep && !dead) {
         if (++it > spin) {
             dead = 1;
             break;
         }
-        v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_sleep(1);        /* ~64 cycles between polls of one slot */
+        v = xch_load(p);
     }
     return __builtin_bit_cast(float, (uint32_t)v);
+}
+
+__device__ __forceinline__ float xch_get(const uint64_t *p, uint32_t ep, int &dead, uint32_t spin)
+{
+    return xch_wait(p, xch_load(p), ep, dead, spin);
+}
+
+/* The values of slots q[0..N) (those with need bit i) once they carry epoch
+ * ep.  Every round re-polls all slots still missing, their loads in flight
+ * together, so a gather costs the rounds until its last slot is published,
+ * not one round trip per slot; at most spin rounds (dead: stop waiting). */
+template <int N>
+__device__ __forceinline__ void xch_gather(const uint64_t *const (&q)[N], unsigned need, uint32_t ep, int &dead,
+                                           uint32_t spin, float (&o)[N])
+{
+    uint64_t r[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) r[i] = xch_load(q[i]);
+    unsigned it = 0;
+    for (;;) {
+        unsigned miss = 0;
+#pragma unroll
+        for (int i = 0; i < N; i++) miss |= ((need >> i) & 1u) && (uint32_t)(r[i] >> 32) != ep ? 1u << i : 0u;
+        if (!miss || dead) break;
+        if (++it > spin) {
+            dead = 1;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            if ((miss >> i) & 1u) r[i] = xch_load(q[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) o[i] = __builtin_bit_cast(float, (uint32_t)r[i]);
 }
 
 /* q_load with the block type chosen at run time (the type comes from the
@@ -1098,9 +1171,9 @@ __device__ __forceinline__ int q_run_a_t(int q6, int c) { return q6 ? q_run_a<tr
 /* silu(gate_j . x) * (up_j . x) from the lane's chunks of one gate/up row
  * pair, x and its run sums in LDS (gu_row's arithmetic for one token). */
 __device__ __forceinline__ float k1_gu_pair(int g6, int u6, const QChunk2 &ch, const float *xn, const float *xsum,
-                                            bool swz, int nb)
+                                            bool swz, int nb, int lane)
 {
-    const int lane = threadIdx.x & 63, c = lane & 7, lb = lane >> 3;
+    const int c = lane & 7, lb = lane >> 3;
     float pg = 0.0f, pu = 0.0f;
     if (lb < nb) {
         const int ga = lb * RQK + q_run_a_t(g6, c), gb = ga + (g6 ? 64 : 32);
@@ -1124,9 +1197,9 @@ __device__ __forceinline__ float k1_gu_pair(int g6, int u6, const QChunk2 &ch, c
  * and its run sums (down_one_token's arithmetic), reduced over the row's
  * lpr lanes. */
 __device__ __forceinline__ float k1_down_row(int d6, const QChunk &ch, const float *eh, const float *ehs, bool live,
-                                             int lpr)
+                                             int lpr, int lane)
 {
-    const int lane = threadIdx.x & 63, lr = lane % lpr, c = lr & 7, lb = lr >> 3;
+    const int lr = lane % lpr, c = lr & 7, lb = lr >> 3;
     float part = 0.0f;
     if (live) {
         const int ca = lb * RQK + q_run_a_t(d6, c), cb = ca + (d6 ? 64 : 32);
@@ -1138,9 +1211,8 @@ __device__ __forceinline__ float k1_down_row(int d6, const QChunk &ch, const flo
 
 /* Router-row dot of one token (router_body's arithmetic): lane partials over
  * its 8 float4 of the row, then the wave sum. */
-__device__ __forceinline__ float k1_row_dot(const float4 (&w)[8], const float4 *x4, int H, bool swz)
+__device__ __forceinline__ float k1_row_dot(const float4 (&w)[8], const float4 *x4, int H, bool swz, int lane)
 {
-    const int lane = threadIdx.x & 63;
     float acc = 0.0f;
 #pragma unroll
     for (int m = 0; m < 8; m++) {
@@ -1156,6 +1228,21 @@ __device__ __forceinline__ float k1_row_dot(const float4 (&w)[8], const float4 *
     return group_sum<64>(acc);
 }
 
+/* Sixteen slots p[0..16) (one 16-column run of a SiLU*up vector) into dst,
+ * and their sum in sum16's order. */
+__device__ __forceinline__ float k1_gather_run(const uint64_t *p, uint32_t ep, int &dead, uint32_t spin, float *dst)
+{
+    float v[16];
+    const uint64_t *q[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) q[i] = p + i;
+    xch_gather<16>(q, 0xFFFFu, ep, dead, spin, v);
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) *(float4 *)(dst + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+    return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7])) +
+           (((v[8] + v[9]) + (v[10] + v[11])) + ((v[12] + v[13]) + (v[14] + v[15])));
+}
+
 #define K1_SYNC_DEAD()          \
     do {                        \
         if (dead) s_dead = 1;   \
@@ -1163,347 +1250,415 @@ __device__ __forceinline__ float k1_row_dot(const float4 (&w)[8], const float4 *
         dead = s_dead;          \
     } while (0)
 
+/* The loads of layer l that depend on nothing computed in it, by wave role:
+ * router row gw (wave K1_WR), the shared-gate vector (K1_WGI), the norm
+ * weights (K1_WN), this workgroup's shared gate/up pairs (K1_WS .. K1_WS +
+ * SP - 1) and shared down rows (the last nsd waves).  Each wave parks its
+ * loaded bytes in its own LDS stage and reads them back when it uses them
+ * (one wave writes and reads a stage, so no barrier is involved): held in
+ * registers they would stay live across the whole layer loop. */
+union K1Stage {
+    float4 rw[8][64];
+    struct {
+        QChunk2 shc[64];
+        QChunk sdc[64];
+    } s;
+};
+
+template <int TY>
+__device__ __forceinline__ void k1_prefetch(const DecArgs &A, const DecLayer &L, int l, K1Stage *stage, float *nw_s,
+                                            int wv, bool rrow, int SP, int sdt, int RO, int rpw, int lane)
+{
+    const int sg6 = TY < 0 ? L.sq6[0] : (TY >> 3) & 1, su6 = TY < 0 ? L.sq6[1] : (TY >> 4) & 1;
+    const int sd6 = TY < 0 ? L.sq6[2] : (TY >> 5) & 1;
+    const int H = A.H, HU = H / 4, c = lane & 7, lb = lane >> 3;
+    const int nbh = H / RQK, nbi = A.I / RQK, lpr = lanes_per_row(nbi), rw_ = lane / lpr, lr = lane % lpr;
+    const int gw = blockIdx.x;
+    float4 rw[8];
+    QChunk2 shc;
+    QChunk sdc;
+    if (wv == K1_WR && rrow) {
+#pragma unroll
+        for (int m = 0; m < 8; m++) rw[m] = gld_f4(L.router + (size_t)gw * H + min(4 * lane + 256 * m, H - 4));
+#pragma unroll
+        for (int m = 0; m < 8; m++) stage[wv].rw[m][lane] = rw[m];
+    } else if (wv == K1_WGI) {
+#pragma unroll
+        for (int m = 0; m < 8; m++) rw[m] = gld_f4(L.gate_inp + min(4 * lane + 256 * m, H - 4));
+#pragma unroll
+        for (int m = 0; m < 8; m++) stage[wv].rw[m][lane] = rw[m];
+    } else if (wv == K1_WN) {
+        const float *nw = A.do_norm && A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * H : NULL;
+        if (nw) {
+            float4 q[8];
+#pragma unroll
+            for (int m = 0; m < 8; m++) q[m] = ((const float4 *)nw)[min(lane + 64 * m, HU - 1)];
+#pragma unroll
+            for (int m = 0; m < 8; m++)
+                if (lane + 64 * m < HU) ((float4 *)nw_s)[lane + 64 * m] = q[m];
+        }
+    }
+    if (wv >= K1_WS && wv < K1_WS + SP) {
+        const size_t j = (size_t)gw * SP + (wv - K1_WS);
+        shc.g = q_load_t(sg6, L.sgate, j, nbh, lb, c);
+        shc.u = q_load_t(su6, L.sup, j, nbh, lb, c);
+    }
+    if (sdt >= 0) sdc = q_load_t(sd6, L.sdown, (size_t)min(gw * RO + sdt * rpw + rw_, H - 1), nbi, lr >> 3, lr & 7);
+    if (wv >= K1_WS && wv < K1_WS + SP) stage[wv].s.shc[lane] = shc;
+    if (sdt >= 0) stage[wv].s.sdc[lane] = sdc;
+}
+
+/* Layer i of the call from its LDS copy, as wave-uniform (scalar) values. */
+__device__ __forceinline__ DecLayer k1_layer(const DecLayer *Ls, int i)
+{
+    DecLayer L;
+    const uint32_t *s = (const uint32_t *)(Ls + i);
+    uint32_t *d = (uint32_t *)&L;
+#pragma unroll
+    for (int w = 0; w < (int)(sizeof(DecLayer) / 4); w++) d[w] = __builtin_amdgcn_readfirstlane(s[w]);
+    return L;
+}
+
 template <int NPG, int ND, int TY>
-__device__ __forceinline__ void layer1_body(const DecArgs &A, int l)
+__device__ __forceinline__ void stack1_body(const DecArgs &A)
 {
     __shared__ __align__(16) float xn[K1_MAXH];
     __shared__ float xsum[K1_MAXH / 16];
+    __shared__ __align__(16) float hraw[K1_MAXH];           /* this layer's h (the owned rows' residual) */
+    __shared__ __align__(16) float nw_s[K1_MAXH];
     __shared__ __align__(16) float ehk[K1_MAXI];
     __shared__ float ehks[K1_MAXI / 16];
     __shared__ __align__(16) float ehsh[K1_MAXI];
     __shared__ float ehshs[K1_MAXI / 16];
-    __shared__ float lg_s[256];
-    __shared__ __align__(16) unsigned long long ck_s[256];
-    __shared__ int slot_s[RTOPK];
-    __shared__ uint32_t gmax_s[8];
-    __shared__ int ncand_s;
-    __shared__ __align__(16) unsigned long long cand_s[64];
+    __shared__ TopkScratch tks;
     __shared__ int ids_s[RTOPK];
     __shared__ float w_s[RTOPK + 1];
     __shared__ float red_s[4];
-    __shared__ float sg_s;
-    __shared__ float dk_s[RTOPK][K1_MAXH / 256];
-    __shared__ float dsh_s[K1_MAXH / 256];
+    __shared__ __align__(16) DecLayer Ls[K1_MAXL];
+    __shared__ K1Stage stage_s[K1_W];
     __shared__ int s_dead, s_err;
 
     const int H = A.H, I = A.I, E = A.E, HU = H / 4, nbh = H / RQK, nbi = I / RQK;
-    const int tid = threadIdx.x, lane = tid & 63, wv = wave_id(), c = lane & 7, lb = lane >> 3;
-    const int grp = blockIdx.x % K1_G, gi = blockIdx.x / K1_G, gw = blockIdx.x;
-    const uint32_t ep = A.epoch;
-    const DecLayer L = A.layers[l];
-    /* matrix types: from the descriptor, or fixed by TY (bit k: routed gate,
-     * up, down, shared gate, up, down is Q6_K) so that every load of a phase
-     * is straight-line code and each use waits for its own loads only */
-    const int g6 = TY < 0 ? L.q6[0] : (TY & 1), u6 = TY < 0 ? L.q6[1] : (TY >> 1) & 1;
-    const int d6 = TY < 0 ? L.q6[2] : (TY >> 2) & 1, sg6 = TY < 0 ? L.sq6[0] : (TY >> 3) & 1;
-    const int su6 = TY < 0 ? L.sq6[1] : (TY >> 4) & 1, sd6 = TY < 0 ? L.sq6[2] : (TY >> 5) & 1;
+    const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
+    /* group = the XCD this workgroup runs on: the dispatcher deals the grid's
+     * workgroups to the 8 XCDs in turn, starting at an XCD that varies from
+     * launch to launch, so XCD(b) = (b + r) % 8 with one r per launch and
+     * b / 8 numbers the 32 workgroups of each XCD (the library checks the
+     * pattern once per process; without it groups are b % 8 and every slot
+     * goes through memory) */
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 0xFu;
+    const bool l2 = A.xl2 && xcc < (unsigned)K1_G;
+    if (A.xl2 && !l2 && threadIdx.x == 0) atomicOr(A.err, 4);
+    const int grp = l2 ? (int)xcc : (int)(blockIdx.x % K1_G), gi = blockIdx.x / K1_G, gw = blockIdx.x;
     const bool swz = A.xswz;
-    uint64_t *xlg = A.xch + XCH_LG(E, H, I);
+    uint64_t *xlg = A.xch + XCH_LG(E, H, I);                 /* across XCDs */
     uint64_t *xehs = A.xch + XCH_EHS(E, H, I);
-    uint64_t *xehx = A.xch + XCH_EHX(E, H, I) + (size_t)grp * I;
     uint64_t *xdx = A.xch + XCH_DX(E, H, I);
+    uint64_t *xdsh = A.xch + XCH_DSH(E, H, I);
+    uint64_t *loc = A.xch + XCH_LOC0(E, H, I) + (size_t)grp * XCH_LOCN(E, H, I);   /* this XCD's */
+    uint64_t *llg = loc + XCH_LLG(I), *lehs = loc + XCH_LEHS(I), *lehx = loc + XCH_LEHX(I), *lh = loc + XCH_LH(I);
+    const int RO = H / 256;                                  /* shared down rows of this workgroup */
+    const int SP = I / 256;                                  /* shared gate/up pairs of this workgroup */
+    const int RD = H / K1_GW;                                /* routed down rows; rows combined */
+    const int LPW = E / K1_GW, SPW = I / K1_GW;              /* logits, shared SiLU*up relayed into the XCD */
+    const int lpr = lanes_per_row(nbi), rpw = 64 / lpr;
+    const int nsd = (RO + rpw - 1) / rpw;                    /* shared down tasks */
+    const int sdt = wv - (K1_W - nsd);
+    const bool rrow = gw < E && !A.logits_in;                /* this workgroup dots router row gw */
+    const int n = A.nlayers;
 #ifdef ROASTER_PHASE_TS
-    unsigned long long tsv[12];
-#define K1_TS(i) asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(tsv[i]) : : "memory")
+    unsigned long long tsv[2][16] = {};
+    int tsl = 0;
+#define K1_TS(i) asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(tsv[tsl][i]) : : "memory")
 #else
 #define K1_TS(i) ((void)0)
 #endif
-    K1_TS(0);
     if (tid == 0) {
         s_dead = 0;
         s_err = 0;
     }
 
-    /* ---- 1. loads that need nothing.  h (with the norm weights and the
-     * owned rows' residual) first; then, by wave: 0 router row gw, 1 the
-     * shared-gate vector, 2 .. 1 + SP the shared gate/up pairs, the last nsd
-     * waves the owned rows of the shared down matrix.  h is stored to LDS in
-     * each branch after its loads, so the store waits for h only (a wave's
-     * loads complete in order); a distinct marker after each store keeps the
-     * compiler from merging the stores past the join. */
-    const float4 hq = ((const float4 *)A.h)[min(tid, HU - 1)];
-    /* error bit 2 from an earlier launch that gave up: wait for nothing (read
-     * after h is requested; first needed at the first wait) */
+    /* first layer: h (threads < 256: units t and t + 256), then the weights
+     * of the layer */
+    float4 hq[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) hq[k] = ((const float4 *)A.h)[min(tid + 256 * k, HU - 1)];
+    /* error bit 2 from an earlier launch that gave up: wait for nothing */
     int dead = (gld_u32(A.err) & 2u) != 0;
-    const float *nw = A.do_norm && A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * H : NULL;
-    const float4 wq = nw ? ((const float4 *)nw)[xpos(min(tid, HU - 1), swz)] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-    const int RO = H / 256;                                  /* output rows owned */
-    const float hv = A.y ? 0.0f : A.h[gw * RO + min(tid, RO - 1)];
-    const int SP = I / 256;                                  /* shared gate/up pairs of this workgroup */
-    const int lpr = lanes_per_row(nbi), rpw = 64 / lpr, rw_ = lane / lpr, lr = lane % lpr, lbd = lr >> 3;
-    const int nsd = (RO + rpw - 1) / rpw;                    /* shared down tasks */
-    const int sdt = wv - (K1_W - nsd);
-    const bool rrow = gw < E && !A.logits_in;                /* this workgroup dots router row gw */
-    float4 rw[8];
-    QChunk2 shc;
-    QChunk sdc;
-#define K1_STORE_H(tag)                                                       \
-    do {                                                                      \
-        ((float4 *)xn)[xpos(min(tid, HU - 1), swz)] = hq;                     \
-        asm volatile("; h stored, " tag);                                     \
-    } while (0)
-    if (wv == 0 && rrow) {
-#pragma unroll
-        for (int m = 0; m < 8; m++) rw[m] = gld_f4(L.router + (size_t)gw * H + min(4 * lane + 256 * m, H - 4));
-        K1_STORE_H("router row");
-    } else if (wv == 1) {
-#pragma unroll
-        for (int m = 0; m < 8; m++) rw[m] = gld_f4(L.gate_inp + min(4 * lane + 256 * m, H - 4));
-        K1_STORE_H("shared-gate vector");
-    } else if (wv >= 2 && wv < 2 + SP) {
-        const size_t j = (size_t)gw * SP + (wv - 2);
-        shc.g = q_load_t(sg6, L.sgate, j, nbh, lb, c);
-        shc.u = q_load_t(su6, L.sup, j, nbh, lb, c);
-        K1_STORE_H("shared gate/up");
-    } else if (sdt >= 0) {
-        sdc = q_load_t(sd6, L.sdown, (size_t)min(gw * RO + sdt * rpw + rw_, H - 1), nbi, lbd, lr & 7);
-        K1_STORE_H("shared down");
-    } else {
-        K1_STORE_H("no rows");
-    }
-#undef K1_STORE_H
+    /* the call's layer descriptors into LDS (read there from the second layer
+     * on: a scalar load in flight would hold every LDS wait) */
+    constexpr int DQ = (int)(sizeof(DecLayer) / 16);
+    const uint4 lq = ((const uint4 *)(A.layers + A.layer0))[min(tid, n * DQ - 1)];
+    DecLayer L = A.layers[A.layer0];
+    k1_prefetch<TY>(A, L, A.layer0, stage_s, nw_s, wv, rrow, SP, sdt, RO, rpw, lane);
 
-    /* ---- 2. normalised input (block_norm_tail for one token) ------------- */
-    __syncthreads();
-    float4 *x4 = (float4 *)xn;
-    if (A.do_norm) {
+    for (int li = 0; li < n; li++) {
+        /* the thread index as a value opaque to the compiler, per layer: else
+         * every lane-derived address is hoisted out of this loop and stays
+         * live across it (spilling) */
+        int tid_v = (int)threadIdx.x;
+        asm volatile("" : "+v"(tid_v));
+        const int tid = tid_v, lane = tid_v & 63, c = lane & 7, lb = lane >> 3;
+        const int rw_ = lane / lpr, lr = lane % lpr, lbd = lr >> 3;
+        const int l = A.layer0 + li;
+        const uint32_t ep = A.epoch + (uint32_t)li;
+        const bool last = li + 1 == n;
+        const float *nwl = A.do_norm && A.norm_w ? nw_s : NULL;
+        /* matrix types: from the descriptor, or fixed by TY (bit k: routed
+         * gate, up, down, shared gate, up, down is Q6_K) so that every load of
+         * a phase is straight-line code and each use waits for its own loads */
+        const int g6 = TY < 0 ? L.q6[0] : (TY & 1), u6 = TY < 0 ? L.q6[1] : (TY >> 1) & 1;
+        const int d6 = TY < 0 ? L.q6[2] : (TY >> 2) & 1, sg6 = TY < 0 ? L.sq6[0] : (TY >> 3) & 1;
+        const int su6 = TY < 0 ? L.sq6[1] : (TY >> 4) & 1, sd6 = TY < 0 ? L.sq6[2] : (TY >> 5) & 1;
+#ifdef ROASTER_PHASE_TS
+        tsl = li + 1 == n ? 1 : 0;
+#endif
+        K1_TS(0);
+        /* ---- 1. h (after the first layer: this XCD's copy), normalised ------ */
+        if (li > 0 && tid < 256) {
+            const uint64_t *q[8];
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) q[i] = lh + 4 * (size_t)min(tid + 256 * (i >> 2), HU - 1) + (i & 3);
+            xch_gather<8>(q, (tid < HU ? 0x0Fu : 0u) | (tid + 256 < HU ? 0xF0u : 0u), ep - 1, dead, A.spin, v);
+            hq[0] = make_float4(v[0], v[1], v[2], v[3]);
+            hq[1] = make_float4(v[4], v[5], v[6], v[7]);
+        }
+        float4 *x4 = (float4 *)xn;
+        if (li == 0 && n > 1 && tid < n * DQ) ((uint4 *)Ls)[tid] = lq;
         if (tid < 256) {
             float ss = 0.0f;
 #pragma unroll
             for (int k = 0; k < 2; k++) {
                 const int u = tid + k * 256;
                 if (u < HU) {
-                    const float4 v = x4[u];
+                    const float4 v = hq[k];
                     ss = fmaf(v.x, v.x, ss);
                     ss = fmaf(v.y, v.y, ss);
                     ss = fmaf(v.z, v.z, ss);
                     ss = fmaf(v.w, v.w, ss);
+                    x4[xpos(u, swz)] = v;
+                    ((float4 *)hraw)[u] = v;
                 }
             }
             ss = group_sum<64>(ss);
             if (lane == 0) red_s[wv] = ss;
         }
-        __syncthreads();
-        float s2 = 0.0f;
+        K1_SYNC_DEAD();
+        if (dead) break;                                  /* workgroup-uniform */
+        K1_TS(1);
+        if (tid < H / 16) {
+            float inv = 1.0f;
+            if (A.do_norm) {
+                float s2 = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; w++) s2 += red_s[w];
-        const float inv = 1.0f / sqrtf(s2 / (float)H + A.eps);
-        if (tid < HU) {
-            float4 v = x4[tid];
-            v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
-            if (nw) { v.x *= wq.x; v.y *= wq.y; v.z *= wq.z; v.w *= wq.w; }
-            x4[tid] = v;
+                for (int w = 0; w < 4; w++) s2 += red_s[w];
+                inv = 1.0f / sqrtf(s2 / (float)H + A.eps);
+            }
+            float4 q[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int u = 4 * tid + i;
+                float4 v = x4[xpos(u, swz)];
+                if (A.do_norm) {
+                    v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
+                    if (nwl) {
+                        const float4 wq = ((const float4 *)nwl)[u];
+                        v.x *= wq.x; v.y *= wq.y; v.z *= wq.z; v.w *= wq.w;
+                    }
+                    x4[xpos(u, swz)] = v;
+                }
+                q[i] = v;
+            }
+            xsum[tid] = ((q[0].x + q[0].y) + (q[0].z + q[0].w)) + ((q[1].x + q[1].y) + (q[1].z + q[1].w)) +
+                        (((q[2].x + q[2].y) + (q[2].z + q[2].w)) + ((q[3].x + q[3].y) + (q[3].z + q[3].w)));
         }
         __syncthreads();
-    }
-    for (int r = tid; r < H / 16; r += K1_T) {
-        const float4 a = x4[xpos(4 * r, swz)], b = x4[xpos(4 * r + 1, swz)];
-        const float4 cc = x4[xpos(4 * r + 2, swz)], d = x4[xpos(4 * r + 3, swz)];
-        xsum[r] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)) +
-                  (((cc.x + cc.y) + (cc.z + cc.w)) + ((d.x + d.y) + (d.z + d.w)));
-    }
-    __syncthreads();
-    K1_TS(1);
+        K1_TS(2);
 
-    /* ---- 3. router logit, shared-gate logit, shared SiLU*up -------------- */
-    if (wv == 0 && rrow) {
-        const float s = k1_row_dot(rw, x4, H, swz);
-        if (lane == 0) {
-            xch_put(xlg + (size_t)gw * XCH_LGP, s, ep);
-            A.logits[gw] = s;
+        /* ---- 2. router logit, shared-gate logit, shared SiLU*up ----------- */
+        if (wv == K1_WR && rrow) {
+            float4 rw[8];
+#pragma unroll
+            for (int m = 0; m < 8; m++) rw[m] = stage_s[wv].rw[m][lane];
+            const float s = k1_row_dot(rw, x4, H, swz, lane);
+            if (lane == 0) {
+                xch_put(xlg + (size_t)gw * XCH_LN, s, ep);
+                if (last) A.logits[gw] = s;
+            }
+        } else if (wv == K1_WGI) {
+            float4 rw[8];
+#pragma unroll
+            for (int m = 0; m < 8; m++) rw[m] = stage_s[wv].rw[m][lane];
+            const float s = k1_row_dot(rw, x4, H, swz, lane);
+            if (lane == 0) w_s[RTOPK] = 1.0f / (1.0f + expf(-s));
         }
-    } else if (wv == 1) {
-        const float s = k1_row_dot(rw, x4, H, swz);
-        if (lane == 0) sg_s = s;
-    } else if (wv >= 2 && wv < 2 + SP) {
-        const float eh = k1_gu_pair(sg6, su6, shc, xn, xsum, swz, nbh);
-        if (lane == 0) xch_put(xehs + (size_t)gw * SP + (wv - 2), eh, ep);
-    }
-    K1_TS(2);
+        if (wv >= K1_WS && wv < K1_WS + SP) {
+            const float eh = k1_gu_pair(sg6, su6, stage_s[wv].s.shc[lane], xn, xsum, swz, nbh, lane);
+            if (lane == 0) xch_put(xehs + (size_t)gw * XCH_LN + (wv - K1_WS), eh, ep);
+        }
+        K1_TS(3);
+        /* ---- 3. wave 0 relays this workgroup's share of the logits (lanes <
+         * LPW) and of the shared SiLU*up values (lanes 32..) into this XCD's
+         * region, then gathers the E logits from there and ranks the top 8;
+         * wave 3 gathers the shared SiLU*up values from there ---------------- */
+        if (wv == 0) {
+            const bool rl_lg = lane < LPW && !A.logits_in, rl_sh = lane >= 32 && lane - 32 < SPW;
+            /* logit j is line j's slot 0; shared value j is slot j % SP of line j / SP */
+            const int j = rl_lg ? gi * LPW + lane : rl_sh ? gi * SPW + lane - 32 : 0;
+            if (rl_lg || rl_sh) {
+                const float v = xch_get(rl_lg ? xlg + (size_t)j * XCH_LN : xehs + (size_t)(j / SP) * XCH_LN + j % SP, ep,
+                                        dead, A.spin);
+                xch_put_xcd((rl_lg ? llg : lehs) + j, v, ep, l2);
+            }
+            K1_TS(13);
+            float v4[4];
+            if (A.logits_in) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) v4[i] = A.logits_in[min(lane + 64 * i, E - 1)];
+            } else {
+                const uint64_t *q[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) q[i] = llg + min(lane + 64 * i, E - 1);
+                xch_gather<4>(q, 0xFu, ep, dead, A.spin, v4);
+            }
+            K1_TS(10);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (lane + 64 * i >= E) v4[i] = -INFINITY;
+            topk8_fast(v4, E, ids_s, w_s, &s_err, &tks);
+        } else if (wv == K1_WN && lane < I / 16) {
+            ehshs[lane] = k1_gather_run(lehs + 16 * lane, ep, dead, A.spin, ehsh + 16 * lane);
+        }
+        K1_SYNC_DEAD();
+        K1_TS(4);
+        if (gw == 0) {
+            if (tid < RTOPK) {
+                const size_t o = (size_t)li * RTOPK + tid;
+                if (A.ids_out) A.ids_out[o] = ids_s[tid];
+                if (A.w_out) A.w_out[o] = w_s[tid];
+            }
+            if (tid == 0 && s_err) atomicOr(A.err, 1);
+        }
 
-    /* ---- 4. the logits; top-8 by rank ------------------------------------ */
-    if (tid < E) lg_s[tid] = A.logits_in ? A.logits_in[tid] : xch_get(xlg + (size_t)tid * XCH_LGP, ep, dead, A.spin);
-    if (tid < RTOPK) slot_s[tid] = -1;
-    if (tid == 0) ncand_s = 0;
-    K1_SYNC_DEAD();
-    K1_TS(3);
-    /* Every selected key is at least T = the smallest of the 8 maxima of
-     * aligned groups of 32 keys (those maxima are 8 keys >= T), so only the
-     * candidates key >= T (typically 15-25) are ranked; with more than 64 of
-     * them (ties at T, or a group without a selectable logit) every key is
-     * ranked against all 256.  Either way slot r holds the key with r larger
-     * composite keys: the order of topk8_fast. */
-    uint32_t key = 0u;
-    if (tid < 256) {
-        key = tid < E ? logit_key(lg_s[tid]) : 0u;
-        uint32_t g = key;
-        g = max(g, (uint32_t)dpp_i<DPP_XOR1>((int)g));
-        g = max(g, (uint32_t)dpp_i<DPP_XOR2>((int)g));
-        g = max(g, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)g));
-        g = max(g, (uint32_t)dpp_i<DPP_MIRROR>((int)g));
-        const uint32_t glo = max((uint32_t)__builtin_amdgcn_readlane((int)g, 0), (uint32_t)__builtin_amdgcn_readlane((int)g, 16));
-        const uint32_t ghi = max((uint32_t)__builtin_amdgcn_readlane((int)g, 32), (uint32_t)__builtin_amdgcn_readlane((int)g, 48));
-        if (lane == 0) {
-            gmax_s[2 * wv] = glo;
-            gmax_s[2 * wv + 1] = ghi;
+        /* ---- 4. the slot's expert -------------------------------------------- */
+        const int e = ids_s[grp];
+        const bool live_slot = e >= 0;
+        const size_t ee = live_slot ? (size_t)e : 0;          /* an unselected slot reads expert 0, unused */
+        const uint8_t *ge = L.gate + ee * L.eb[0], *ue = L.up + ee * L.eb[1], *de = L.down + ee * L.eb[2];
+        const int RGP = I / K1_GW, npg = NPG ? NPG : (RGP + K1_W - 1) / K1_W;
+        const int ndt = (RD + rpw - 1) / rpw, nd = ND ? ND : (ndt + K1_W - 1) / K1_W;
+        constexpr int MPG = NPG ? NPG : K1_MAXPG, MD = ND ? ND : K1_MAXD;
+        QChunk2 gch[MPG];
+        QChunk dch[MD];
+#pragma unroll
+        for (int f = 0; f < MPG; f++) {
+            if (NPG || f < npg) {
+                const size_t j = (size_t)gi * RGP + min(wv + f * K1_W, RGP - 1);
+                gch[f].g = q_load_t(g6, ge, j, nbh, lb, c);
+                gch[f].u = q_load_t(u6, ue, j, nbh, lb, c);
+            }
         }
-    }
-    __syncthreads();
-    if (tid < 256) {
-        uint32_t T = gmax_s[0];
-#pragma unroll
-        for (int i = 1; i < 8; i++) T = min(T, gmax_s[i]);
-        const bool cand = key != 0u && key >= T;
-        const uint64_t bal = __ballot(cand);
-        int base = 0;
-        if (lane == 0 && bal) base = atomicAdd(&ncand_s, __popcll(bal));
-        base = __builtin_amdgcn_readfirstlane(base);
-        const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-        if (cand && pos < 64) cand_s[pos] = topk_ck(key, tid);
-        ck_s[tid] = topk_ck(key, tid);
-    }
-    __syncthreads();
-    const int ncand = ncand_s;
-    if (ncand > 64) {                                   /* workgroup-uniform */
-        const int k = tid >> 1, half = tid & 1;         /* two threads per key, half the table each */
-        const unsigned long long my = ck_s[k];
-        const ulonglong2 *t2 = (const ulonglong2 *)ck_s + half * 64;
-        int rank = 0;
-#pragma unroll
-        for (int j0 = 0; j0 < 64; j0 += 16) {
-            ulonglong2 v[16];
-#pragma unroll
-            for (int u = 0; u < 16; u++) v[u] = t2[j0 + u];
-#pragma unroll
-            for (int u = 0; u < 16; u++) rank += (v[u].x > my ? 1 : 0) + (v[u].y > my ? 1 : 0);
+        /* the shared expert's down rows [gw RO, (gw + 1) RO) while the routed
+         * rows are in flight (its SiLU*up values came with the top-8): slot 8
+         * of the down outputs */
+        if (sdt >= 0) {
+            const int rl = sdt * rpw + rw_;
+            const bool live = rl < RO && lbd < nbi;
+            const float part = k1_down_row(sd6, stage_s[wv].s.sdc[lane], ehsh, ehshs, live, lpr, lane);
+            if (live && lr == 0) xch_put(xdsh + (size_t)gw * XCH_LN + rl, part, ep);
         }
-        rank += dpp_i<DPP_XOR1>(rank);
-        if (!half && k < E && (uint32_t)(my >> 32) != 0u && rank < RTOPK) slot_s[rank] = k;
-        __syncthreads();
-    } else if (wv == 0) {
-        const unsigned long long my = lane < ncand ? cand_s[lane] : 0ull;
-        int rank = 0;
-        for (int j0 = 0; j0 < ncand; j0 += 16) {
-            unsigned long long v[16];
+        /* the down rows once the gate/up rows have arrived (loads complete in
+         * order: waiting for the last one waits for all) */
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("; gate/up rows arrived" ::"v"(gch[(NPG ? NPG : 1) - 1].u.dd), "v"(gch[(NPG ? NPG : 1) - 1].u.q.x)
+                     : "memory");
 #pragma unroll
-            for (int u = 0; u < 16; u++) v[u] = cand_s[min(j0 + u, 63)];
+        for (int f = 0; f < MD; f++) {
+            if (ND || f < nd) {
+                const int task = min(wv + f * K1_W, ndt - 1);
+                dch[f] = q_load_t(d6, de, (size_t)min(gi * RD + task * rpw + rw_, H - 1), nbi, lbd, lr & 7);
+            }
+        }
+        K1_TS(5);
 #pragma unroll
-            for (int u = 0; u < 16; u++) rank += (j0 + u < ncand && v[u] > my) ? 1 : 0;
+        for (int f = 0; f < MPG; f++) {
+            const int pj = wv + f * K1_W;
+            if ((NPG || f < npg) && pj < RGP) {
+                const float eh = k1_gu_pair(g6, u6, gch[f], xn, xsum, swz, nbh, lane);
+                if (lane == 0) xch_put_xcd(lehx + (size_t)gi * RGP + pj, live_slot ? eh : 0.0f, ep, l2);
+            }
         }
-        if (lane < ncand && rank < RTOPK) slot_s[rank] = 255 - (int)(uint32_t)my;
-        __builtin_amdgcn_s_waitcnt(LGKM_ONLY);
-        __builtin_amdgcn_wave_barrier();
-    }
-    if (wv == 0) {
-        const int id = lane < RTOPK ? slot_s[lane] : -1;
-        const int nsel = __popcll(__ballot(id >= 0));       /* the ranks fill a prefix of the slots */
-        const float v = id >= 0 ? key_logit(logit_key(lg_s[id])) : -INFINITY;
-        topk_finish(v, id, nsel, ids_s, w_s, &s_err);
-        if (lane == 0) w_s[RTOPK] = 1.0f / (1.0f + expf(-sg_s));
-    }
-    __syncthreads();
-    K1_TS(4);
-    if (gw == 0) {
-        if (tid < RTOPK) {
-            const size_t o = (size_t)(l - A.layer0) * RTOPK + tid;
-            if (A.ids_out) A.ids_out[o] = ids_s[tid];
-            if (A.w_out) A.w_out[o] = w_s[tid];
+        K1_TS(6);
+        if (wv == 0 && lane < I / 16) ehks[lane] = k1_gather_run(lehx + 16 * lane, ep, dead, A.spin, ehk + 16 * lane);
+        K1_SYNC_DEAD();
+        K1_TS(7);
+#pragma unroll
+        for (int f = 0; f < MD; f++) {
+            const int task = wv + f * K1_W;
+            if ((ND || f < nd) && task < ndt) {
+                const int rl = task * rpw + rw_, row = gi * RD + rl;
+                const bool live = rl < RD && lbd < nbi;
+                const float part = k1_down_row(d6, dch[f], ehk, ehks, live, lpr, lane);
+                if (live && lr == 0) xch_put(xdx + (size_t)grp * H + row, live_slot ? part : 0.0f, ep);
+            }
         }
-        if (tid == 0 && s_err) atomicOr(A.err, 1);
-    }
+        K1_TS(8);
 
-    /* ---- 5. the slot's expert: gate/up pairs and down rows loaded together */
-    const int e = ids_s[grp];
-    const bool live_slot = e >= 0;
-    const size_t ee = live_slot ? (size_t)e : 0;              /* an unselected slot reads expert 0, unused */
-    const uint8_t *ge = L.gate + ee * L.eb[0], *ue = L.up + ee * L.eb[1], *de = L.down + ee * L.eb[2];
-    const int RGP = I / K1_GW, npg = NPG ? NPG : (RGP + K1_W - 1) / K1_W;
-    const int RD = H / K1_GW, ndt = (RD + rpw - 1) / rpw, nd = ND ? ND : (ndt + K1_W - 1) / K1_W;
-    constexpr int MPG = NPG ? NPG : K1_MAXPG, MD = ND ? ND : K1_MAXD;
-    QChunk2 gch[MPG];
-    QChunk dch[MD];
-#pragma unroll
-    for (int f = 0; f < MPG; f++) {
-        if (NPG || f < npg) {
-            const size_t j = (size_t)gi * RGP + min(wv + f * K1_W, RGP - 1);
-            gch[f].g = q_load_t(g6, ge, j, nbh, lb, c);
-            gch[f].u = q_load_t(u6, ue, j, nbh, lb, c);
+        /* ---- 5. the next layer's loads; this XCD's rows [gi RD, (gi + 1) RD)
+         * of h: the nine slots' down outputs combined -------------------------- */
+        if (!last) {
+            L = k1_layer(Ls, li + 1);
+            k1_prefetch<TY>(A, L, l + 1, stage_s, nw_s, wv, rrow, SP, sdt, RO, rpw, lane);
         }
-    }
+        K1_TS(11);
+        if (wv == 0) {
+            const int row = gi * RD + min(lane, RD - 1);
+            const uint64_t *q[RTOPK + 1];
+            float d[RTOPK + 1];
 #pragma unroll
-    for (int f = 0; f < MD; f++) {
-        if (ND || f < nd) {
-            const int task = min(wv + f * K1_W, ndt - 1);
-            dch[f] = q_load_t(d6, de, (size_t)min(gi * RD + task * rpw + rw_, H - 1), nbi, lbd, lr & 7);
+            for (int k = 0; k < RTOPK; k++) q[k] = xdx + (size_t)k * H + row;
+            q[RTOPK] = xdsh + (size_t)(row / RO) * XCH_LN + row % RO;
+            xch_gather<RTOPK + 1>(q, lane < RD ? 0x1FFu : 0u, ep, dead, A.spin, d);
+            K1_TS(12);
+            if (lane < RD) {
+                float y = 0.0f;
+#pragma unroll
+                for (int k = 0; k < RTOPK; k++) y = fmaf(w_s[k], d[k], y);
+                y = fmaf(w_s[RTOPK], d[RTOPK], y);
+                const float hn = hraw[row] + y;
+                if (!last) xch_put_xcd(lh + row, hn, ep, l2);
+                else if (grp == 0) {
+                    if (A.y) A.y[row] = y;
+                    else A.h[row] = hn;
+                }
+            }
         }
+        K1_TS(9);
     }
-#pragma unroll
-    for (int f = 0; f < MPG; f++) {
-        const int pj = wv + f * K1_W;
-        if ((NPG || f < npg) && pj < RGP) {
-            const float eh = k1_gu_pair(g6, u6, gch[f], xn, xsum, swz, nbh);
-            if (lane == 0) xch_put(xehx + (size_t)gi * RGP + pj, live_slot ? eh : 0.0f, ep);
-        }
-        if (f == 0) K1_TS(5);
-    }
-    K1_TS(6);
-    for (int t = tid; t < I; t += K1_T) ehk[t] = xch_get(xehx + t, ep, dead, A.spin);
-    K1_SYNC_DEAD();
-    K1_TS(7);
-    for (int r = tid; r < I / 16; r += K1_T) ehks[r] = sum16(ehk + r * 16);
-    __syncthreads();
-#pragma unroll
-    for (int f = 0; f < MD; f++) {
-        const int task = wv + f * K1_W;
-        if ((ND || f < nd) && task < ndt) {
-            const int rl = task * rpw + rw_, row = gi * RD + rl;
-            const bool live = rl < RD && lbd < nbi;
-            const float part = k1_down_row(d6, dch[f], ehk, ehks, live, lpr);
-            if (live && lr == 0) xch_put(xdx + (size_t)grp * H + row, live_slot ? part : 0.0f, ep);
-        }
-    }
-    K1_TS(8);
-
-    /* ---- 6. owned rows: shared down, the eight slots' outputs, combine ---- */
-    for (int t = tid; t < I; t += K1_T) ehsh[t] = xch_get(xehs + t, ep, dead, A.spin);
-    K1_SYNC_DEAD();
-    K1_TS(9);
-    for (int r = tid; r < I / 16; r += K1_T) ehshs[r] = sum16(ehsh + r * 16);
-    __syncthreads();
-    if (sdt >= 0) {
-        const int rl = sdt * rpw + rw_;
-        const bool live = rl < RO && lbd < nbi;
-        const float part = k1_down_row(sd6, sdc, ehsh, ehshs, live, lpr);
-        if (live && lr == 0) dsh_s[rl] = part;
-    }
-    if (tid < RTOPK * RO) {
-        const int k = tid / RO, rl = tid % RO;
-        dk_s[k][rl] = xch_get(xdx + (size_t)k * H + gw * RO + rl, ep, dead, A.spin);
-    }
-    K1_SYNC_DEAD();
-    K1_TS(10);
-    if (tid < RO) {
-        float y = 0.0f;
-#pragma unroll
-        for (int k = 0; k < RTOPK; k++) y = fmaf(w_s[k], dk_s[k][tid], y);
-        y = fmaf(w_s[RTOPK], dsh_s[tid], y);
-        const int row = gw * RO + tid;
-        if (A.y) A.y[row] = y;
-        else A.h[row] = hv + y;
-    }
-    if (tid == 0 && dead) atomicOr(A.err, 2);
-    K1_TS(11);
+    if (tid == 0 && (dead || s_dead)) atomicOr(A.err, 2);
 #ifdef ROASTER_PHASE_TS
-    if (tid == 0)
-        for (int i = 0; i < 12; i++) g_phase_ts[i >> 3][blockIdx.x][i & 7] = tsv[i];
+    if (threadIdx.x == 0 || threadIdx.x == 64)
+        for (int k = 0; k < 2; k++)
+            for (int i = 0; i < 16; i++) g_k1_ts[k][blockIdx.x][threadIdx.x >> 6][i] = tsv[k][i];
 #endif
 #undef K1_TS
 }
 
-extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_layer1_kernel(DecArgs A, int l) { layer1_body<0, 0, -1>(A, l); }
+extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stack1_kernel(DecArgs A) { stack1_body<0, 0, -1>(A); }
 /* hidden 2048, inter 512: two gate/up pairs and two down tasks per wave;
  * gate/up Q4_K and down Q6_K, routed and shared (types 0b100100) */
-extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_layer1_2x2_kernel(DecArgs A, int l) { layer1_body<2, 2, 0x24>(A, l); }
+extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stack1_2x2_kernel(DecArgs A) { stack1_body<2, 2, 0x24>(A); }
+
+/* Every workgroup's XCC_ID, in a grid of the stack kernel's shape. */
+extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_xcd_probe_kernel(unsigned *out)
+{
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    if (threadIdx.x == 0) out[blockIdx.x] = xcc & 0xFu;
+}
 
 /* Clears an exchange buffer (before epochs start again at 1). */
 extern "C" __global__ void dec_xch_clear_kernel(uint64_t *p, size_t n)
@@ -1597,26 +1752,66 @@ DecXch *dec_xch_default(int E, int H, int I)
     return &g_xch;
 }
 
-/* One launch per layer (dec_layer1_kernel) on the exchange buffer A.xbuf. */
-static int launch_layer1(DecArgs &A)
+/* Whether the dispatcher deals the stack kernel's grid to the XCDs in turn,
+ * XCC_ID(b) = (b + r) % 8 (then a group is an XCD and its SiLU*up slots stay
+ * in its L2): -1 = not probed yet. */
+static int g_xl2 = -1;
+
+int dec_probe_placement()
 {
-    DecXch &X = *A.xbuf;
-    A.xch = X.p;
-    for (int l = A.layer0; l < A.layer0 + A.nlayers; l++) {
-        if (X.epoch == 0xFFFFFFFFu) {                 /* epochs start again on cleared slots */
+    g_xl2 = 0;
+    unsigned *d = NULL;
+    if (rt().n_cu < K1_NWG) return 0;
+    if (rt_check(hipMalloc((void **)&d, K1_NWG * sizeof(unsigned)), "placement probe hipMalloc")) return ROASTER_EDEVICE;
+    unsigned h[K1_NWG];
+    hipLaunchKernelGGL(dec_xcd_probe_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, d);
+    int rc = rt_check(hipGetLastError(), "placement probe launch");
+    if (!rc) rc = rt_check(hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, rt().stream), "placement probe copy");
+    if (!rc) rc = rt_check(hipStreamSynchronize(rt().stream), "placement probe sync");
+    (void)hipFree(d);
+    if (rc) return ROASTER_EDEVICE;
+    /* one rotation r for the whole grid: XCC_ID(b) = (b + r) % 8 */
+    int ok = h[0] < (unsigned)K1_G;
+    for (int b = 0; b < K1_NWG; b++) ok &= h[b] < (unsigned)K1_G && ((h[b] - b) & 7u) == ((h[0] - 0u) & 7u);
+    g_xl2 = ok;
+    return 0;
+}
+
+void dec_placement_failed() { g_xl2 = 0; }
+
+/* One launch per run of up to K1_MAXL layers (dec_stack1_kernel) on the
+ * exchange buffer A.xbuf. */
+static int launch_stack1(DecArgs &A0)
+{
+    DecXch &X = *A0.xbuf;
+    for (int c0 = A0.layer0; c0 < A0.layer0 + A0.nlayers; c0 += K1_MAXL) {
+        const int cn = min(K1_MAXL, A0.layer0 + A0.nlayers - c0), off = c0 - A0.layer0;
+        DecArgs A = A0;
+        A.xch = X.p;
+        A.layer0 = c0;
+        A.nlayers = cn;
+        if (A.ids_out) A.ids_out += (size_t)off * RTOPK;
+        if (A.w_out) A.w_out += (size_t)off * RTOPK;
+        if (A.norm_w) A.norm_w += (size_t)off * A.H;
+        if (X.epoch > 0xFFFFFFFFu - (uint32_t)cn - 1u) {  /* epochs start again on cleared slots */
             hipLaunchKernelGGL(dec_xch_clear_kernel, dim3(64), dim3(256), 0, rt().stream, X.p, X.n);
             if (rt_check(hipGetLastError(), "exchange buffer clear")) return ROASTER_EDEVICE;
             X.epoch = 0;
         }
-        A.epoch = ++X.epoch;
+        A.epoch = X.epoch + 1;
+        X.epoch += (uint32_t)cn;
         A.spin = g_spin;
+        A.xl2 = g_xl2 == 1;
         const int nbi = A.I / RQK, rpw = 64 / lanes_per_row(nbi);
         const int npg = (A.I / K1_GW + K1_W - 1) / K1_W, nd = ((A.H / K1_GW + rpw - 1) / rpw + K1_W - 1) / K1_W;
-        const DecLayer *Lh = A.layers_h ? A.layers_h + l : nullptr;
-        const bool ty = Lh && !Lh->q6[0] && !Lh->q6[1] && Lh->q6[2] && !Lh->sq6[0] && !Lh->sq6[1] && Lh->sq6[2];
-        if (npg == 2 && nd == 2 && ty) hipLaunchKernelGGL(dec_layer1_2x2_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A, l);
-        else hipLaunchKernelGGL(dec_layer1_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A, l);
-        if (rt_check(hipGetLastError(), "layer launch")) return ROASTER_EDEVICE;
+        bool ty = A.layers_h != nullptr;
+        for (int l = c0; ty && l < c0 + cn; l++) {
+            const DecLayer *Lh = A.layers_h + l;
+            ty = !Lh->q6[0] && !Lh->q6[1] && Lh->q6[2] && !Lh->sq6[0] && !Lh->sq6[1] && Lh->sq6[2];
+        }
+        if (npg == 2 && nd == 2 && ty) hipLaunchKernelGGL(dec_stack1_2x2_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
+        else hipLaunchKernelGGL(dec_stack1_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
+        if (rt_check(hipGetLastError(), "stack launch")) return ROASTER_EDEVICE;
     }
     return 0;
 }
@@ -1631,7 +1826,7 @@ int dec_launch(DecArgs &A)
         if (!ctrl || !A.plan_g) return ROASTER_ENOMEM;
         A.err = (int *)(ctrl + 16);
     }
-    if (A.xbuf && !A.ffn_out && dec_layer1_ok(A.E, A.H, A.I, A.B)) return launch_layer1(A);
+    if (A.xbuf && !A.ffn_out && dec_layer1_ok(A.E, A.H, A.I, A.B)) return launch_stack1(A);
     for (int l = A.layer0; l < A.layer0 + A.nlayers; l++)
         if (int rc = launch_layer(A, l, true)) return rc;
     return 0;

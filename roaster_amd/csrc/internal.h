@@ -74,5 +74,7 @@ void rt_set_aux_err(int *dev_word);   /* a second device error word rt_take_err 
 int noalloc_setup(int dev);  /* api.hip: device address of the allocation-free scratch array */
 
 void dec_release();          /* decode.hip: frees the decode exchange buffer */
+int dec_probe_placement();   /* decode.hip: whether stack-kernel workgroup b runs on XCD b % 8 */
+void dec_placement_failed(); /* decode.hip: a launch found otherwise: exchanges through memory */
 
 #endif

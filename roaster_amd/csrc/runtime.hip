@@ -67,6 +67,9 @@ int rt_init_locked()
     /* device address of the allocation-free entry point's scratch array; a
      * failure is reported by that entry point and leaves the others working */
     (void)noalloc_setup(dev);
+    /* workgroup placement of the one-launch decode stack (a failure leaves
+     * its exchanges going through memory) */
+    (void)dec_probe_placement();
     return 0;
 }
 
@@ -83,9 +86,10 @@ extern "C" void *roaster_stream(void)
     return (void *)g_rt.stream;
 }
 
-/* Control words of the persistent kernels: [0] grid-barrier arrivals (reset
- * before each launch), [16] sticky error bits (1 = routing found fewer than 8
- * finite logits, 2 = a grid barrier wait timed out), cleared when reported. */
+/* Control words of the decode kernels: [16] sticky error bits (1 = routing
+ * found fewer than 8 finite logits, 2 = an exchange wait of the one-launch
+ * stack gave up, 4 = a workgroup of it read an XCC_ID out of range), cleared
+ * when reported; 4 also sends later launches' exchanges through memory. */
 static unsigned *g_ctrl;
 static int *g_aux_err;      /* error word of the allocation-free entry point's scratch, or NULL */
 
@@ -114,6 +118,8 @@ int rt_take_err()
         e |= w;
     }
     if (!e) return 0;
+    if (e & 4) dec_placement_failed();   /* later launches exchange through memory, groups fixed by index */
+    if (e & 4) return rt_fail(ROASTER_EDEVICE, "a decode stack workgroup read an XCC_ID out of range");
     if (e & 2) return rt_fail(ROASTER_EDEVICE, "a decode layer's exchange wait timed out (workgroups not all resident?)");
     return rt_fail(ROASTER_EROUTE, "router produced fewer than 8 finite logits for some token");
 }
