@@ -86,13 +86,13 @@ struct DecArgs {
  * different XCDs are slow to propagate): router logit b [256][16], workgroup
  * b's shared-expert SiLU*up values [256][16], the 8 routed slots' down
  * outputs [8][H] and the shared expert's, H/256 rows per workgroup,
- * [256][16].  Then one region per XCD, written and read within it: its copies
- * of the logits [256] and the shared SiLU*up [I], its group's routed SiLU*up
- * [I] and its copy of the next layer's hidden state [H]. */
+ * [256][16].  Then one region per XCD, written and read within it: its copy
+ * of the logits [256] and of the shared SiLU*up values [I], its group's
+ * routed SiLU*up [I] and its copy of the next layer's hidden state [H]. */
 #define XCH_LN 16                                   /* slots per line */
-#define XCH_LG(E, H, I) 0
+#define XCH_LG(E, H, I) ((size_t)0)
 #define XCH_EHS(E, H, I) ((size_t)256 * XCH_LN)
-#define XCH_DX(E, H, I) (XCH_EHS(E, H, I) + (size_t)256 * XCH_LN)
+#define XCH_DX(E, H, I) ((size_t)512 * XCH_LN)
 #define XCH_DSH(E, H, I) (XCH_DX(E, H, I) + 8 * (size_t)(H))
 #define XCH_LOC0(E, H, I) (XCH_DSH(E, H, I) + (size_t)256 * XCH_LN)
 #define XCH_LOCN(E, H, I) ((size_t)256 + 2 * (size_t)(I) + (size_t)(H))

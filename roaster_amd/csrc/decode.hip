@@ -62,8 +62,8 @@ extern "C" int roaster_phase_ts(unsigned long long *out)
 {
     return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_phase_ts), sizeof(g_phase_ts));
 }
-/* one-launch stack: [last two layers][workgroup][wave 0, wave 1][mark] */
-__device__ unsigned long long g_k1_ts[2][256][2][16];
+/* one-launch stack: [last two layers][workgroup][wave 0, 1, 3][mark] */
+__device__ unsigned long long g_k1_ts[2][256][3][16];
 extern "C" int roaster_phase_ts_k1(unsigned long long *out)
 {
     return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_k1_ts), sizeof(g_k1_ts));
@@ -1083,6 +1083,12 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_down_kernel(DecArgs A, i
 #define K1_WS 4                                          /* first shared gate/up pair */
 #define K1_MAXL 64                                       /* layers per launch (descriptors in LDS) */
 
+/* Back-off between polling rounds of an exchange slot, in units of 64 cycles
+ * (longer back-offs measured slower). */
+#ifndef K1_POLL_SLEEP
+#define K1_POLL_SLEEP 1
+#endif
+
 __device__ __forceinline__ uint64_t xch_word(float v, uint32_t ep)
 {
     return ((uint64_t)ep << 32) | __builtin_bit_cast(uint32_t, v);
@@ -1117,7 +1123,7 @@ __device__ __forceinline__ float xch_wait(const uint64_t *p, uint64_t v, uint32_
             dead = 1;
             break;
         }
-        __builtin_amdgcn_s_sleep(1);        /* ~64 cycles between polls of one slot */
+        __builtin_amdgcn_s_sleep(K1_POLL_SLEEP);
         v = xch_load(p);
     }
     return __builtin_bit_cast(float, (uint32_t)v);
@@ -1131,7 +1137,9 @@ __device__ __forceinline__ float xch_get(const uint64_t *p, uint32_t ep, int &de
 /* The values of slots q[0..N) (those with need bit i) once they carry epoch
  * ep.  Every round re-polls all slots still missing, their loads in flight
  * together, so a gather costs the rounds until its last slot is published,
- * not one round trip per slot; at most spin rounds (dead: stop waiting). */
+ * not one round trip per slot; at most spin rounds (dead: stop waiting).
+ * Rounds are spaced by K1_POLL_SLEEP; a second round kept in flight measured
+ * slower (the round left in flight at the end delays the wave's next load). */
 template <int N>
 __device__ __forceinline__ void xch_gather(const uint64_t *const (&q)[N], unsigned need, uint32_t ep, int &dead,
                                            uint32_t spin, float (&o)[N])
@@ -1149,7 +1157,7 @@ __device__ __forceinline__ void xch_gather(const uint64_t *const (&q)[N], unsign
             dead = 1;
             break;
         }
-        __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_s_sleep(K1_POLL_SLEEP);
 #pragma unroll
         for (int i = 0; i < N; i++)
             if ((miss >> i) & 1u) r[i] = xch_load(q[i]);
@@ -1250,53 +1258,46 @@ __device__ __forceinline__ float k1_gather_run(const uint64_t *p, uint32_t ep, i
         dead = s_dead;          \
     } while (0)
 
-/* The loads of layer l that depend on nothing computed in it, by wave role:
- * router row gw (wave K1_WR), the shared-gate vector (K1_WGI), the norm
- * weights (K1_WN), this workgroup's shared gate/up pairs (K1_WS .. K1_WS +
- * SP - 1) and shared down rows (the last nsd waves).  Each wave parks its
- * loaded bytes in its own LDS stage and reads them back when it uses them
- * (one wave writes and reads a stage, so no barrier is involved): held in
- * registers they would stay live across the whole layer loop. */
-union K1Stage {
-    float4 rw[8][64];
-    struct {
-        QChunk2 shc[64];
-        QChunk sdc[64];
-    } s;
+/* The loads of layer l that depend on nothing computed in it, parked in LDS
+ * (held in registers they would stay live across the whole layer loop) by
+ * waves 1..7, so that wave 0, which combines and publishes h, never waits for
+ * them: router row gw (wave K1_WR), the shared-gate vector (K1_WGI), the norm
+ * weights (K1_WN), this workgroup's shared gate/up pairs (waves K1_WS .. K1_WS
+ * + SP - 1) and shared down rows (the last nsd waves).  Each store waits for
+ * its own loads; waves 1..7 have nothing else to do at that point of a layer.
+ * (Every XCD computing all E logits itself would save the relay but read the
+ * router 8 times: measured slower over 40 layers.) */
+struct K1Pre {
+    float4 (*rw)[64];           /* [m][lane] router row gw */
+    float4 (*gin)[64];          /* [m][lane] shared-gate vector */
+    float *nw;                  /* [H] norm weights */
+    QChunk2 (*shc)[64];         /* [pair][lane] */
+    QChunk (*sdc)[64];          /* [task][lane] */
 };
 
 template <int TY>
-__device__ __forceinline__ void k1_prefetch(const DecArgs &A, const DecLayer &L, int l, K1Stage *stage, float *nw_s,
-                                            int wv, bool rrow, int SP, int sdt, int RO, int rpw, int lane)
+__device__ __forceinline__ void k1_prefetch(const DecArgs &A, const DecLayer &L, int l, const K1Pre &P, int wv,
+                                            bool rrow, int SP, int sdt, int RO, int rpw, int lane)
 {
     const int sg6 = TY < 0 ? L.sq6[0] : (TY >> 3) & 1, su6 = TY < 0 ? L.sq6[1] : (TY >> 4) & 1;
     const int sd6 = TY < 0 ? L.sq6[2] : (TY >> 5) & 1;
     const int H = A.H, HU = H / 4, c = lane & 7, lb = lane >> 3;
     const int nbh = H / RQK, nbi = A.I / RQK, lpr = lanes_per_row(nbi), rw_ = lane / lpr, lr = lane % lpr;
     const int gw = blockIdx.x;
-    float4 rw[8];
+    if (wv == 0) return;
+    float4 r1[8];
     QChunk2 shc;
     QChunk sdc;
+    const float *nw = A.do_norm && A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * H : NULL;
     if (wv == K1_WR && rrow) {
 #pragma unroll
-        for (int m = 0; m < 8; m++) rw[m] = gld_f4(L.router + (size_t)gw * H + min(4 * lane + 256 * m, H - 4));
-#pragma unroll
-        for (int m = 0; m < 8; m++) stage[wv].rw[m][lane] = rw[m];
+        for (int m = 0; m < 8; m++) r1[m] = gld_f4(L.router + (size_t)gw * H + min(4 * lane + 256 * m, H - 4));
     } else if (wv == K1_WGI) {
 #pragma unroll
-        for (int m = 0; m < 8; m++) rw[m] = gld_f4(L.gate_inp + min(4 * lane + 256 * m, H - 4));
+        for (int m = 0; m < 8; m++) r1[m] = gld_f4(L.gate_inp + min(4 * lane + 256 * m, H - 4));
+    } else if (wv == K1_WN && nw) {
 #pragma unroll
-        for (int m = 0; m < 8; m++) stage[wv].rw[m][lane] = rw[m];
-    } else if (wv == K1_WN) {
-        const float *nw = A.do_norm && A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * H : NULL;
-        if (nw) {
-            float4 q[8];
-#pragma unroll
-            for (int m = 0; m < 8; m++) q[m] = ((const float4 *)nw)[min(lane + 64 * m, HU - 1)];
-#pragma unroll
-            for (int m = 0; m < 8; m++)
-                if (lane + 64 * m < HU) ((float4 *)nw_s)[lane + 64 * m] = q[m];
-        }
+        for (int m = 0; m < 8; m++) r1[m] = ((const float4 *)nw)[min(lane + 64 * m, HU - 1)];
     }
     if (wv >= K1_WS && wv < K1_WS + SP) {
         const size_t j = (size_t)gw * SP + (wv - K1_WS);
@@ -1304,8 +1305,19 @@ __device__ __forceinline__ void k1_prefetch(const DecArgs &A, const DecLayer &L,
         shc.u = q_load_t(su6, L.sup, j, nbh, lb, c);
     }
     if (sdt >= 0) sdc = q_load_t(sd6, L.sdown, (size_t)min(gw * RO + sdt * rpw + rw_, H - 1), nbi, lr >> 3, lr & 7);
-    if (wv >= K1_WS && wv < K1_WS + SP) stage[wv].s.shc[lane] = shc;
-    if (sdt >= 0) stage[wv].s.sdc[lane] = sdc;
+    if (wv == K1_WR && rrow) {
+#pragma unroll
+        for (int m = 0; m < 8; m++) P.rw[m][lane] = r1[m];
+    } else if (wv == K1_WGI) {
+#pragma unroll
+        for (int m = 0; m < 8; m++) P.gin[m][lane] = r1[m];
+    } else if (wv == K1_WN && nw) {
+#pragma unroll
+        for (int m = 0; m < 8; m++)
+            if (lane + 64 * m < HU) ((float4 *)P.nw)[lane + 64 * m] = r1[m];
+    }
+    if (wv >= K1_WS && wv < K1_WS + SP) P.shc[wv - K1_WS][lane] = shc;
+    if (sdt >= 0) P.sdc[sdt][lane] = sdc;
 }
 
 /* Layer i of the call from its LDS copy, as wave-uniform (scalar) values. */
@@ -1335,7 +1347,10 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
     __shared__ float w_s[RTOPK + 1];
     __shared__ float red_s[4];
     __shared__ __align__(16) DecLayer Ls[K1_MAXL];
-    __shared__ K1Stage stage_s[K1_W];
+    __shared__ float4 rrow_s[8][64];                          /* router row gw */
+    __shared__ float4 gin_s[8][64];
+    __shared__ QChunk2 shc_s[K1_MAXI / 256][64];
+    __shared__ QChunk sdc_s[4][64];
     __shared__ int s_dead, s_err;
 
     const int H = A.H, I = A.I, E = A.E, HU = H / 4, nbh = H / RQK, nbi = I / RQK;
@@ -1353,7 +1368,7 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
     if (A.xl2 && !l2 && threadIdx.x == 0) atomicOr(A.err, 4);
     const int grp = l2 ? (int)xcc : (int)(blockIdx.x % K1_G), gi = blockIdx.x / K1_G, gw = blockIdx.x;
     const bool swz = A.xswz;
-    uint64_t *xlg = A.xch + XCH_LG(E, H, I);                 /* across XCDs */
+    uint64_t *xlg = A.xch + XCH_LG(E, H, I);                  /* across XCDs */
     uint64_t *xehs = A.xch + XCH_EHS(E, H, I);
     uint64_t *xdx = A.xch + XCH_DX(E, H, I);
     uint64_t *xdsh = A.xch + XCH_DSH(E, H, I);
@@ -1366,6 +1381,7 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
     const int lpr = lanes_per_row(nbi), rpw = 64 / lpr;
     const int nsd = (RO + rpw - 1) / rpw;                    /* shared down tasks */
     const int sdt = wv - (K1_W - nsd);
+    const K1Pre P = {rrow_s, gin_s, nw_s, shc_s, sdc_s};
     const bool rrow = gw < E && !A.logits_in;                /* this workgroup dots router row gw */
     const int n = A.nlayers;
 #ifdef ROASTER_PHASE_TS
@@ -1392,7 +1408,7 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
     constexpr int DQ = (int)(sizeof(DecLayer) / 16);
     const uint4 lq = ((const uint4 *)(A.layers + A.layer0))[min(tid, n * DQ - 1)];
     DecLayer L = A.layers[A.layer0];
-    k1_prefetch<TY>(A, L, A.layer0, stage_s, nw_s, wv, rrow, SP, sdt, RO, rpw, lane);
+    k1_prefetch<TY>(A, L, A.layer0, P, wv, rrow, SP, sdt, RO, rpw, lane);
 
     for (int li = 0; li < n; li++) {
         /* the thread index as a value opaque to the compiler, per layer: else
@@ -1478,11 +1494,13 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
         __syncthreads();
         K1_TS(2);
 
-        /* ---- 2. router logit, shared-gate logit, shared SiLU*up ----------- */
+        /* ---- 2. router logit gw (wave K1_WR), the shared-gate logit (wave
+         * K1_WGI), this workgroup's shared SiLU*up values (waves K1_WS..): the
+         * logit and the shared values go to every XCD ------------------------ */
         if (wv == K1_WR && rrow) {
             float4 rw[8];
 #pragma unroll
-            for (int m = 0; m < 8; m++) rw[m] = stage_s[wv].rw[m][lane];
+            for (int m = 0; m < 8; m++) rw[m] = rrow_s[m][lane];
             const float s = k1_row_dot(rw, x4, H, swz, lane);
             if (lane == 0) {
                 xch_put(xlg + (size_t)gw * XCH_LN, s, ep);
@@ -1491,27 +1509,26 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
         } else if (wv == K1_WGI) {
             float4 rw[8];
 #pragma unroll
-            for (int m = 0; m < 8; m++) rw[m] = stage_s[wv].rw[m][lane];
+            for (int m = 0; m < 8; m++) rw[m] = gin_s[m][lane];
             const float s = k1_row_dot(rw, x4, H, swz, lane);
             if (lane == 0) w_s[RTOPK] = 1.0f / (1.0f + expf(-s));
-        }
-        if (wv >= K1_WS && wv < K1_WS + SP) {
-            const float eh = k1_gu_pair(sg6, su6, stage_s[wv].s.shc[lane], xn, xsum, swz, nbh, lane);
+        } else if (wv >= K1_WS && wv < K1_WS + SP) {
+            const float eh = k1_gu_pair(sg6, su6, shc_s[wv - K1_WS][lane], xn, xsum, swz, nbh, lane);
             if (lane == 0) xch_put(xehs + (size_t)gw * XCH_LN + (wv - K1_WS), eh, ep);
         }
         K1_TS(3);
         /* ---- 3. wave 0 relays this workgroup's share of the logits (lanes <
-         * LPW) and of the shared SiLU*up values (lanes 32..) into this XCD's
-         * region, then gathers the E logits from there and ranks the top 8;
-         * wave 3 gathers the shared SiLU*up values from there ---------------- */
+         * LPW) into this XCD's region, gathers all E from there and ranks the
+         * top 8; wave K1_WN relays its share of the shared SiLU*up values and
+         * gathers them all.  The two relays are kept apart so that the logits
+         * never wait for the later shared values. ---------------------------- */
         if (wv == 0) {
-            const bool rl_lg = lane < LPW && !A.logits_in, rl_sh = lane >= 32 && lane - 32 < SPW;
-            /* logit j is line j's slot 0; shared value j is slot j % SP of line j / SP */
-            const int j = rl_lg ? gi * LPW + lane : rl_sh ? gi * SPW + lane - 32 : 0;
-            if (rl_lg || rl_sh) {
-                const float v = xch_get(rl_lg ? xlg + (size_t)j * XCH_LN : xehs + (size_t)(j / SP) * XCH_LN + j % SP, ep,
-                                        dead, A.spin);
-                xch_put_xcd((rl_lg ? llg : lehs) + j, v, ep, l2);
+            if (lane < LPW && !A.logits_in) {
+                const int j = gi * LPW + lane;
+                const uint64_t *q[1] = {xlg + (size_t)j * XCH_LN};
+                float v[1];
+                xch_gather<1>(q, 1u, ep, dead, A.spin, v);
+                xch_put_xcd(llg + j, v[0], ep, l2);
             }
             K1_TS(13);
             float v4[4];
@@ -1529,8 +1546,16 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
             for (int i = 0; i < 4; i++)
                 if (lane + 64 * i >= E) v4[i] = -INFINITY;
             topk8_fast(v4, E, ids_s, w_s, &s_err, &tks);
-        } else if (wv == K1_WN && lane < I / 16) {
-            ehshs[lane] = k1_gather_run(lehs + 16 * lane, ep, dead, A.spin, ehsh + 16 * lane);
+            K1_TS(14);
+        } else if (wv == K1_WN) {
+            if (lane < SPW) {                       /* shared value j: slot j % SP of line j / SP */
+                const int j = gi * SPW + lane;
+                const uint64_t *q[1] = {xehs + (size_t)(j / SP) * XCH_LN + j % SP};
+                float v[1];
+                xch_gather<1>(q, 1u, ep, dead, A.spin, v);
+                xch_put_xcd(lehs + j, v[0], ep, l2);
+            }
+            if (lane < I / 16) ehshs[lane] = k1_gather_run(lehs + 16 * lane, ep, dead, A.spin, ehsh + 16 * lane);
         }
         K1_SYNC_DEAD();
         K1_TS(4);
@@ -1567,7 +1592,7 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
         if (sdt >= 0) {
             const int rl = sdt * rpw + rw_;
             const bool live = rl < RO && lbd < nbi;
-            const float part = k1_down_row(sd6, stage_s[wv].s.sdc[lane], ehsh, ehshs, live, lpr, lane);
+            const float part = k1_down_row(sd6, sdc_s[sdt][lane], ehsh, ehshs, live, lpr, lane);
             if (live && lr == 0) xch_put(xdsh + (size_t)gw * XCH_LN + rl, part, ep);
         }
         /* the down rows once the gate/up rows have arrived (loads complete in
@@ -1611,7 +1636,7 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
          * of h: the nine slots' down outputs combined -------------------------- */
         if (!last) {
             L = k1_layer(Ls, li + 1);
-            k1_prefetch<TY>(A, L, l + 1, stage_s, nw_s, wv, rrow, SP, sdt, RO, rpw, lane);
+            k1_prefetch<TY>(A, L, l + 1, P, wv, rrow, SP, sdt, RO, rpw, lane);
         }
         K1_TS(11);
         if (wv == 0) {
@@ -1640,9 +1665,9 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
     }
     if (tid == 0 && (dead || s_dead)) atomicOr(A.err, 2);
 #ifdef ROASTER_PHASE_TS
-    if (threadIdx.x == 0 || threadIdx.x == 64)
+    if (threadIdx.x == 0 || threadIdx.x == 64 || threadIdx.x == 192)
         for (int k = 0; k < 2; k++)
-            for (int i = 0; i < 16; i++) g_k1_ts[k][blockIdx.x][threadIdx.x >> 6][i] = tsv[k][i];
+            for (int i = 0; i < 16; i++) g_k1_ts[k][blockIdx.x][min((int)threadIdx.x >> 6, 2)][i] = tsv[k][i];
 #endif
 #undef K1_TS
 }
