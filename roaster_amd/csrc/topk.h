@@ -139,7 +139,9 @@ __device__ __forceinline__ unsigned long long topk_ck(uint32_t key, int e)
 /* Wave-level top-8 of one token (model.c:869-897) by ranking a candidate
  * set, the same selection as topk8_wave.  The 256 keys fall into 8 groups of
  * 32 (the 4 keys of each 8-lane group); T = the smallest of the 8 group
- * maxima is at most the 8th largest key, so every selected key is >= T.  The
+ * maxima is at most the 8th largest key, so every selected key is >= T (the
+ * maxima by DPP, their minimum by a row mirror and permlane16 / permlane32
+ * swaps, so T reaches every lane without readlane round trips).  The
  * candidates (key >= T, key != 0) are compacted into LDS and each candidate's
  * rank is the number of candidates with a larger composite key; rank r < 8
  * fills slot r.  The rounds of topk8_wave run instead when more than 64 keys
@@ -155,8 +157,10 @@ static __device__ void topk8_fast(const float v4in[4], int E, int *ids, float *w
     g = max(g, (uint32_t)dpp_i<DPP_XOR2>((int)g));
     g = max(g, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)g));          /* group maximum in each 8-lane group */
     g = min(g, (uint32_t)dpp_i<DPP_MIRROR>((int)g));              /* smaller of the row's two groups */
-    const uint32_t T = min(min((uint32_t)__builtin_amdgcn_readlane((int)g, 0), (uint32_t)__builtin_amdgcn_readlane((int)g, 16)),
-                           min((uint32_t)__builtin_amdgcn_readlane((int)g, 32), (uint32_t)__builtin_amdgcn_readlane((int)g, 48)));
+    const auto p16 = __builtin_amdgcn_permlane16_swap(g, g, false, false);
+    g = min((uint32_t)p16[0], (uint32_t)p16[1]);                   /* rows 0-1 and rows 2-3 */
+    const auto p32 = __builtin_amdgcn_permlane32_swap(g, g, false, false);
+    const uint32_t T = min((uint32_t)p32[0], (uint32_t)p32[1]);    /* all eight groups, in every lane */
     bool c[4];
     uint64_t b[4];
     int n = 0;
@@ -170,6 +174,7 @@ static __device__ void topk8_fast(const float v4in[4], int E, int *ids, float *w
         topk8_wave(v4in, E, ids, w, bad);
         return;
     }
+    S->cand[lane] = 0ull;                           /* entries past the candidates compare below every key */
     int base = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -181,14 +186,41 @@ static __device__ void topk8_fast(const float v4in[4], int E, int *ids, float *w
     if (lane < RTOPK) S->slot[lane] = 0ull;
     __builtin_amdgcn_s_waitcnt(0xC07F);             /* lgkmcnt(0): the wave's LDS writes are done */
     __builtin_amdgcn_wave_barrier();
-    const unsigned long long my = S->cand[lane];          /* lanes >= n read a stale entry and write nothing */
+    /* candidate p's rank = the number of candidates with a larger composite
+     * key; with at most 16 (32) candidates four (two) lanes share candidate p,
+     * each counting over a quarter (half) of the list, and permlane swaps add
+     * the parts: a dependent chain of 4 (8) compares instead of n */
+    const ulonglong2 *c2 = (const ulonglong2 *)S->cand;
+    unsigned long long my;
     int rank = 0;
-    for (int j0 = 0; j0 < n; j0 += 16) {            /* 16 reads in flight, then the compares */
-        unsigned long long cj[16];
+    if (n <= 16) {
+        my = S->cand[lane & 15];
+        const int q = lane >> 4;
+        const ulonglong2 x = c2[2 * q], y = c2[2 * q + 1];
+        rank = (x.x > my) + (x.y > my) + (y.x > my) + (y.y > my);
+        const auto p16 = __builtin_amdgcn_permlane16_swap(rank, rank, false, false);
+        rank = (int)p16[0] + (int)p16[1];
+        const auto p32 = __builtin_amdgcn_permlane32_swap(rank, rank, false, false);
+        rank = (int)p32[0] + (int)p32[1];
+    } else if (n <= 32) {
+        my = S->cand[lane & 31];
+        const int hf = lane >> 5;
+        ulonglong2 x[8];
 #pragma unroll
-        for (int u = 0; u < 16; u++) cj[u] = S->cand[j0 + u];
+        for (int u = 0; u < 8; u++) x[u] = c2[8 * hf + u];
 #pragma unroll
-        for (int u = 0; u < 16; u++) rank += (j0 + u < n && cj[u] > my) ? 1 : 0;
+        for (int u = 0; u < 8; u++) rank += (x[u].x > my) + (x[u].y > my);
+        const auto p32 = __builtin_amdgcn_permlane32_swap(rank, rank, false, false);
+        rank = (int)p32[0] + (int)p32[1];
+    } else {
+        my = S->cand[lane];                         /* lanes >= n read an entry they never write */
+        for (int j0 = 0; j0 < n; j0 += 16) {        /* 8 reads of two candidates in flight, then the compares */
+            ulonglong2 cj[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) cj[u] = c2[(j0 >> 1) + u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) rank += (cj[u].x > my) + (cj[u].y > my);
+        }
     }
     if (lane < n && rank < RTOPK) S->slot[rank] = my;
     __builtin_amdgcn_s_waitcnt(0xC07F);
