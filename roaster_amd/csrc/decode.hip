@@ -1080,7 +1080,6 @@ extern "C" __global__ void __launch_bounds__(DT, 3) dec_down_kernel(DecArgs A, i
 #define K1_WR 1                                          /* wave roles: router row */
 #define K1_WGI 2                                         /* shared-gate vector */
 #define K1_WN 3                                          /* norm weights; shared SiLU*up gather */
-#define K1_WS 4                                          /* first shared gate/up pair */
 #define K1_MAXL 64                                       /* layers per launch (descriptors in LDS) */
 
 /* Back-off between polling rounds of an exchange slot, in units of 64 cycles
@@ -1262,8 +1261,10 @@ __device__ __forceinline__ float k1_gather_run(const uint64_t *p, uint32_t ep, i
  * (held in registers they would stay live across the whole layer loop) by
  * waves 1..7, so that wave 0, which combines and publishes h, never waits for
  * them: router row gw (wave K1_WR), the shared-gate vector (K1_WGI), the norm
- * weights (K1_WN), this workgroup's shared gate/up pairs (waves K1_WS .. K1_WS
- * + SP - 1) and shared down rows (the last nsd waves).  Each store waits for
+ * weights (K1_WN), this workgroup's shared gate/up pairs (the last SP waves:
+ * a SIMD's second wave is wave w + 4, and waves 1 and 0 on SIMDs 1 and 0 must
+ * not share them with a pair's dot when they dot the router row and rank the
+ * top 8) and shared down rows (the last nsd waves).  Each store waits for
  * its own loads; waves 1..7 have nothing else to do at that point of a layer.
  * (Every XCD computing all E logits itself would save the relay but read the
  * router 8 times: measured slower over 40 layers.) */
@@ -1279,6 +1280,7 @@ template <int TY>
 __device__ __forceinline__ void k1_prefetch(const DecArgs &A, const DecLayer &L, int l, const K1Pre &P, int wv,
                                             bool rrow, int SP, int sdt, int RO, int rpw, int lane)
 {
+    const int ws = K1_W - SP;                                /* first shared gate/up pair */
     const int sg6 = TY < 0 ? L.sq6[0] : (TY >> 3) & 1, su6 = TY < 0 ? L.sq6[1] : (TY >> 4) & 1;
     const int sd6 = TY < 0 ? L.sq6[2] : (TY >> 5) & 1;
     const int H = A.H, HU = H / 4, c = lane & 7, lb = lane >> 3;
@@ -1299,8 +1301,8 @@ __device__ __forceinline__ void k1_prefetch(const DecArgs &A, const DecLayer &L,
 #pragma unroll
         for (int m = 0; m < 8; m++) r1[m] = ((const float4 *)nw)[min(lane + 64 * m, HU - 1)];
     }
-    if (wv >= K1_WS && wv < K1_WS + SP) {
-        const size_t j = (size_t)gw * SP + (wv - K1_WS);
+    if (wv >= ws) {
+        const size_t j = (size_t)gw * SP + (wv - ws);
         shc.g = q_load_t(sg6, L.sgate, j, nbh, lb, c);
         shc.u = q_load_t(su6, L.sup, j, nbh, lb, c);
     }
@@ -1316,7 +1318,7 @@ __device__ __forceinline__ void k1_prefetch(const DecArgs &A, const DecLayer &L,
         for (int m = 0; m < 8; m++)
             if (lane + 64 * m < HU) ((float4 *)P.nw)[lane + 64 * m] = r1[m];
     }
-    if (wv >= K1_WS && wv < K1_WS + SP) P.shc[wv - K1_WS][lane] = shc;
+    if (wv >= ws) P.shc[wv - ws][lane] = shc;
     if (sdt >= 0) P.sdc[sdt][lane] = sdc;
 }
 
@@ -1495,7 +1497,7 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
         K1_TS(2);
 
         /* ---- 2. router logit gw (wave K1_WR), the shared-gate logit (wave
-         * K1_WGI), this workgroup's shared SiLU*up values (waves K1_WS..): the
+         * K1_WGI), this workgroup's shared SiLU*up values (the last SP waves): the
          * logit and the shared values go to every XCD ------------------------ */
         if (wv == K1_WR && rrow) {
             float4 rw[8];
@@ -1512,9 +1514,10 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
             for (int m = 0; m < 8; m++) rw[m] = gin_s[m][lane];
             const float s = k1_row_dot(rw, x4, H, swz, lane);
             if (lane == 0) w_s[RTOPK] = 1.0f / (1.0f + expf(-s));
-        } else if (wv >= K1_WS && wv < K1_WS + SP) {
-            const float eh = k1_gu_pair(sg6, su6, shc_s[wv - K1_WS][lane], xn, xsum, swz, nbh, lane);
-            if (lane == 0) xch_put(xehs + (size_t)gw * XCH_LN + (wv - K1_WS), eh, ep);
+        } else if (wv >= K1_W - SP) {
+            const int pr = wv - (K1_W - SP);
+            const float eh = k1_gu_pair(sg6, su6, shc_s[pr][lane], xn, xsum, swz, nbh, lane);
+            if (lane == 0) xch_put(xehs + (size_t)gw * XCH_LN + pr, eh, ep);
         }
         K1_TS(3);
         /* ---- 3. wave 0 relays this workgroup's share of the logits (lanes <

@@ -169,6 +169,11 @@ __device__ __forceinline__ void q_word(const QChunk &ch, int i, int c, uint32_t 
         a |= ((hv >> sh) & 0x03030303u) << 4;
         b |= ((hv >> (sh + 4)) & 0x03030303u) << 4;
     }
+    /* opaque to the compiler: otherwise it folds each mask into the byte
+     * extraction of dot4u8 (a bit-field extract plus a convert per quant)
+     * instead of converting bytes 0..3 of the word directly (one
+     * v_cvt_f32_ubyteN per quant) */
+    asm("" : "+v"(a), "+v"(b));
 }
 
 __device__ __forceinline__ float dot4u8(uint32_t q, const float4 x, float acc)
