@@ -73,7 +73,8 @@ def parse():
     ap.add_argument("--three-kernel", action="store_true",
                     help="decode one token's layers with three launches each instead of one (for comparison)")
     ap.add_argument("--legs", default="decode,prefill,config1,config2,dense",
-                    help="comma-separated legs to run (the decode headline always runs unless omitted here)")
+                    help="comma-separated legs to run (the decode headline always runs unless omitted here); "
+                         "prefill5 / prefill3 run one prefill workload alone (config 5 / config 3)")
     return ap.parse_args()
 
 
@@ -277,12 +278,22 @@ def event_ms(torch, stream, fn, reps):
     return a.elapsed_time(b) / reps
 
 
-def prefill_legs(torch, L, R, dev, stream, reps, with_cpu):
+def prefill_legs(torch, L, R, dev, stream, reps, with_cpu, parts=("q6", "zipf", "api")):
     """Prefill: config 5 (all-Q6_K, 2048 tokens x 4 layers, N(0,1) logits
     given) is the line's prefill value with its MFMA roofline; config 3 (512
     Zipf-routed tokens through one Q4_K/Q6_K layer with the router) is
-    HBM-bound and reported against min(MFMA peak, AI x HBM peak)."""
-    # config 5: all-Q6_K, T = 2048, 4 layers, N(0,1) logits given (no router)
+    HBM-bound and reported against min(MFMA peak, AI x HBM peak); "api" adds
+    the kernels.h kernel_moe_prefill leg on the config-3 layer."""
+    out = {}
+    if "q6" in parts:
+        out = prefill_q6_leg(torch, L, R, dev, stream, reps, with_cpu)
+    if "zipf" in parts:
+        out["zipf_512x1"] = prefill_zipf_leg(torch, L, R, dev, stream, reps, with_cpu, "api" in parts)
+    return out
+
+
+def prefill_q6_leg(torch, L, R, dev, stream, reps, with_cpu):
+    """Config 5: all-Q6_K, T = 2048, 4 layers, N(0,1) logits given (no router)."""
     T, NL, seed = 2048, 4, 4
     desc = R.table_desc(NL, q6=(1, 1, 1), sh_q6=(1, 1, 1))
     t = L.roaster_table_create(C.byref(desc))
@@ -341,7 +352,11 @@ def prefill_legs(torch, L, R, dev, stream, reps, with_cpu):
                 out["cpu_baseline"] = cb
     finally:
         L.roaster_table_destroy(t)
-    # config 3: Q4_K/Q6_K, T = 512, router + Zipf bias, one layer
+    return out
+
+
+def prefill_zipf_leg(torch, L, R, dev, stream, reps, with_cpu, with_api):
+    """Config 3: Q4_K/Q6_K, T = 512, router + Zipf bias, one layer."""
     T, seed = 512, 2
     desc = R.table_desc(1)
     t = L.roaster_table_create(C.byref(desc))
@@ -382,15 +397,15 @@ def prefill_legs(torch, L, R, dev, stream, reps, with_cpu):
                             "algorithmic_bytes": int(nbytes), "algorithmic_flops": int(flops),
                             "arithmetic_intensity": round(ai, 1), "achieved_TFLOPs": round(tf, 2),
                             "roof_TFLOPs": round(roof_tf, 1), "frac_mfma_peak": round(tf / MFMA_PEAK_TFLOPS, 4)}}
-        leg["kernels_h_moe_prefill"] = moe_prefill_hostbuf_leg(L, R, t, desc, seed, Xh, idh)
+        if with_api:
+            leg["kernels_h_moe_prefill"] = moe_prefill_hostbuf_leg(L, R, t, desc, seed, Xh, idh)
         if with_cpu:
             cb = cpu_baseline_prefill(t, desc, seed, Xh, idh, layer=0, with_router=True, label="Zipf-routed Q4_K/Q6_K")
             if cb:
                 leg["cpu_baseline"] = cb
-        out["zipf_512x1"] = leg
     finally:
         L.roaster_table_destroy(t)
-    return out
+    return leg
 
 
 def moe_prefill_hostbuf_leg(L, R, table, desc, seed, X, ids, reps=3):
@@ -683,8 +698,10 @@ def main():
     line = {"metric": "partial run: legs %s" % sorted(legs)}
     if "decode" in legs:
         line = decode_legs(args, torch, L, R, dev, stream)
-    if "prefill" in legs and not args.no_prefill:
-        line["prefill"] = prefill_legs(torch, L, R, dev, stream, args.prefill_reps, not args.no_cpu)
+    parts = {"prefill": ("q6", "zipf", "api"), "prefill5": ("q6",), "prefill3": ("zipf",)}
+    want = tuple(p for leg in legs if leg in parts for p in parts[leg])
+    if want and not args.no_prefill:
+        line["prefill"] = prefill_legs(torch, L, R, dev, stream, args.prefill_reps, not args.no_cpu, want)
     if "config1" in legs:
         line["config1"] = config1_leg(torch, L, R, dev, stream, not args.no_cpu)
     if "config2" in legs:
