@@ -88,7 +88,10 @@ struct DecArgs {
  * outputs [8][H] and the shared expert's, H/256 rows per workgroup,
  * [256][16].  Then one region per XCD, written and read within it: its copy
  * of the logits [256] and of the shared SiLU*up values [I], its group's
- * routed SiLU*up [I] and its copy of the next layer's hidden state [H]. */
+ * routed SiLU*up [I] and its copy of the next layer's hidden state [H].  The
+ * per-XCD vectors are stored so that a gather's lanes read contiguous slots:
+ * SiLU*up value j at (j % 16) (I / 16) + j / 16 (a lane reads one 16-value
+ * run), hidden row r at (r % 4) (H / 4) + r / 4 (a lane reads one float4). */
 #define XCH_LN 16                                   /* slots per line */
 #define XCH_LG(E, H, I) ((size_t)0)
 #define XCH_EHS(E, H, I) ((size_t)256 * XCH_LN)

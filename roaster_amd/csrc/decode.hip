@@ -1235,14 +1235,22 @@ __device__ __forceinline__ float k1_row_dot(const float4 (&w)[8], const float4 *
     return group_sum<64>(acc);
 }
 
-/* Sixteen slots p[0..16) (one 16-column run of a SiLU*up vector) into dst,
- * and their sum in sum16's order. */
-__device__ __forceinline__ float k1_gather_run(const uint64_t *p, uint32_t ep, int &dead, uint32_t spin, float *dst)
+/* SiLU*up vectors of I values in this XCD's region are stored run-major:
+ * value j (run j / 16, position j % 16) at slot (j % 16) * (I / 16) + j / 16,
+ * so that the 16 polling loads of a gather each read one contiguous span of
+ * I / 16 slots across the lanes (two cache lines for I = 512) instead of
+ * one line per lane. */
+__device__ __forceinline__ size_t k1_run_slot(int j, int I) { return (size_t)(j & 15) * (I >> 4) + (j >> 4); }
+
+/* Run r (values 16r .. 16r + 15) of a run-major vector into dst, and their
+ * sum in sum16's order. */
+__device__ __forceinline__ float k1_gather_run(const uint64_t *base, int I, int r, uint32_t ep, int &dead,
+                                               uint32_t spin, float *dst)
 {
     float v[16];
     const uint64_t *q[16];
 #pragma unroll
-    for (int i = 0; i < 16; i++) q[i] = p + i;
+    for (int i = 0; i < 16; i++) q[i] = base + (size_t)i * (I >> 4) + r;
     xch_gather<16>(q, 0xFFFFu, ep, dead, spin, v);
 #pragma unroll
     for (int i = 0; i < 16; i += 4) *(float4 *)(dst + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
@@ -1439,7 +1447,7 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
             const uint64_t *q[8];
             float v[8];
 #pragma unroll
-            for (int i = 0; i < 8; i++) q[i] = lh + 4 * (size_t)min(tid + 256 * (i >> 2), HU - 1) + (i & 3);
+            for (int i = 0; i < 8; i++) q[i] = lh + (size_t)(i & 3) * HU + min(tid + 256 * (i >> 2), HU - 1);
             xch_gather<8>(q, (tid < HU ? 0x0Fu : 0u) | (tid + 256 < HU ? 0xF0u : 0u), ep - 1, dead, A.spin, v);
             hq[0] = make_float4(v[0], v[1], v[2], v[3]);
             hq[1] = make_float4(v[4], v[5], v[6], v[7]);
@@ -1556,9 +1564,9 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
                 const uint64_t *q[1] = {xehs + (size_t)(j / SP) * XCH_LN + j % SP};
                 float v[1];
                 xch_gather<1>(q, 1u, ep, dead, A.spin, v);
-                xch_put_xcd(lehs + j, v[0], ep, l2);
+                xch_put_xcd(lehs + k1_run_slot(j, I), v[0], ep, l2);
             }
-            if (lane < I / 16) ehshs[lane] = k1_gather_run(lehs + 16 * lane, ep, dead, A.spin, ehsh + 16 * lane);
+            if (lane < I / 16) ehshs[lane] = k1_gather_run(lehs, I, lane, ep, dead, A.spin, ehsh + 16 * lane);
         }
         K1_SYNC_DEAD();
         K1_TS(4);
@@ -1616,11 +1624,11 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
             const int pj = wv + f * K1_W;
             if ((NPG || f < npg) && pj < RGP) {
                 const float eh = k1_gu_pair(g6, u6, gch[f], xn, xsum, swz, nbh, lane);
-                if (lane == 0) xch_put_xcd(lehx + (size_t)gi * RGP + pj, live_slot ? eh : 0.0f, ep, l2);
+                if (lane == 0) xch_put_xcd(lehx + k1_run_slot(gi * RGP + pj, I), live_slot ? eh : 0.0f, ep, l2);
             }
         }
         K1_TS(6);
-        if (wv == 0 && lane < I / 16) ehks[lane] = k1_gather_run(lehx + 16 * lane, ep, dead, A.spin, ehk + 16 * lane);
+        if (wv == 0 && lane < I / 16) ehks[lane] = k1_gather_run(lehx, I, lane, ep, dead, A.spin, ehk + 16 * lane);
         K1_SYNC_DEAD();
         K1_TS(7);
 #pragma unroll
@@ -1657,7 +1665,7 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
                 for (int k = 0; k < RTOPK; k++) y = fmaf(w_s[k], d[k], y);
                 y = fmaf(w_s[RTOPK], d[RTOPK], y);
                 const float hn = hraw[row] + y;
-                if (!last) xch_put_xcd(lh + row, hn, ep, l2);
+                if (!last) xch_put_xcd(lh + (size_t)(row & 3) * (H / 4) + (row >> 2), hn, ep, l2);
                 else if (grp == 0) {
                     if (A.y) A.y[row] = y;
                     else A.h[row] = hn;

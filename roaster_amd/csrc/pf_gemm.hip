@@ -6,12 +6,12 @@
  * one group.  Launch grids are sized for the worst case and surplus
  * workgroups exit at once.
  *
- * v2 (PF_F16, the default) -- weight-stationary, 256 threads (one wave per
- * SIMD, so a wave may hold up to 512 registers):
+ * v2 (PF_F16, the default) -- weight-stationary, 512 threads (two waves per
+ * SIMD, up to 256 registers each):
  *   A workgroup owns up to 96 rows of one group (MS = 1..3 row blocks of 32)
- *   and 256 weight rows; every wave owns 64 of those rows as two 32-row MFMA
- *   column blocks (gate/up: the same 32 gate rows and 32 up rows, so the
- *   SiLU(gate) * up epilogue pairs accumulators in registers).  Each lane
+ *   and 256 weight rows; every wave owns 32 of those rows as one 32-row MFMA
+ *   column block (gate/up: 16 gate rows and the 16 up rows of the same
+ *   columns, so the SiLU(gate) * up epilogue pairs lanes n and n + 16).  Each lane
  *   dequantises, for one weight row, the half super-block that forms its MFMA
  *   B operand, straight into registers: weights never pass through LDS.
  *   Inside a super-block the K order is permuted so that the 8 k-items a lane
@@ -424,6 +424,84 @@ __device__ __forceinline__ void tile_load(RawQ4 &r, const uint8_t *tile, int lan
     }
 }
 
+/* Slice i of a lane's record (one 16-byte load, the last Q6_K slice 12
+ * bytes): the pieces of tile_load, issued one at a time. */
+__device__ __forceinline__ void tile_slice(RawQ6 &r, const uint8_t *tile, int lane, int i)
+{
+    const uint8_t *p = tile + 16 * lane + 1024 * i;
+    if (i < 4) {
+        const uint4 s = gld_u4(p);
+        r.L[4 * i] = s.x; r.L[4 * i + 1] = s.y; r.L[4 * i + 2] = s.z; r.L[4 * i + 3] = s.w;
+    } else if (i < 6) {
+        const uint4 s = gld_u4(p);
+        const int k = 4 * (i - 4);
+        r.Hh[k] = s.x; r.Hh[k + 1] = s.y; r.Hh[k + 2] = s.z; r.Hh[k + 3] = s.w;
+    } else {
+        const uint3 s = gld_u3(p);
+        r.S[0] = s.x; r.S[1] = s.y; r.d = s.z & 0xFFFFu;
+    }
+}
+
+__device__ __forceinline__ void tile_slice(RawQ4 &r, const uint8_t *tile, int lane, int i)
+{
+    const uint4 s = gld_u4(tile + 16 * lane + 1024 * i);
+    if (i == 0) {
+        r.hd[0] = s.x; r.hd[1] = s.y; r.hd[2] = s.z; r.hd[3] = s.w;
+    } else {
+        const int k = 4 * (i - 1);
+        r.Q[k] = s.x; r.Q[k + 1] = s.y; r.Q[k + 2] = s.z; r.Q[k + 3] = s.w;
+    }
+}
+
+/* v4_mfma with the next K step's loads spread over its eight groups and the
+ * dequantisation software-pipelined: group j runs piece(j) (a share of the
+ * next step's loads), its activation reads, then the dequantisation of group
+ * j + 1 interleaved with group j's MFMAs (one MFMA, then a share of the VALU
+ * work, in turn), so that loads queue at the vector memory unit a few at a
+ * time and the VALU work runs while the matrix core is busy.  A scheduling
+ * fence after each group keeps every piece in its slot. */
+template <int MS, bool Q6, class Piece>
+__device__ __forceinline__ void v8_mfma(f32x16 (&acc)[MS], const _Float16 *Xs, const typename RawOf<Q6>::T &r,
+                                        int h, Piece &&piece)
+{
+    typename ConstOf<Q6>::T c;
+    raw_consts(r, h, c);
+    const int l = threadIdx.x & 63;
+    const _Float16 *xa = Xs + (l & 31) * V2_LD + 8 * (l >> 5);
+    f16x8 b0, b1;
+    dequant_pair(r, c, 0, b0, b1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        piece(j);
+        f16x8 x0[MS], x1[MS];
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++) {
+            x0[ms] = *(const f16x8 *)(xa + ms * 32 * V2_LD + 16 * j);
+            x1[ms] = *(const f16x8 *)(xa + ms * 32 * V2_LD + 16 * (j + 8));
+        }
+        f16x8 n0 = b0, n1 = b1;
+        if (j < 7) dequant_pair(r, c, j + 1, n0, n1);
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++) {
+            acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0[ms], b0, acc[ms], 0, 0, 0);
+            acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1[ms], b1, acc[ms], 0, 0, 0);
+        }
+        constexpr int VPM = (34 + 2 * MS - 1) / (2 * MS);
+        __builtin_amdgcn_sched_group_barrier(0x0020, 8, 0);      /* the piece's loads */
+        __builtin_amdgcn_sched_group_barrier(0x0100, 2 * MS, 0); /* activation reads */
+        __builtin_amdgcn_sched_group_barrier(0x0002, 6, 0);
+#pragma unroll
+        for (int i = 0; i < 2 * MS; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x0002, VPM, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        b0 = n0;
+        b1 = n1;
+    }
+}
+
 /* Gate/up tile: lanes n < 16 of wave w take gate row j0 + 16 w + n, lanes
  * n >= 16 the up row of the same column.  QG == QU: one raw type per wave;
  * otherwise the two halves load and dequantise on divergent paths and share
@@ -486,34 +564,65 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
     w_load(0, 0);
     x_store(Xb);
     __syncthreads();
-    /* steady state: steps kb (raw buffer 0, activation buffer 0) and kb + 1
-     * (buffers 1), each issuing the next step's loads first, activations
-     * before weights: a wave's loads complete in order, so the activation
-     * store (and with it the barrier) waits for the activation loads only,
-     * not for the next step's weights from HBM */
     int kb = 0;
-    for (; kb + 2 < nkb; kb += 2) {
-        x_load(kb + 1);
-        w_load(1, kb + 1);
-        step(0, Xb);
-        x_store(Xb + V3_XBUF);
-        __syncthreads();
-        x_load(kb + 2);
-        w_load(0, kb + 2);
-        step(1, Xb + V3_XBUF);
-        x_store(Xb);
-        __syncthreads();
-    }
-    /* last one or two steps */
-    if (kb + 1 < nkb) {
-        x_load(kb + 1);
-        w_load(1, kb + 1);
-        step(0, Xb);
-        x_store(Xb + V3_XBUF);
-        __syncthreads();
-        step(1, Xb + V3_XBUF);
+    if constexpr (QG == QU) {
+        /* step kb's MFMA work on raw buffer buf with step kn's loads spread
+         * over it: the activations in the first group (a wave's loads complete
+         * in order, so the activation store waits for them only), then one
+         * weight slice per group */
+        auto step_ld = [&](int buf, const _Float16 *Xs, int kn) {
+            const uint8_t *wn = wt + (size_t)kn * tb;
+            __builtin_amdgcn_sched_barrier(0);
+            v8_mfma<MS, QG>(acc, Xs, rg[buf], h, [&](int j) {
+                if (j == 0) x_load(kn);
+                if (j < TL_SLICES(QG)) tile_slice(rg[buf ^ 1], wn, tlane, j);
+            });
+        };
+        for (; kb + 2 < nkb; kb += 2) {
+            step_ld(0, Xb, kb + 1);
+            x_store(Xb + V3_XBUF);
+            __syncthreads();
+            step_ld(1, Xb + V3_XBUF, kb + 2);
+            x_store(Xb);
+            __syncthreads();
+        }
+        if (kb + 1 < nkb) {
+            step_ld(0, Xb, kb + 1);
+            x_store(Xb + V3_XBUF);
+            __syncthreads();
+            step(1, Xb + V3_XBUF);
+        } else {
+            step(0, Xb);
+        }
     } else {
-        step(0, Xb);
+        /* steady state: steps kb (raw buffer 0, activation buffer 0) and kb +
+         * 1 (buffers 1), each issuing the next step's loads first, activations
+         * before weights: a wave's loads complete in order, so the activation
+         * store (and with it the barrier) waits for the activation loads only,
+         * not for the next step's weights from HBM */
+        for (; kb + 2 < nkb; kb += 2) {
+            x_load(kb + 1);
+            w_load(1, kb + 1);
+            step(0, Xb);
+            x_store(Xb + V3_XBUF);
+            __syncthreads();
+            x_load(kb + 2);
+            w_load(0, kb + 2);
+            step(1, Xb + V3_XBUF);
+            x_store(Xb);
+            __syncthreads();
+        }
+        /* last one or two steps */
+        if (kb + 1 < nkb) {
+            x_load(kb + 1);
+            w_load(1, kb + 1);
+            step(0, Xb);
+            x_store(Xb + V3_XBUF);
+            __syncthreads();
+            step(1, Xb + V3_XBUF);
+        } else {
+            step(0, Xb);
+        }
     }
     /* epilogue: lane n < 16 holds gate and lane n + 16 up of column col.  For
      * the row pair (i, i + 1) one swizzle (lane ^ 16) gives lanes n < 16 the up
