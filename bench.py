@@ -564,9 +564,10 @@ def config2_leg(torch, L, R, dev, stream, with_cpu):
 
 def dense_leg(torch, L, R, dev, stream):
     """Dense quantised projections through roaster_matvec_q (model.c:113-121):
-    the LM head Q6_K [248320 x 2048] (model.c:1368-1370) at 1 and 8 tokens, the
-    8-token case also through the split-operand MFMA GEMM, and the attention
-    output projection Q4_K [2048 x 4096] (model.c:862) at 1 and 8 tokens.
+    the LM head Q6_K [248320 x 2048] (model.c:1368-1370) and the attention
+    output projection Q4_K [2048 x 4096] (model.c:862) at 1 and 8 tokens (8:
+    the quants-on-MFMA kernel, the default from 2 tokens, and for comparison
+    the dequantising matvec, "T8_valu").
     Device time from HIP events, HBM roofline over the matrix bytes."""
     out = {}
     for name, q6, rows, cols in (("lm_head_q6k_248320x2048", 1, 248320, 2048), ("attn_out_q4k_2048x4096", 0, 2048, 4096)):
@@ -574,7 +575,7 @@ def dense_leg(torch, L, R, dev, stream):
         W = R.synth_q6k(5, R.synth_stream(0, 0, 9), nb) if q6 else R.synth_q4k(5, R.synth_stream(0, 0, 9), nb)
         dw = torch.from_numpy(W).to(dev)
         leg = {"matrix_bytes": int(W.nbytes)}
-        for T, mfma in ((1, False), (8, False), (8, True)):
+        for T, mfma in ((1, False), (8, True), (8, False)):
             x = torch.from_numpy(np.stack([R.synth_normal(5, R.synth_stream(0, t, 5), cols) for t in range(T)])).to(dev)
             y = torch.empty((T, rows), dtype=torch.float32, device=dev)
             old = L.roaster_dense_mfma_min_tokens(0)
@@ -589,7 +590,7 @@ def dense_leg(torch, L, R, dev, stream):
             ms = event_ms(torch, stream, run, 50 if rows > 100000 else 200)
             L.roaster_dense_mfma_min_tokens(old)
             gbs = W.nbytes / (ms * 1e-3) / 1e9
-            leg["T%d%s" % (T, "_mfma" if mfma else "")] = {
+            leg["T%d%s" % (T, "_valu" if T > 1 and not mfma else "")] = {
                 "us": round(ms * 1e3, 2), "tokens_per_s": round(T / (ms * 1e-3), 1),
                 "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(gbs / HBM_PEAK_GBS, 4)}}

@@ -196,8 +196,8 @@ int roaster_moe_decode_stack_noalloc(RoasterTable *t, float *h, int B, int layer
  * 1368-1370), the products kernel_matvec_q4_k / _q6_k compute from host
  * buffers.  Device pointers; ordered on the library stream. */
 int roaster_matvec_q(const void *W, int q6, const float *X, float *Y, size_t rows, size_t cols, int T);
-/* Calls of roaster_matvec_q with at least t tokens (and rows a multiple of
- * 64) run as the split-operand MFMA GEMM instead of the dequantising matvec;
+/* Calls of roaster_matvec_q with at least t tokens (default 2) run with the
+ * quants as MFMA operands instead of the dequantising matvec (t = 9: never);
  * t = 0 queries.  Returns the threshold in force. */
 int roaster_dense_mfma_min_tokens(int t);
 

@@ -43,7 +43,7 @@ int  rt_init_locked();                      /* 0 ok, else ROASTER_EDEVICE */
 int  rt_fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int  rt_check(hipError_t e, const char *what);  /* 0 or ROASTER_EDEVICE with message */
 /* Grow-only device scratch slots (kept until trim/shutdown). */
-enum { SCR_IN = 0, SCR_OUT, SCR_A, SCR_B, SCR_C, SCR_D, SCR_E, SCR_F, SCR_CTRL, SCR_PF, SCR_N };
+enum { SCR_IN = 0, SCR_OUT, SCR_A, SCR_B, SCR_C, SCR_D, SCR_E, SCR_F, SCR_CTRL, SCR_PF, SCR_MM, SCR_N };
 void *rt_scratch(int slot, size_t bytes);
 void  rt_scratch_trim();
 /* Pinned host staging (grow-only). */
