@@ -258,7 +258,19 @@ extern "C" int kernel_matmul_quant_batch(const KernelMatmulJob *jobs, int n)
         if (owner[i] == i &&
             rt_check(hipMemcpyAsync(dx + xoff[i], j.X, j.T * j.cols * 4, hipMemcpyHostToDevice, R.stream), "X upload"))
             return -1;
-        if (j.T >= MM_MFMA_MIN_T && j.rows % GEMM_ROWS == 0) {
+        const bool big = j.T >= MM_MFMA_MIN_T && j.rows % GEMM_ROWS == 0;
+        if (!big && (int)j.T >= dense_mfma_min_tokens() && j.cols <= 4096) {
+            /* a few tokens: the quants-on-MFMA product, eight tokens per launch */
+            for (size_t t0 = 0; t0 < j.T; t0 += 8)
+                if (dense_mm8_launch(W, j.is_q6 ? 1 : 0, (const float *)(dx + xoff[i]) + t0 * j.cols,
+                                     (float *)(dy + yoff[i]) + t0 * j.rows, j.rows, j.cols,
+                                     (int)(j.T - t0 < 8 ? j.T - t0 : 8)))
+                    return -1;
+            hj[i] = MvJob{ W, (const float *)(dx + xoff[i]), (float *)(dy + yoff[i]), 0, (int)j.cols, 0, j.is_q6 ? 1 : 0,
+                           tasks };
+            continue;
+        }
+        if (big) {
             /* split-operand MFMA GEMM (the down GEMM of the prefill path as a
              * plain product); the job keeps a zero-task slot in the matvec launch */
             if (matmul_mfma(W, j.is_q6 ? 1 : 0, (const float *)(dx + xoff[i]), (float *)(dy + yoff[i]), j.rows, j.cols,

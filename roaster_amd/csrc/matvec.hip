@@ -355,7 +355,7 @@ __device__ __forceinline__ void mm8_block(const Mm8Q6 &r, const uint8_t *frag, c
 
 template <bool Q6>
 __global__ void __launch_bounds__(MM8_T) dense_mm8_kernel(const uint8_t *W, const uint8_t *buf, float *Y, int rows,
-                                                          int cols, int T)
+                                                          int cols, int T, int ksplit)
 {
     extern __shared__ __align__(16) uint8_t mm8_lds[];
     constexpr int SB = Q6 ? 16 : 32;                  /* weights per scale sub-block */
@@ -371,9 +371,54 @@ __global__ void __launch_bounds__(MM8_T) dense_mm8_kernel(const uint8_t *W, cons
     const float *ge = xs + (size_t)ns * 8;
     __syncthreads();
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    /* 16-row groups, wave-strided; items (group, kb) with the next item's raw
-     * quants loaded while the current computes */
     const int ngroups = (rows + 15) >> 4;
+    if (ksplit) {
+        /* few groups (nb <= 16): a workgroup per group, wave w takes super-
+         * blocks w and w + 8, the 8 partial sums added by wave 0 in wave order */
+        __shared__ float2 red[MM8_W][64];
+        const int j = lane >> 4, t0 = 2 * j;
+        for (int g = blockIdx.x; g < ngroups; g += gridDim.x) {
+            const int r = min(16 * g + (lane & 15), rows - 1);
+            const uint8_t *wr = W + (size_t)r * nb * BS;
+            Raw r0, r1;
+            const int k0 = min(wv, nb - 1), k1 = min(wv + MM8_W, nb - 1);
+            mm8_load(r0, wr + (size_t)k0 * BS, j);
+            mm8_load(r1, wr + (size_t)k1 * BS, j);
+            float y0 = 0.0f, y1 = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int kb = wv + u * MM8_W;
+                if (kb < nb) {
+                    float z0 = 0.0f, z1 = 0.0f;
+                    mm8_block(u ? r1 : r0, frag + (size_t)kb * (RQK / SB) * FB, xs + (size_t)kb * (RQK / SB) * 8, lane,
+                              z0, z1);
+                    const float2 g2 = *(const float2 *)(ge + kb * 8 + t0);
+                    y0 = fmaf(z0, g2.x, y0);
+                    y1 = fmaf(z1, g2.y, y1);
+                }
+            }
+            red[wv][lane] = make_float2(y0, y1);
+            __syncthreads();
+            if (wv == 0) {
+                float2 a = red[0][lane];
+#pragma unroll
+                for (int w = 1; w < MM8_W; w++) {
+                    const float2 b = red[w][lane];
+                    a.x += b.x;
+                    a.y += b.y;
+                }
+                const int rr = 16 * g + (lane & 15);
+                if (rr < rows) {
+                    if (t0 < T) Y[(size_t)t0 * rows + rr] = a.x;
+                    if (t0 + 1 < T) Y[(size_t)(t0 + 1) * rows + rr] = a.y;
+                }
+            }
+            __syncthreads();
+        }
+        return;
+    }
+    /* many groups: 16-row groups, wave-strided; items (group, kb) with the
+     * next item's raw quants loaded while the current computes */
     const int gw = blockIdx.x * MM8_W + wv, nw = gridDim.x * MM8_W;
     const int mine = gw < ngroups ? (ngroups - 1 - gw) / nw + 1 : 0;
     const int total = mine * nb;
@@ -416,24 +461,29 @@ __global__ void __launch_bounds__(MM8_T) dense_mm8_kernel(const uint8_t *W, cons
     }
 }
 
-static int dense_mm8_launch(const uint8_t *W, int q6, const float *X, float *Y, size_t rows, size_t cols, int T)
+int dense_mfma_min_tokens() { return g_dense_mfma_t; }
+
+int dense_mm8_launch(const uint8_t *W, int q6, const float *X, float *Y, size_t rows, size_t cols, int T)
 {
     const size_t bytes = mm8_buf_bytes(cols, q6);
     uint8_t *buf = (uint8_t *)rt_scratch(SCR_MM, bytes);
     if (!buf) return ROASTER_EDEVICE;
     const size_t ng = (rows + 15) / 16;
-    size_t blocks = (ng + MM8_W - 1) / MM8_W;
     const size_t cap = (size_t)(bytes <= 80 * 1024 ? 2 : 1) * rt().n_cu;
-    if (blocks > cap) blocks = cap;
     const int nb = (int)(cols / RQK);
+    /* fewer groups than waves in a full grid (and at most 16 super-blocks):
+     * the super-blocks of a group split over a workgroup's waves */
+    const int ksplit = ng < MM8_W * cap && nb <= 2 * MM8_W;
+    size_t blocks = ksplit ? ng : (ng + MM8_W - 1) / MM8_W;
+    if (blocks > cap) blocks = cap;
     if (q6) {
         hipLaunchKernelGGL(mm8_prep_kernel<true>, dim3(nb), dim3(256), 0, rt().stream, X, (int)cols, T, buf);
         hipLaunchKernelGGL(dense_mm8_kernel<true>, dim3((unsigned)blocks), dim3(MM8_T), bytes, rt().stream, W, buf, Y,
-                           (int)rows, (int)cols, T);
+                           (int)rows, (int)cols, T, ksplit);
     } else {
         hipLaunchKernelGGL(mm8_prep_kernel<false>, dim3(nb), dim3(256), 0, rt().stream, X, (int)cols, T, buf);
         hipLaunchKernelGGL(dense_mm8_kernel<false>, dim3((unsigned)blocks), dim3(MM8_T), bytes, rt().stream, W, buf, Y,
-                           (int)rows, (int)cols, T);
+                           (int)rows, (int)cols, T, ksplit);
     }
     return rt_check(hipGetLastError(), "dense MFMA launch") ? ROASTER_EDEVICE : 0;
 }

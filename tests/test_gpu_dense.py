@@ -3,10 +3,12 @@ oracle's matvec (kernels.c:407-432, 553-578): Q4_K / Q6_K, widths of 1..8
 super-blocks (3, 5, 6, 7 included: row lane groups rounded up to a power of
 two) and 9..16 super-blocks (two per lane: the attention output and
 DeltaNet ssm_out projections are [2048 x 4096], model.c:862, 1344-1347), 1..8
-tokens, ragged row counts, the split-operand MFMA route for several tokens
-(roaster_dense_mfma_min_tokens), and an LM-head-sized Q6_K matrix
+tokens, ragged row counts, the MFMA route for several tokens switched off
+and on (roaster_dense_mfma_min_tokens), and an LM-head-sized Q6_K matrix
 [248320 x 2048] checked on sampled rows.  Tolerance: max|d|/max|y| <= 2e-5
-(fp32 accumulation in another order; the reference test allows 2e-4)."""
+(fp32 accumulation in another order; the reference test allows 2e-4).
+Two or more tokens run with the quants as MFMA operands; small matrices and
+large ones take its two work splits."""
 import ctypes as C
 
 import numpy as np
@@ -59,19 +61,21 @@ def test_dense_matvec_invalid():
 @pytest.mark.parametrize("q6", [0, 1])
 @pytest.mark.parametrize("cols", [2048, 4096])
 def test_dense_mfma_route(q6, cols):
-    """8 tokens through the split-operand MFMA GEMM (threshold lowered to 2),
-    rows a multiple of 64, and 7 rows short of one (the matvec again)."""
+    """8 tokens with the MFMA route switched off (threshold 9: the
+    dequantising matvec) and on (threshold 2, the default), rows a multiple
+    of 16 and 7 rows short of one."""
     L = R.lib()
     old = L.roaster_dense_mfma_min_tokens(0)
-    L.roaster_dense_mfma_min_tokens(2)
     try:
-        for rows in (1024, 1017):
-            W = weights(q6, rows, cols, 60 + cols)
-            X = np.stack([R.synth_normal(61, R.synth_stream(t, cols, 5), cols) for t in range(8)])
-            Y = run(q6, W, X, rows, cols)
-            for t in range(8):
-                err = rel_err(Y[t], O.matvec(q6, W, X[t], rows, cols))
-                assert err <= TOL, (rows, t, err)
+        for thr in (9, 2):
+            L.roaster_dense_mfma_min_tokens(thr)
+            for rows in (1024, 1017):
+                W = weights(q6, rows, cols, 60 + cols)
+                X = np.stack([R.synth_normal(61, R.synth_stream(t, cols, 5), cols) for t in range(8)])
+                Y = run(q6, W, X, rows, cols)
+                for t in range(8):
+                    err = rel_err(Y[t], O.matvec(q6, W, X[t], rows, cols))
+                    assert err <= TOL, (thr, rows, t, err)
     finally:
         L.roaster_dense_mfma_min_tokens(old)
 
@@ -87,6 +91,24 @@ def test_kernels_h_matvec_odd_block_count(q6):
     fn = R.lib().kernel_matvec_q6_k if q6 else R.lib().kernel_matvec_q4_k
     fn(W.ctypes.data, x.ctypes.data, y.ctypes.data, rows, cols)
     assert rel_err(y, O.matvec(q6, W, x, rows, cols)) <= TOL
+
+
+@pytest.mark.parametrize("q6,rows,cols,T", [(1, 40009, 4096, 8), (0, 65543, 2048, 3)])
+def test_dense_mfma_many_groups(q6, rows, cols, T):
+    """Matrices with more 16-row groups than the grid has waves: the
+    wave-strided mode of the multi-token MFMA kernel (smaller matrices split
+    a group's super-blocks over a workgroup's waves), checked on sampled
+    rows for every token."""
+    log(f"dense MFMA, many groups: q6={q6} rows={rows} cols={cols} T={T}")
+    W = weights(q6, rows, cols, 70 + T)
+    X = np.stack([R.synth_normal(71, R.synth_stream(t, cols, 5), cols) for t in range(T)])
+    Y = run(q6, W, X, rows, cols)
+    pick = np.sort(np.random.default_rng(7).choice(rows, 1500, replace=False))
+    pick[-1] = rows - 1
+    Wr = np.ascontiguousarray(W.reshape(rows, -1)[pick].reshape(-1))
+    for t in range(T):
+        err = rel_err(Y[t][pick], O.matvec(q6, Wr, X[t], len(pick), cols))
+        assert err <= TOL, (t, err)
 
 
 def test_lm_head_q6k_sampled_rows():
