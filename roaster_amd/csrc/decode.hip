@@ -1200,6 +1200,23 @@ __device__ __forceinline__ float k1_gu_pair(int g6, int u6, const QChunk2 &ch, c
     return silu_mul(pg, pu);
 }
 
+/* One gate or up row's dot (k1_gu_pair's arithmetic for one of its rows). */
+__device__ __forceinline__ float k1_q_row(int q6, const QChunk &ch, const float *xn, const float *xsum, bool swz, int nb,
+                                          int lane)
+{
+    const int c = lane & 7, lb = lane >> 3;
+    float p = 0.0f;
+    if (lb < nb) {
+        const int a = lb * RQK + q_run_a_t(q6, c), b = a + (q6 ? 64 : 32);
+        float4 x0[4], x1[4];
+        load_x16(xn, a, x0, swz);
+        load_x16(xn, b, x1, swz);
+        p = q6 ? q_chunk_dot_r<true>(ch, c, x0, x1, xsum[a >> 4], xsum[b >> 4])
+               : q_chunk_dot_r<false>(ch, c, x0, x1, xsum[a >> 4], xsum[b >> 4]);
+    }
+    return group_sum<64>(p);
+}
+
 /* One down row's lane partial against a SiLU*up vector in LDS (plain layout)
  * and its run sums (down_one_token's arithmetic), reduced over the row's
  * lpr lanes. */
@@ -1594,6 +1611,12 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
             if (NPG || f < npg) {
                 const size_t j = (size_t)gi * RGP + min(wv + f * K1_W, RGP - 1);
                 gch[f].g = q_load_t(g6, ge, j, nbh, lb, c);
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < MPG; f++) {
+            if (NPG || f < npg) {
+                const size_t j = (size_t)gi * RGP + min(wv + f * K1_W, RGP - 1);
                 gch[f].u = q_load_t(u6, ue, j, nbh, lb, c);
             }
         }
@@ -1606,11 +1629,15 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
             const float part = k1_down_row(sd6, sdc_s[sdt][lane], ehsh, ehshs, live, lpr, lane);
             if (live && lr == 0) xch_put(xdsh + (size_t)gw * XCH_LN + rl, part, ep);
         }
-        /* the down rows once the gate/up rows have arrived (loads complete in
-         * order: waiting for the last one waits for all) */
+        /* the gate rows were issued first: their dots run while the up rows
+         * arrive (each waits for its own rows only: loads complete in order);
+         * then the down rows are issued, behind the up rows (issued with the
+         * gate rows they measured slower: a 64 KB burst per CU) */
+        float pgs[MPG];
+#pragma unroll
+        for (int f = 0; f < MPG; f++) pgs[f] = (NPG || f < npg) ? k1_q_row(g6, gch[f].g, xn, xsum, swz, nbh, lane) : 0.0f;
         __builtin_amdgcn_sched_barrier(0);
-        asm volatile("; gate/up rows arrived" ::"v"(gch[(NPG ? NPG : 1) - 1].u.dd), "v"(gch[(NPG ? NPG : 1) - 1].u.q.x)
-                     : "memory");
+        asm volatile("; gate rows dotted" ::"v"(pgs[0]) : "memory");
 #pragma unroll
         for (int f = 0; f < MD; f++) {
             if (ND || f < nd) {
@@ -1623,7 +1650,7 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
         for (int f = 0; f < MPG; f++) {
             const int pj = wv + f * K1_W;
             if ((NPG || f < npg) && pj < RGP) {
-                const float eh = k1_gu_pair(g6, u6, gch[f], xn, xsum, swz, nbh, lane);
+                const float eh = silu_mul(pgs[f], k1_q_row(u6, gch[f].u, xn, xsum, swz, nbh, lane));
                 if (lane == 0) xch_put_xcd(lehx + k1_run_slot(gi * RGP + pj, I), live_slot ? eh : 0.0f, ep, l2);
             }
         }
