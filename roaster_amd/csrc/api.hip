@@ -598,6 +598,7 @@ extern "C" int roaster_moe_decode_stack_noalloc(RoasterTable *t, float *h, int B
     A.ids_out = ids_out;
     A.w_out = w_out;
     A.err = (int *)base;
+    rt_aux_err_used();
     A.plan_g = (DecPlan *)(base + o_plan);
     A.logits = (float *)(base + o_log);
     A.sgate_raw = (float *)(base + o_sg);

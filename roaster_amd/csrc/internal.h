@@ -71,6 +71,7 @@ int wt_scan(uintptr_t start, size_t n, std::vector<std::pair<uintptr_t, uintptr_
 unsigned *rt_ctrl();        /* persistent-kernel control words (device) */
 int rt_take_err();           /* sync the stream, report and clear kernel error bits */
 void rt_set_aux_err(int *dev_word);   /* a second device error word rt_take_err reports and clears */
+void rt_aux_err_used();      /* a launch that may set it was queued */
 int noalloc_setup(int dev);  /* api.hip: device address of the allocation-free scratch array */
 
 void dec_release();          /* decode.hip: frees the decode exchange buffer */

@@ -92,8 +92,11 @@ extern "C" void *roaster_stream(void)
  * when reported; 4 also sends later launches' exchanges through memory. */
 static unsigned *g_ctrl;
 static int *g_aux_err;      /* error word of the allocation-free entry point's scratch, or NULL */
+static int *g_err_pin;      /* pinned host copies of the two error words */
+static bool g_aux_used;     /* a launch since the last report may have set the second word */
 
 void rt_set_aux_err(int *dev_word) { g_aux_err = dev_word; }
+void rt_aux_err_used() { g_aux_used = true; }
 
 unsigned *rt_ctrl()
 {
@@ -106,14 +109,28 @@ unsigned *rt_ctrl()
 
 int rt_take_err()
 {
-    if (rt_check(hipStreamSynchronize(g_rt.stream), "hipStreamSynchronize")) return ROASTER_EDEVICE;
-    int e = 0;
-    int *words[2] = { g_ctrl ? (int *)(g_ctrl + 16) : NULL, g_aux_err };
+    /* the error words come back with the stream's last work: copies queued
+     * behind it into pinned memory, then one synchronisation (two blocking
+     * copies cost about 20 us per call) */
+    int *words[2] = { g_ctrl ? (int *)(g_ctrl + 16) : NULL, g_aux_used ? g_aux_err : NULL };
+    g_aux_used = false;
+    if (!g_err_pin && (words[0] || words[1]) &&
+        rt_check(hipHostMalloc((void **)&g_err_pin, 64, hipHostMallocDefault), "error word hipHostMalloc")) {
+        g_err_pin = NULL;
+        return ROASTER_EDEVICE;
+    }
     for (int i = 0; i < 2; i++) {
         if (!words[i]) continue;
-        int w = 0;
-        if (rt_check(hipMemcpy(&w, words[i], sizeof(int), hipMemcpyDeviceToHost), "error word readback"))
+        g_err_pin[i] = 0;
+        if (rt_check(hipMemcpyAsync(g_err_pin + i, words[i], sizeof(int), hipMemcpyDeviceToHost, g_rt.stream),
+                     "error word readback"))
             return ROASTER_EDEVICE;
+    }
+    if (rt_check(hipStreamSynchronize(g_rt.stream), "hipStreamSynchronize")) return ROASTER_EDEVICE;
+    int e = 0;
+    for (int i = 0; i < 2; i++) {
+        if (!words[i]) continue;
+        const int w = g_err_pin[i];
         if (w && rt_check(hipMemset(words[i], 0, sizeof(int)), "error word reset")) return ROASTER_EDEVICE;
         e |= w;
     }
@@ -607,6 +624,10 @@ extern "C" void kernel_vk_shutdown(void)
     if (g_ctrl) {
         (void)hipFree(g_ctrl);
         g_ctrl = NULL;
+    }
+    if (g_err_pin) {
+        (void)hipHostFree(g_err_pin);
+        g_err_pin = NULL;
     }
     (void)hipStreamDestroy(g_rt.stream);
     g_rt.stream = NULL;
