@@ -439,9 +439,15 @@ extern "C" int kernel_ffn_fused(const KernelFfnExpert *ex, int n, const float *x
     float *dout = (float *)rt_scratch(SCR_OUT, (size_t)n * hidden * 4);
     float *eh = (float *)rt_scratch(SCR_B, 9 * inter * 4);
     DecActive *dex = (DecActive *)rt_scratch(SCR_A, sizeof(hx));
-    if (!dx || !dout || !eh || !dex) return 0;
-    if (rt_check(hipMemcpyAsync(dx, x, hidden * 4, hipMemcpyHostToDevice, R.stream), "x upload") ||
-        rt_check(hipMemcpyAsync(dex, hx, sizeof(hx), hipMemcpyHostToDevice, R.stream), "expert upload"))
+    /* pinned staging: x then the expert table (one upload), then the outputs
+     * (one download); pageable copies cost a bounce each */
+    const size_t xo = (hidden * 4 + 255) & ~(size_t)255, oo = xo + ((sizeof(hx) + 255) & ~(size_t)255);
+    uint8_t *pin = (uint8_t *)rt_pinned(3, oo + (size_t)n * hidden * 4);
+    if (!dx || !dout || !eh || !dex || !pin) return 0;
+    memcpy(pin, x, hidden * 4);
+    memcpy(pin + xo, hx, sizeof(hx));
+    if (rt_check(hipMemcpyAsync(dx, pin, hidden * 4, hipMemcpyHostToDevice, R.stream), "x upload") ||
+        rt_check(hipMemcpyAsync(dex, pin + xo, sizeof(hx), hipMemcpyHostToDevice, R.stream), "expert upload"))
         return 0;
     DecArgs A;
     memset(&A, 0, sizeof(A));
@@ -455,11 +461,11 @@ extern "C" int kernel_ffn_fused(const KernelFfnExpert *ex, int n, const float *x
     A.ffn_n = n;
     A.ffn_out = dout;
     if (dec_ffn_launch(A)) return 0;
-    for (int i = 0; i < n; i++)
-        if (rt_check(hipMemcpyAsync(ex[i].out, dout + (size_t)i * hidden, hidden * 4, hipMemcpyDeviceToHost, R.stream),
-                     "out download"))
-            return 0;
-    return rt_take_err() == 0 ? 1 : 0;
+    if (rt_check(hipMemcpyAsync(pin + oo, dout, (size_t)n * hidden * 4, hipMemcpyDeviceToHost, R.stream), "out download"))
+        return 0;
+    if (rt_take_err()) return 0;     /* synchronises the stream */
+    for (int i = 0; i < n; i++) memcpy(ex[i].out, pin + oo + (size_t)i * hidden * 4, hidden * 4);
+    return 1;
 }
 
 /* ---- table-based decode ---------------------------------------------------- */

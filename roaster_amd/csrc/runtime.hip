@@ -285,6 +285,9 @@ struct Twin {
     bool tracked;                   /* pages registered for write tracking */
     bool owns_dev;                  /* dev is this twin's own allocation */
     std::vector<uint32_t> synced;   /* per page of the span: version copied (VER_NEVER: none) */
+    uintptr_t last_a = 0;           /* the range last brought up to date, and g_epoch then */
+    size_t last_n = 0;
+    uint32_t last_epoch = 0;
 };
 struct Arena { uint8_t *host; uint8_t *dev; size_t used, size; bool tracked; };
 
@@ -410,6 +413,10 @@ static int twin_sync(Twin &T, uintptr_t h, uintptr_t a, size_t bytes)
         ++g_epoch;
         for (auto &r : runs)
             for (uintptr_t pg = r.first; pg < r.second; pg += P) set_page_ver(pg / P, g_epoch);
+    } else if (T.last_n && a == T.last_a && bytes == T.last_n && T.last_epoch == g_epoch) {
+        /* no page anywhere found written since this range was last brought up
+         * to date (every write found bumps g_epoch): nothing to copy */
+        return 0;
     }
     /* Whole pages (clipped to the twin): the scan re-protected them, so this
      * twin must now hold all of each, not only the part inside [a, a+bytes). */
@@ -430,6 +437,9 @@ static int twin_sync(Twin &T, uintptr_t h, uintptr_t a, size_t bytes)
         }
     }
     if (run1 > run0 && stage_upload(T.dev + (run0 - h), (const uint8_t *)run0, run1 - run0)) return ROASTER_EDEVICE;
+    T.last_a = a;
+    T.last_n = bytes;
+    T.last_epoch = g_epoch;
     return 0;
 }
 
