@@ -216,6 +216,11 @@ typedef struct {
  * ascending id of w * expert(X[t]) -- model.c:1671-1791.  X, Y: [T x hidden]. */
 int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, int T, float *Y,
                         const RoasterPrefillOpts *opts);
+/* The fp16-mode down GEMM (inter <= 512) as one workgroup per CU over an even
+ * split of its output tiles (1, default) or one workgroup per four output
+ * tiles (0); -1 queries.  Both give bit-identical results.  Returns the mode
+ * in force. */
+int roaster_prefill_balanced_down(int enable);
 
 #ifdef __cplusplus
 }

@@ -851,17 +851,11 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_gu_kernel(PfGemmArgs A)
 #undef GU_CASE
 }
 
-extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
+/* Per-row meta of the down GEMM for tile rows [0, mlen): slot, the row's
+ * power-of-two scale (from its part maxima) and each part's shift onto it. */
+__device__ __forceinline__ void dn_meta(const PfGemmArgs &A, const PfGroup &G, const PfTile &tile, int mlen,
+                                        V4Shared &meta)
 {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds4[];
-    __shared__ V4Shared meta;
-    const int nt_count = A.dn_nt;              /* output tiles per workgroup */
-    const int nblk = A.H / V2_DN_N / nt_count;
-    int v;
-    PfTile tile;
-    if (!v2_tile(A, nblk, v, tile)) return;
-    const PfGroup &G = A.groups[tile.grp];
-    const int mlen = min(A.chunk, G.n - tile.m0);
     const int t = threadIdx.x;
     if (t < mlen) {
         const int slot = G.slot0 + tile.m0 + t;
@@ -878,6 +872,20 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
         for (int b = 0; b < nb && b < V5_MAXPART; b++)
             meta.psh[t][b] = (int8_t)max(pf_scale_exp(A.pmax[(size_t)slot * nb + b]) - er, -64);   /* 2^-64: 0 in fp16 */
     }
+}
+
+extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds4[];
+    __shared__ V4Shared meta;
+    const int nt_count = A.dn_nt;              /* output tiles per workgroup */
+    const int nblk = A.H / V2_DN_N / nt_count;
+    int v;
+    PfTile tile;
+    if (!v2_tile(A, nblk, v, tile)) return;
+    const PfGroup &G = A.groups[tile.grp];
+    const int mlen = min(A.chunk, G.n - tile.m0);
+    dn_meta(A, G, tile, mlen, meta);
     __syncthreads();
     const int n0 = (v % nblk) * nt_count * V2_DN_N;
     const int ms = (mlen + 31) >> 5;
@@ -899,7 +907,57 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
 #undef DN_CASE
 }
 
+/* The down GEMM for inter <= 512 on a fixed grid (one workgroup per CU): the
+ * (tile, 256-row output tile) units, tile-major, are split into gridDim.x
+ * contiguous ranges of equal length, so every workgroup does the same number
+ * of output tiles and no last wave of workgroups runs on a few CUs while the
+ * rest idle.  A range crosses at most a few tiles; each piece is walked like
+ * pf2_down_kernel's nt_count tiles (activations staged once, the next output
+ * tile's weights loaded during the current one's MFMA work).  Workgroups of
+ * one XCD (grid dealt round-robin over the 8 XCDs) take neighbouring ranges,
+ * so the activation rows of a tile are fetched into one L2. */
+extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_bal_kernel(PfGemmArgs A)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds4[];
+    __shared__ V4Shared meta;
+    const int NT = A.H / V2_DN_N, Gd = (int)gridDim.x, b = blockIdx.x;
+    const int U = *A.ntiles * NT;
+    const int vb = (Gd & 7) ? b : (b & 7) * (Gd >> 3) + (b >> 3);
+    int u = (int)((long long)vb * U / Gd);
+    const int u1 = (int)((long long)(vb + 1) * U / Gd);
+    while (u < u1) {
+        const int ti = u / NT, t0 = u % NT, cnt = min(NT - t0, u1 - u);
+        const PfTile tile = A.tiles[ti];
+        const PfGroup &G = A.groups[tile.grp];
+        const int mlen = min(A.chunk, G.n - tile.m0);
+        dn_meta(A, G, tile, mlen, meta);
+        __syncthreads();
+        const int ms = (mlen + 31) >> 5, n0 = t0 * V2_DN_N;
+        if (ms == 1) {
+            if (G.dq6) v6_dn_body<1, true>(A, G, meta, mlen, n0, cnt, lds4);
+            else v6_dn_body<1, false>(A, G, meta, mlen, n0, cnt, lds4);
+        } else if (ms == 2) {
+            if (G.dq6) v6_dn_body<2, true>(A, G, meta, mlen, n0, cnt, lds4);
+            else v6_dn_body<2, false>(A, G, meta, mlen, n0, cnt, lds4);
+        } else {
+            if (G.dq6) v6_dn_body<3, true>(A, G, meta, mlen, n0, cnt, lds4);
+            else v6_dn_body<3, false>(A, G, meta, mlen, n0, cnt, lds4);
+        }
+        u += cnt;
+        __syncthreads();                        /* meta and the staged activations are rewritten next */
+    }
+}
+
 /* ---- host ----------------------------------------------------------------- */
+static int g_pf_dn_bal = 1;             /* roaster_prefill_balanced_down */
+
+extern "C" int roaster_prefill_balanced_down(int enable)
+{
+    std::lock_guard<std::recursive_mutex> g(rt_lock());
+    if (enable == 0 || enable == 1) g_pf_dn_bal = enable;
+    return g_pf_dn_bal;
+}
+
 template <int OP>
 static int launch_v1(const PfGemmArgs &A, int max_tiles)
 {
@@ -935,6 +993,13 @@ int pf_gemm_launch(const PfGemmArgs &A, int max_tiles, int op)
     hipLaunchKernelGGL(pf2_gu_kernel, dim3(max_tiles * (A.I / V2_GU_J)), dim3(V2_T), lds_gu, R.stream, A);
     if (rt_check(hipGetLastError(), "prefill gate/up launch")) return ROASTER_EDEVICE;
     PfGemmArgs D = A;
+    if (A.I <= 2 * GK && g_pf_dn_bal) {
+        /* every K step's activations fit in LDS: one workgroup per CU over an
+         * even split of the output tiles */
+        D.dn_nt = 0;
+        hipLaunchKernelGGL(pf2_down_bal_kernel, dim3(R.n_cu), dim3(V2_T), lds_dn, R.stream, D);
+        return rt_check(hipGetLastError(), "prefill down launch") ? ROASTER_EDEVICE : 0;
+    }
     /* several output tiles per workgroup when every K step's activations fit in
      * LDS and the tile count divides evenly, else one */
     D.dn_nt = A.I <= 2 * GK && (A.H / V2_DN_N) % PF_DN_NT == 0 ? PF_DN_NT : 1;

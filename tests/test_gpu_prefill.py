@@ -141,6 +141,25 @@ def test_prefill_token_permutation_bit_exact(cfg3):
     np.testing.assert_array_equal(Yp, Y[perm])
 
 
+@pytest.mark.parametrize("T", [512, 37])
+def test_prefill_balanced_down_bit_exact(cfg3, T):
+    """The down GEMM on one workgroup per CU over an even split of its output
+    tiles gives the bits of the grid with one workgroup per four tiles
+    (Zipf routing: tiles of 1..96 rows; T = 37: fewer output tiles than CUs)."""
+    X = tokens(12, T, start=5000)
+    b = zipf_bias(256, 2)
+    lib = R.lib()
+    assert lib.roaster_prefill_balanced_down(-1) == 1
+    Y1, _, ids1, _, _ = prefill(cfg3, X, bias=b)
+    try:
+        assert lib.roaster_prefill_balanced_down(0) == 0
+        Y0, _, ids0, _, _ = prefill(cfg3, X, bias=b)
+    finally:
+        lib.roaster_prefill_balanced_down(1)
+    np.testing.assert_array_equal(ids0, ids1)
+    np.testing.assert_array_equal(Y0, Y1)
+
+
 def test_prefill_reports_routing_failure(cfg3, cfg3_oracle):
     T = 70
     X = tokens(10, T, start=4000)
