@@ -1482,7 +1482,6 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
                     ss = fmaf(v.y, v.y, ss);
                     ss = fmaf(v.z, v.z, ss);
                     ss = fmaf(v.w, v.w, ss);
-                    x4[xpos(u, swz)] = v;
                     ((float4 *)hraw)[u] = v;
                 }
             }
@@ -1492,7 +1491,11 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
         K1_SYNC_DEAD();
         if (dead) break;                                  /* workgroup-uniform */
         K1_TS(1);
-        if (tid < H / 16) {
+        /* the normalised input from the h still in registers (waves 0..3,
+         * units tid and tid + 256), and the run sums: run r is units 4r ..
+         * 4r + 3, i.e. the four lanes of a quad, added pairwise by DPP in
+         * the order ((s0 + s1) + (s2 + s3)) */
+        if (tid < 256) {
             float inv = 1.0f;
             if (A.do_norm) {
                 float s2 = 0.0f;
@@ -1500,23 +1503,25 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
                 for (int w = 0; w < 4; w++) s2 += red_s[w];
                 inv = 1.0f / sqrtf(s2 / (float)H + A.eps);
             }
-            float4 q[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int u = 4 * tid + i;
-                float4 v = x4[xpos(u, swz)];
+            for (int k = 0; k < 2; k++) {
+                const int u = tid + k * 256;
+                float4 v = hq[k];
                 if (A.do_norm) {
                     v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
                     if (nwl) {
-                        const float4 wq = ((const float4 *)nwl)[u];
+                        const float4 wq = ((const float4 *)nwl)[min(u, HU - 1)];
                         v.x *= wq.x; v.y *= wq.y; v.z *= wq.z; v.w *= wq.w;
                     }
-                    x4[xpos(u, swz)] = v;
                 }
-                q[i] = v;
+                float r = (v.x + v.y) + (v.z + v.w);
+                r += dpp_f<DPP_XOR1>(r);
+                r += dpp_f<DPP_XOR2>(r);
+                if (u < HU) {
+                    x4[xpos(u, swz)] = v;
+                    if ((tid & 3) == 0) xsum[u >> 2] = r;
+                }
             }
-            xsum[tid] = ((q[0].x + q[0].y) + (q[0].z + q[0].w)) + ((q[1].x + q[1].y) + (q[1].z + q[1].w)) +
-                        (((q[2].x + q[2].y) + (q[2].z + q[2].w)) + ((q[3].x + q[3].y) + (q[3].z + q[3].w)));
         }
         __syncthreads();
         K1_TS(2);
