@@ -267,6 +267,15 @@ def cpu_baseline_prefill(table, desc, seed, X, ids, layer=0, with_router=True, r
     return out
 
 
+def warm(L, R, fn, n, what):
+    """n untimed calls of fn, then a synchronisation: the timed calls that follow
+    see the steady state (the first timed pass after a single warm-up call
+    measured about 10% slower than the following ones)."""
+    for _ in range(n):
+        fn()
+    R.check(L.roaster_sync(), what)
+
+
 def event_ms(torch, stream, fn, reps):
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
@@ -317,8 +326,7 @@ def prefill_q6_leg(torch, L, R, dev, stream, reps, with_cpu):
                 if rc:
                     raise RuntimeError(R.last_error())
 
-        run()
-        R.check(L.roaster_sync(), "prefill warmup")
+        warm(L, R, run, reps, "prefill warmup")
         ms = event_ms(torch, stream, run, reps)
         R.check(L.roaster_sync(), "prefill")
         counts = cnt.cpu().numpy()
@@ -376,8 +384,7 @@ def prefill_zipf_leg(torch, L, R, dev, stream, reps, with_cpu, with_api):
             if rc:
                 raise RuntimeError(R.last_error())
 
-        run3()
-        R.check(L.roaster_sync(), "prefill warmup")
+        warm(L, R, run3, reps, "prefill warmup")
         ms = event_ms(torch, stream, run3, reps)
         R.check(L.roaster_sync(), "prefill")
         idh = ids.cpu().numpy()
@@ -483,8 +490,7 @@ def config1_leg(torch, L, R, dev, stream, with_cpu):
         if rc:
             raise RuntimeError(R.last_error())
 
-    one(0)
-    R.check(L.roaster_sync(), "config1 warmup")
+    warm(L, R, lambda: one(0), 50, "config1 warmup")
     hot_ms = event_ms(torch, stream, lambda: one(0), 200)
     it = iter(range(10 ** 9))
     rot_ms = event_ms(torch, stream, lambda: one(next(it) % ncopy), 2 * ncopy)
@@ -543,8 +549,7 @@ def config2_leg(torch, L, R, dev, stream, with_cpu):
             if rc:
                 raise RuntimeError(R.last_error())
 
-        run()
-        R.check(L.roaster_sync(), "config2 warmup")
+        warm(L, R, run, 50, "config2 warmup")
         dev_ms = event_ms(torch, stream, run, 200)
         lat = []
         for _ in range(50):
@@ -585,8 +590,7 @@ def dense_leg(torch, L, R, dev, stream):
                 rc = L.roaster_matvec_q(dw.data_ptr(), q6, x.data_ptr(), y.data_ptr(), rows, cols, T)
                 if rc:
                     raise RuntimeError(R.last_error())
-            run()
-            R.check(L.roaster_sync(), "dense warmup")
+            warm(L, R, run, 10, "dense warmup")
             ms = event_ms(torch, stream, run, 50 if rows > 100000 else 200)
             L.roaster_dense_mfma_min_tokens(old)
             gbs = W.nbytes / (ms * 1e-3) / 1e9
@@ -665,9 +669,7 @@ def decode_legs(args, torch, L, R, dev, stream):
     }
     if B == 1:
         h8_0, h8, ids8 = stack_setup(8)
-        for _ in range(3):
-            stack_step(8, h8_0, h8, ids8)
-        R.check(L.roaster_sync(), "batch8 warmup")
+        warm(L, R, lambda: stack_step(8, h8_0, h8, ids8), 10, "batch8 warmup")
         ms8 = event_ms(torch, stream, lambda: stack_step(8, h8_0, h8, ids8), 20)
         R.check(L.roaster_sync(), "batch8")
         b8 = decode_bytes(ids8.cpu().numpy())
