@@ -182,6 +182,20 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
     /* X row: max |x| and the shared-expert gate dot.  The row (H <= 2048: at
      * most 8 float4 per lane) and the gate vector are loaded at once, indices
      * clamped, and the row stays in registers for the fp16 conversion. */
+    /* the token's logits (or router partial sums) are loaded first, so that
+     * they arrive with the X row instead of after its conversion */
+    float v4[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int e = min(lane + 64 * i, A.E - 1);
+        const size_t o = (size_t)t * A.E + e;
+        if (A.logits_in) {
+            v4[i] = A.logits_in[o];
+        } else {
+            const size_t TE = (size_t)A.T * A.E;
+            v4[i] = ((A.part[o] + A.part[TE + o]) + A.part[2 * TE + o]) + A.part[3 * TE + o];
+        }
+    }
     const float *x = A.X + (size_t)t * A.H;
     float4 xv[8], gv[8];
 #pragma unroll
@@ -224,22 +238,15 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
         }
     }
     if (lane == 0) A.sg[t] = 1.0f / (1.0f + expf(-dot));
-    /* logits */
-    float v4[4];
+    /* logits (+ bias) */
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int e = lane + 64 * i;
         float l = -INFINITY;
         if (e < A.E) {
-            const size_t o = (size_t)t * A.E + e;
-            if (A.logits_in) {
-                l = A.logits_in[o];
-            } else {
-                const size_t TE = (size_t)A.T * A.E;
-                l = ((A.part[o] + A.part[TE + o]) + A.part[2 * TE + o]) + A.part[3 * TE + o];
-            }
+            l = v4[i];
             if (A.bias) l = l + A.bias[e];
-            if (A.logits_out) A.logits_out[o] = l;
+            if (A.logits_out) A.logits_out[(size_t)t * A.E + e] = l;
         }
         v4[i] = l;
     }
@@ -262,32 +269,39 @@ extern "C" __global__ void __launch_bounds__(256) pf_bucket_kernel(const int *id
     __shared__ int wsum[4];
     const int e = blockIdx.x;
     int base = 0;
-    /* the ids of up to 8 chunks of 256 tokens are loaded at once (indices
-     * clamped), then the chunks are ranked in token order */
+    /* 2048 tokens per round: thread i takes tokens 8i .. 8i + 7 of the round
+     * (their ids loaded at once, indices clamped), counts its matches, and one
+     * block scan gives its first rank, so the ranks follow token order */
     for (int c0 = 0; c0 < T; c0 += 8 * 256) {
         int4 a[8], b[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int t = min(c0 + 256 * j + (int)threadIdx.x, T - 1);
+            const int t = min(c0 + 8 * (int)threadIdx.x + j, T - 1);
             a[j] = *(const int4 *)(ids + (size_t)t * 8);
             b[j] = *(const int4 *)(ids + (size_t)t * 8 + 4);
         }
+        int k[8], n = 0;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            if (c0 + 256 * j >= T) break;
-            const int t = c0 + 256 * j + threadIdx.x;
-            int k = -1;
+            const int t = c0 + 8 * (int)threadIdx.x + j;
+            k[j] = -1;
             if (t < T)
-                k = a[j].x == e ? 0 : a[j].y == e ? 1 : a[j].z == e ? 2 : a[j].w == e ? 3
-                  : b[j].x == e ? 4 : b[j].y == e ? 5 : b[j].z == e ? 6 : b[j].w == e ? 7 : -1;
-            int total;
-            const int r = base + block_scan_256(k >= 0 ? 1 : 0, wsum, &total);
-            if (k >= 0) {
-                list[(size_t)e * T + r] = t;
-                rank[(size_t)t * 8 + k] = r;
-            }
-            base += total;
+                k[j] = a[j].x == e ? 0 : a[j].y == e ? 1 : a[j].z == e ? 2 : a[j].w == e ? 3
+                     : b[j].x == e ? 4 : b[j].y == e ? 5 : b[j].z == e ? 6 : b[j].w == e ? 7 : -1;
+            n += k[j] >= 0 ? 1 : 0;
         }
+        int total;
+        int r = base + block_scan_256(n, wsum, &total);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (k[j] >= 0) {
+                const int t = c0 + 8 * (int)threadIdx.x + j;
+                list[(size_t)e * T + r] = t;
+                rank[(size_t)t * 8 + k[j]] = r;
+                r++;
+            }
+        }
+        base += total;
     }
     if (threadIdx.x == 0) cnt[e] = base;
 }
