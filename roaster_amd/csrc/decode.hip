@@ -1275,6 +1275,14 @@ __device__ __forceinline__ float k1_gather_run(const uint64_t *base, int I, int 
            (((v[8] + v[9]) + (v[10] + v[11])) + ((v[12] + v[13]) + (v[14] + v[15])));
 }
 
+/* Wait until an LDS flag set by another wave of the workgroup reaches v
+ * (acquire: that wave's LDS stores before the flag are then visible).  The
+ * waves that set the flags reach them through bounded waits only. */
+__device__ __forceinline__ void k1_flag_wait(int *flag, int v)
+{
+    while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < v) __builtin_amdgcn_s_sleep(1);
+}
+
 #define K1_SYNC_DEAD()          \
     do {                        \
         if (dead) s_dead = 1;   \
@@ -1379,6 +1387,7 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
     __shared__ QChunk2 shc_s[K1_MAXI / 256][64];
     __shared__ QChunk sdc_s[4][64];
     __shared__ int s_dead, s_err;
+    __shared__ int s_ids_ready, s_ehsh_ready;                  /* layer index + 1 once ids_s / ehsh are in */
 
     const int H = A.H, I = A.I, E = A.E, HU = H / 4, nbh = H / RQK, nbi = I / RQK;
     const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
@@ -1421,6 +1430,8 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
     if (tid == 0) {
         s_dead = 0;
         s_err = 0;
+        s_ids_ready = 0;
+        s_ehsh_ready = 0;
     }
 
     /* first layer: h (threads < 256: units t and t + 256), then the weights
@@ -1578,7 +1589,7 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
 #pragma unroll
             for (int i = 0; i < 4; i++)
                 if (lane + 64 * i >= E) v4[i] = -INFINITY;
-            topk8_fast(v4, E, ids_s, w_s, &s_err, &tks);
+            topk8_fast(v4, E, ids_s, w_s, &s_err, &tks, &s_ids_ready, li + 1);
             K1_TS(14);
         } else if (wv == K1_WN) {
             if (lane < SPW) {                       /* shared value j: slot j % SP of line j / SP */
@@ -1589,17 +1600,23 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
                 xch_put_xcd(lehs + k1_run_slot(j, I), v[0], ep, l2);
             }
             if (lane < I / 16) ehshs[lane] = k1_gather_run(lehs, I, lane, ep, dead, A.spin, ehsh + 16 * lane);
+            if (lane == 0) __hip_atomic_store(&s_ehsh_ready, li + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        K1_SYNC_DEAD();
-        K1_TS(4);
-        if (gw == 0) {
-            if (tid < RTOPK) {
-                const size_t o = (size_t)li * RTOPK + tid;
-                if (A.ids_out) A.ids_out[o] = ids_s[tid];
-                if (A.w_out) A.w_out[o] = w_s[tid];
+        /* the other waves go on as soon as wave 0 has stored the ids (before
+         * the softmax weights, which only wave 0 uses, in the combine) */
+        if (wv == 0) {
+            if (gw == 0) {
+                if (lane < RTOPK) {
+                    const size_t o = (size_t)li * RTOPK + lane;
+                    if (A.ids_out) A.ids_out[o] = ids_s[lane];
+                    if (A.w_out) A.w_out[o] = w_s[lane];
+                }
+                if (lane == 0 && s_err) atomicOr(A.err, 1);
             }
-            if (tid == 0 && s_err) atomicOr(A.err, 1);
+        } else {
+            k1_flag_wait(&s_ids_ready, li + 1);
         }
+        K1_TS(4);
 
         /* ---- 4. the slot's expert -------------------------------------------- */
         const int e = ids_s[grp];
@@ -1629,6 +1646,7 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
          * rows are in flight (its SiLU*up values came with the top-8): slot 8
          * of the down outputs */
         if (sdt >= 0) {
+            if (wv != K1_WN) k1_flag_wait(&s_ehsh_ready, li + 1);
             const int rl = sdt * rpw + rw_;
             const bool live = rl < RO && lbd < nbi;
             const float part = k1_down_row(sd6, sdc_s[sdt][lane], ehsh, ehshs, live, lpr, lane);

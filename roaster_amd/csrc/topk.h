@@ -90,9 +90,16 @@ __device__ __forceinline__ int topk_round(uint32_t key[4], int r, float &v, int 
 /* Softmax over the selected logits (lane k holds slot k's), summed in slot
  * order like the reference; lanes 0..7 write ids and weights, and *bad is set
  * when fewer than 8 logits were selectable (the remaining ids are -1). */
-__device__ __forceinline__ void topk_finish(float v, int myid, int nsel, int *ids, float *w, int *bad)
+__device__ __forceinline__ void topk_finish(float v, int myid, int nsel, int *ids, float *w, int *bad,
+                                            int *ready = nullptr, int ready_val = 0)
 {
     const int lane = threadIdx.x & 63;
+    if (ready) {
+        /* ids first, then the flag (release: the ids' LDS stores complete
+         * before it), then the weights */
+        if (lane < RTOPK) ids[lane] = myid;
+        if (lane == 0) __hip_atomic_store(ready, ready_val, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
     const float mx = lane_f(v, 0);
     const float ex = expf(v - mx);
     float sum = 0.0f;
@@ -109,7 +116,8 @@ __device__ __forceinline__ void topk_finish(float v, int myid, int nsel, int *id
 /* Wave-level top-8 of one token (model.c:869-897).  Each logit becomes an
  * order-preserving 32-bit key (NaN and -inf: key 0, never selected); eight
  * rounds of topk_round, then the softmax over the selected logits. */
-static __device__ void topk8_wave(const float v4in[4], int E, int *ids, float *w, int *bad)
+static __device__ void topk8_wave(const float v4in[4], int E, int *ids, float *w, int *bad, int *ready = nullptr,
+                                  int ready_val = 0)
 {
     uint32_t key[4];
     topk_keys(v4in, E, key);
@@ -120,7 +128,7 @@ static __device__ void topk8_wave(const float v4in[4], int E, int *ids, float *w
         if (topk_round(key, r, v, myid) < 0) break;     /* no selectable logit left */
         nsel++;
     }
-    topk_finish(v, myid, nsel, ids, w, bad);
+    topk_finish(v, myid, nsel, ids, w, bad, ready, ready_val);
 }
 
 /* LDS scratch of topk8_fast, per wave. */
@@ -147,7 +155,8 @@ __device__ __forceinline__ unsigned long long topk_ck(uint32_t key, int e)
  * fills slot r.  The rounds of topk8_wave run instead when more than 64 keys
  * qualify (many ties at the threshold, or a group without a selectable
  * logit).  All 64 lanes must be active; S is this wave's scratch. */
-static __device__ void topk8_fast(const float v4in[4], int E, int *ids, float *w, int *bad, TopkScratch *S)
+static __device__ void topk8_fast(const float v4in[4], int E, int *ids, float *w, int *bad, TopkScratch *S,
+                                  int *ready = nullptr, int ready_val = 0)
 {
     const int lane = threadIdx.x & 63;
     uint32_t key[4];
@@ -171,7 +180,7 @@ static __device__ void topk8_fast(const float v4in[4], int E, int *ids, float *w
         n += __builtin_popcountll(b[i]);
     }
     if (n > 64) {                                   /* wave-uniform */
-        topk8_wave(v4in, E, ids, w, bad);
+        topk8_wave(v4in, E, ids, w, bad, ready, ready_val);
         return;
     }
     S->cand[lane] = 0ull;                           /* entries past the candidates compare below every key */
@@ -229,7 +238,7 @@ static __device__ void topk8_fast(const float v4in[4], int E, int *ids, float *w
     const bool sel = lane < RTOPK && sk != 0ull;
     const float v = sel ? key_logit((uint32_t)(sk >> 32)) : -INFINITY;
     const int myid = sel ? 255 - (int)(uint32_t)sk : -1;
-    topk_finish(v, myid, min(n, RTOPK), ids, w, bad);
+    topk_finish(v, myid, min(n, RTOPK), ids, w, bad, ready, ready_val);
 }
 
 #endif
