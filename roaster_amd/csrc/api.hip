@@ -486,7 +486,7 @@ static int dec_scratch(DecArgs &A)
     A.sgate_raw = (float *)rt_scratch(SCR_E, B * 4);
     A.eh = (float *)rt_scratch(SCR_F, B * 9 * (size_t)A.I * 4);
     A.xn_g = (float *)rt_scratch(SCR_B, B * ((size_t)A.H + A.H / 16) * 4);
-    if (dec_layer1_ok(A.E, A.H, A.I, A.B) && !(A.xbuf = dec_xch_default(A.E, A.H, A.I))) return ROASTER_ENOMEM;
+    if ((dec_layer1_ok(A.E, A.H, A.I, A.B) || dec_layerB_ok(A.E, A.H, A.I, A.B)) && !(A.xbuf = dec_xch_default(A.E, A.H, A.I))) return ROASTER_ENOMEM;
     return A.logits && A.sgate_raw && A.eh && A.xn_g ? 0 : ROASTER_ENOMEM;
 }
 

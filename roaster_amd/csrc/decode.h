@@ -105,6 +105,25 @@ struct DecArgs {
 #define XCH_LH(I) ((size_t)256 + 2 * (size_t)(I))
 #define XCH_U64(E, H, I) (XCH_LOC0(E, H, I) + 8 * XCH_LOCN(E, H, I))
 
+/* The same regions for the batched one-launch stack (2..8 tokens, sized for
+ * NB >= B tokens), each with a token index outermost: logits [NB][256][16],
+ * shared SiLU*up [NB][256][16], routed down outputs [NB][8][H], shared down
+ * outputs [NB][256][16]; per XCD: logits [NB][256], shared SiLU*up [NB][I],
+ * routed SiLU*up [NB][I], next hidden state [NB][H] (the per-token vectors in
+ * the run-major layouts above). */
+#define XCHB_LG(NB, E, H, I) ((size_t)0)
+#define XCHB_EHS(NB, E, H, I) ((size_t)(NB) * 256 * XCH_LN)
+#define XCHB_DX(NB, E, H, I) (XCHB_EHS(NB, E, H, I) + (size_t)(NB) * 256 * XCH_LN)
+#define XCHB_DSH(NB, E, H, I) (XCHB_DX(NB, E, H, I) + (size_t)(NB) * 8 * (size_t)(H))
+#define XCHB_LOC0(NB, E, H, I) (XCHB_DSH(NB, E, H, I) + (size_t)(NB) * 256 * XCH_LN)
+#define XCHB_LOCN(NB, E, H, I) ((size_t)(NB) * ((size_t)256 + 2 * (size_t)(I) + (size_t)(H)))
+#define XCHB_LLG(NB, I) ((size_t)0)
+#define XCHB_LEHS(NB, I) ((size_t)(NB) * 256)
+#define XCHB_LEHX(NB, I) ((size_t)(NB) * ((size_t)256 + (size_t)(I)))
+#define XCHB_LH(NB, I) ((size_t)(NB) * ((size_t)256 + 2 * (size_t)(I)))
+#define XCHB_U64(NB, E, H, I) (XCHB_LOC0(NB, E, H, I) + 8 * XCHB_LOCN(NB, E, H, I))
+#define K1B_MAXB 8                                  /* tokens of the batched one-launch stack */
+
 /* Exchange buffer of the one-launch stack: the slots and the last epoch
  * written into them.  Epochs grow by one per layer; before the 32-bit epoch
  * would wrap, the slots are cleared (by a fill kernel) and epochs start
@@ -119,6 +138,9 @@ int dec_ffn_launch(DecArgs &A);      /* kernel_ffn_fused: gate/up + down kernels
 /* Whether one token's layers can run as one launch (dec_stack1_kernel) for
  * these shapes on this device. */
 bool dec_layer1_ok(int E, int H, int I, int B);
+/* Whether B = 2..8 tokens' layers can run as one launch (dec_stackB_kernel)
+ * for these shapes on this device (the matrix types are checked per launch). */
+bool dec_layerB_ok(int E, int H, int I, int B);
 /* The library's exchange buffer (allocated and cleared on first use). */
 DecXch *dec_xch_default(int E, int H, int I);
 

@@ -1738,6 +1738,399 @@ extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stack1_kernel(DecArgs 
  * gate/up Q4_K and down Q6_K, routed and shared (types 0b100100) */
 extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stack1_2x2_kernel(DecArgs A) { stack1_body<2, 2, 0x24>(A); }
 
+/* ---- the batched one-launch stack: 2..8 tokens --------------------------------
+ * The one-token stack's groups and exchanges with a token index: group k (an
+ * XCD) serves slot k of every token (the token's k-th expert), so the chain
+ * of exchanges per layer is the one-token chain carrying B values where it
+ * carried one, and the expert rows of the B tokens are streamed back to back.
+ * Per layer:
+ *   1. every thread u < H/4: unit u of each token's h (this XCD's copy, or the
+ *      caller's h in the first layer), RMSNorm per token (the sums of squares
+ *      as lane partials, wave sums in wave order), the normalised inputs and
+ *      their run sums in LDS, and the owned rows' residuals;
+ *   2. router row gw (wave K1_WR), the shared-gate logits (K1_WGI) and this
+ *      workgroup's shared SiLU*up pairs (the last SP waves) for every token;
+ *   3. wave 0 relays the logits, wave K1_WN the shared values, into the XCD's
+ *      region; wave b ranks token b's top 8 and gathers its shared SiLU*up;
+ *   4. the slot experts' gate/up rows token after token (the next token's rows
+ *      in flight while the current one's are dotted), SiLU*up within the XCD,
+ *      wave b gathers token b's; the down rows likewise; the shared expert's
+ *      down rows;
+ *   5. wave b combines token b's owned rows (model.c:1139-1144 order) and
+ *      publishes them within the XCD.
+ * Shapes: inter 512, hidden 1280..2048; gate/up Q4_K and down Q6_K, routed
+ * and shared (dec_layerB_ok and the launch check the rest).  Results agree
+ * with the three-kernel path within float rounding (the sums of squares are
+ * added in a different order). */
+template <int NB>
+__device__ __forceinline__ void k1b_gather_h(const uint64_t *lh, int H, int HU, int u, int B, uint32_t ep, int &dead,
+                                             uint32_t spin, float4 (&hv)[NB])
+{
+    uint64_t r[NB][4];
+    const int uc = min(u, HU - 1);
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) r[b][i] = xch_load(lh + (size_t)b * H + (size_t)i * HU + uc);
+    unsigned it = 0;
+    for (;;) {
+        unsigned miss = 0;
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                miss |= b < B && u < HU && (uint32_t)(r[b][i] >> 32) != ep ? 1u << (4 * b + i) : 0u;
+        if (!miss || dead) break;
+        if (++it > spin) {
+            dead = 1;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(K1_POLL_SLEEP);
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if ((miss >> (4 * b + i)) & 1u) r[b][i] = xch_load(lh + (size_t)b * H + (size_t)i * HU + uc);
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+        hv[b] = make_float4(__builtin_bit_cast(float, (uint32_t)r[b][0]), __builtin_bit_cast(float, (uint32_t)r[b][1]),
+                            __builtin_bit_cast(float, (uint32_t)r[b][2]), __builtin_bit_cast(float, (uint32_t)r[b][3]));
+}
+
+template <int NB>
+__device__ __forceinline__ void stackB_body(const DecArgs &A)
+{
+    __shared__ __align__(16) float xn[NB][K1_MAXH];
+    __shared__ float xsum[NB][K1_MAXH / 16];
+    __shared__ float hown[NB][64];                           /* the owned rows' residual */
+    __shared__ __align__(16) float ehk[NB][512];
+    __shared__ float ehks[NB][512 / 16];
+    __shared__ __align__(16) float ehsh[NB][512];
+    __shared__ float ehshs[NB][512 / 16];
+    __shared__ TopkScratch tks[NB];
+    __shared__ int ids_s[NB][RTOPK];
+    __shared__ float w_s[NB][RTOPK + 1];
+    __shared__ float red_s[K1_W][NB];
+    __shared__ __align__(16) DecLayer Ls[K1_MAXL];
+    __shared__ float4 rrow_s[8][64];                          /* router row gw */
+    __shared__ float4 gin_s[8][64];                           /* shared-gate vector */
+    __shared__ QChunk2 shc_s[2][64];                          /* this workgroup's shared gate/up pairs */
+    __shared__ int s_dead, s_err;
+
+    constexpr int I = 512, nbi = 2, SP = 2, RGP = I / K1_GW;
+    const int H = A.H, E = A.E, B = A.B, HU = H / 4, nbh = H / RQK;
+    const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 0xFu;
+    const bool l2 = A.xl2 && xcc < (unsigned)K1_G;
+    if (A.xl2 && !l2 && threadIdx.x == 0) atomicOr(A.err, 4);
+    const int grp = l2 ? (int)xcc : (int)(blockIdx.x % K1_G), gi = blockIdx.x / K1_G, gw = blockIdx.x;
+    const bool swz = A.xswz;
+    uint64_t *xlg = A.xch + XCHB_LG(NB, E, H, I), *xehs = A.xch + XCHB_EHS(NB, E, H, I);
+    uint64_t *xdx = A.xch + XCHB_DX(NB, E, H, I), *xdsh = A.xch + XCHB_DSH(NB, E, H, I);
+    uint64_t *loc = A.xch + XCHB_LOC0(NB, E, H, I) + (size_t)grp * XCHB_LOCN(NB, E, H, I);
+    uint64_t *llg = loc + XCHB_LLG(NB, I), *lehs = loc + XCHB_LEHS(NB, I), *lehx = loc + XCHB_LEHX(NB, I);
+    uint64_t *lh = loc + XCHB_LH(NB, I);
+    const int RO = H / 256, RD = H / K1_GW;
+    const int LPW = E / K1_GW, SPW = I / K1_GW;
+    const int lpr = lanes_per_row(nbi), rpw = 64 / lpr;
+    const int nsd = (RO + rpw - 1) / rpw, sdt = wv - (K1_W - nsd);
+    const int ndt = (RD + rpw - 1) / rpw;
+    const bool rrow = gw < E && !A.logits_in;
+    const int n = A.nlayers;
+    if (tid == 0) {
+        s_dead = 0;
+        s_err = 0;
+    }
+    int dead = (gld_u32(A.err) & 2u) != 0;
+    constexpr int DQ = (int)(sizeof(DecLayer) / 16);
+    if (tid < n * DQ) ((uint4 *)Ls)[tid] = ((const uint4 *)(A.layers + A.layer0))[tid];
+    __syncthreads();
+
+    for (int li = 0; li < n; li++) {
+        int tid_v = (int)threadIdx.x;
+        asm volatile("" : "+v"(tid_v));
+        const int tid = tid_v, lane = tid_v & 63, c = lane & 7, lb = lane >> 3;
+        const int rw_ = lane / lpr, lr = lane % lpr, lbd = lr >> 3;
+        const int l = A.layer0 + li;
+        const uint32_t ep = A.epoch + (uint32_t)li;
+        const bool last = li + 1 == n;
+        const DecLayer L = k1_layer(Ls, li);
+        const float *nwg = A.do_norm && A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * H : NULL;
+
+        /* ---- 1. this layer's own weights first (they do not depend on h),
+         * then h, normalised per token ---------------------------------------- */
+        float4 rw[8];
+        QChunk2 shc;
+        QChunk sdc;
+        if ((wv == K1_WR && rrow) || wv == K1_WGI) {
+            const float *row = wv == K1_WR ? L.router + (size_t)gw * H : L.gate_inp;
+#pragma unroll
+            for (int m = 0; m < 8; m++) rw[m] = gld_f4(row + min(4 * lane + 256 * m, H - 4));
+        }
+        if (wv >= K1_W - SP) {
+            const size_t j = (size_t)gw * SP + (wv - (K1_W - SP));
+            shc.g = q_load_t(0, L.sgate, j, nbh, lb, c);
+            shc.u = q_load_t(0, L.sup, j, nbh, lb, c);
+        }
+        if (sdt >= 0) sdc = q_load_t(1, L.sdown, (size_t)min(gw * RO + sdt * rpw + rw_, H - 1), nbi, lr >> 3, lr & 7);
+        const int u = tid;
+        const float4 nwv = nwg ? ((const float4 *)nwg)[min(u, HU - 1)] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        float4 hv[NB];
+        if (li == 0) {
+#pragma unroll
+            for (int b = 0; b < NB; b++) hv[b] = ((const float4 *)A.h)[(size_t)min(b, B - 1) * HU + min(u, HU - 1)];
+        } else {
+            k1b_gather_h<NB>(lh, H, HU, u, B, ep - 1, dead, A.spin, hv);
+        }
+        /* parked for the per-token dots of phase 2 (their loads were issued
+         * before the gather's and have completed with it) */
+        if ((wv == K1_WR && rrow) || wv == K1_WGI) {
+            float4 (*dst)[64] = wv == K1_WR ? rrow_s : gin_s;
+#pragma unroll
+            for (int m = 0; m < 8; m++) dst[m][lane] = rw[m];
+        }
+        if (wv >= K1_W - SP) shc_s[wv - (K1_W - SP)][lane] = shc;
+        /* the raw h (read back for the sums of squares) and the owned rows'
+         * residual: units gi RD / 4 .. + RD / 4 */
+        if (u < HU) {
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+                if (b < B) ((float4 *)xn[b])[u] = hv[b];
+        }
+        {
+            const int o = u - gi * (RD / 4);
+            if (o >= 0 && o < RD / 4) {
+#pragma unroll
+                for (int b = 0; b < NB; b++) {
+                    hown[b][4 * o] = hv[b].x;
+                    hown[b][4 * o + 1] = hv[b].y;
+                    hown[b][4 * o + 2] = hv[b].z;
+                    hown[b][4 * o + 3] = hv[b].w;
+                }
+            }
+        }
+        K1_SYNC_DEAD();
+        if (dead) break;                                  /* workgroup-uniform */
+        /* sums of squares in the one-token order: lane t adds units t and
+         * t + 256, waves 0..3, the four wave sums in wave order */
+        if (A.do_norm && tid < 256) {
+            for (int b = 0; b < B; b++) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    const int uu = tid + 256 * k;
+                    if (uu < HU) {
+                        const float4 v = ((const float4 *)xn[b])[uu];
+                        ss = fmaf(v.x, v.x, ss);
+                        ss = fmaf(v.y, v.y, ss);
+                        ss = fmaf(v.z, v.z, ss);
+                        ss = fmaf(v.w, v.w, ss);
+                    }
+                }
+                ss = group_sum<64>(ss);
+                if (lane == 0) red_s[wv][b] = ss;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            if (b >= B) break;
+            float4 v = hv[b];
+            if (A.do_norm) {
+                float s2 = 0.0f;
+#pragma unroll
+                for (int w = 0; w < 4; w++) s2 += red_s[w][b];
+                const float inv = 1.0f / sqrtf(s2 / (float)H + A.eps);
+                v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
+                if (nwg) { v.x *= nwv.x; v.y *= nwv.y; v.z *= nwv.z; v.w *= nwv.w; }
+            }
+            float r = (v.x + v.y) + (v.z + v.w);
+            r += dpp_f<DPP_XOR1>(r);
+            r += dpp_f<DPP_XOR2>(r);
+            if (u < HU) {
+                ((float4 *)xn[b])[xpos(u, swz)] = v;
+                if ((u & 3) == 0) xsum[b][u >> 2] = r;
+            }
+        }
+        __syncthreads();
+
+        /* ---- 2. per token b, on wave b: router logit gw, then the shared-gate
+         * logit; the 2 B shared SiLU*up values (pair t & 1 of token t >> 1)
+         * dealt to the waves in turn ------------------------------------------ */
+        for (int b = wv; b < B; b += K1_W) {
+            float4 r4[8];
+            if (rrow) {
+#pragma unroll
+                for (int m = 0; m < 8; m++) r4[m] = rrow_s[m][lane];
+                const float s = k1_row_dot(r4, (const float4 *)xn[b], H, swz, lane);
+                if (lane == 0) {
+                    xch_put(xlg + ((size_t)b * 256 + gw) * XCH_LN, s, ep);
+                    if (last) A.logits[(size_t)b * E + gw] = s;
+                }
+            }
+        }
+        for (int t = wv; t < SP * B; t += K1_W) {
+            const int pr = t % SP, b = t / SP;
+            const float eh = k1_gu_pair(0, 0, shc_s[pr][lane], xn[b], xsum[b], swz, nbh, lane);
+            if (lane == 0) xch_put(xehs + ((size_t)b * 256 + gw) * XCH_LN + pr, eh, ep);
+        }
+        for (int b = wv; b < B; b += K1_W) {
+            float4 r4[8];
+#pragma unroll
+            for (int m = 0; m < 8; m++) r4[m] = gin_s[m][lane];
+            const float s = k1_row_dot(r4, (const float4 *)xn[b], H, swz, lane);
+            if (lane == 0) w_s[b][RTOPK] = 1.0f / (1.0f + expf(-s));
+        }
+
+        /* ---- 3. relays into the XCD's region; token b's top 8 (wave b) and its
+         * shared SiLU*up values -------------------------------------------------- */
+        if (wv == 0 && !A.logits_in && lane < B * LPW) {
+            const int b = lane / LPW, j = gi * LPW + lane % LPW;
+            const uint64_t *q[1] = {xlg + ((size_t)b * 256 + j) * XCH_LN};
+            float v[1];
+            xch_gather<1>(q, 1u, ep, dead, A.spin, v);
+            xch_put_xcd(llg + (size_t)b * 256 + j, v[0], ep, l2);
+        } else if (wv == K1_WN) {
+            for (int idx = lane; idx < B * SPW; idx += 64) {
+                const int b = idx / SPW, j = gi * SPW + idx % SPW;
+                const uint64_t *q[1] = {xehs + ((size_t)b * 256 + j / SP) * XCH_LN + j % SP};
+                float v[1];
+                xch_gather<1>(q, 1u, ep, dead, A.spin, v);
+                xch_put_xcd(lehs + (size_t)b * I + k1_run_slot(j, I), v[0], ep, l2);
+            }
+        }
+        if (wv < B) {
+            const int b = wv;
+            float v4[4];
+            if (A.logits_in) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) v4[i] = A.logits_in[(size_t)b * E + min(lane + 64 * i, E - 1)];
+            } else {
+                const uint64_t *q[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) q[i] = llg + (size_t)b * 256 + min(lane + 64 * i, E - 1);
+                xch_gather<4>(q, 0xFu, ep, dead, A.spin, v4);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (lane + 64 * i >= E) v4[i] = -INFINITY;
+            topk8_fast(v4, E, ids_s[b], w_s[b], &s_err, &tks[b]);
+            if (lane < I / 16) ehshs[b][lane] = k1_gather_run(lehs + (size_t)b * I, I, lane, ep, dead, A.spin, ehsh[b] + 16 * lane);
+        }
+        K1_SYNC_DEAD();
+        if (gw == 0) {
+            if (tid < B * RTOPK) {
+                const size_t o = ((size_t)li * B + (tid >> 3)) * RTOPK + (tid & 7);
+                if (A.ids_out) A.ids_out[o] = ids_s[tid >> 3][tid & 7];
+                if (A.w_out) A.w_out[o] = w_s[tid >> 3][tid & 7];
+            }
+            if (tid == 0 && s_err) atomicOr(A.err, 1);
+        }
+
+        /* ---- 4. the slot experts of the B tokens -------------------------- */
+        {
+            QChunk2 cur[2], nxt[2];
+            auto gu_load = [&](int b, QChunk2 (&ch)[2]) {
+                const int e = ids_s[min(b, B - 1)][grp];
+                const size_t ee = e >= 0 ? (size_t)e : 0;
+                const uint8_t *ge = L.gate + ee * L.eb[0], *ue = L.up + ee * L.eb[1];
+#pragma unroll
+                for (int f = 0; f < 2; f++) ch[f].g = q_load_t(0, ge, (size_t)gi * RGP + wv + f * K1_W, nbh, lb, c);
+#pragma unroll
+                for (int f = 0; f < 2; f++) ch[f].u = q_load_t(0, ue, (size_t)gi * RGP + wv + f * K1_W, nbh, lb, c);
+            };
+            gu_load(0, cur);
+            for (int b = 0; b < B; b++) {
+                const bool live_slot = ids_s[b][grp] >= 0;
+                gu_load(b + 1, nxt);                 /* the next token's rows in flight (past the last: unused) */
+#pragma unroll
+                for (int f = 0; f < 2; f++) {
+                    const int pj = wv + f * K1_W;
+                    const float pg = k1_q_row(0, cur[f].g, xn[b], xsum[b], swz, nbh, lane);
+                    const float eh = silu_mul(pg, k1_q_row(0, cur[f].u, xn[b], xsum[b], swz, nbh, lane));
+                    if (lane == 0) xch_put_xcd(lehx + (size_t)b * I + k1_run_slot(gi * RGP + pj, I), live_slot ? eh : 0.0f, ep, l2);
+                }
+#pragma unroll
+                for (int f = 0; f < 2; f++) cur[f] = nxt[f];
+            }
+        }
+        /* the shared expert's down rows [gw RO, (gw + 1) RO) for every token */
+        if (sdt >= 0) {
+            const int rl = sdt * rpw + rw_;
+            const bool live = rl < RO && lbd < nbi;
+            for (int b = 0; b < B; b++) {
+                const float part = k1_down_row(1, sdc, ehsh[b], ehshs[b], live, lpr, lane);
+                if (live && lr == 0) xch_put(xdsh + ((size_t)b * 256 + gw) * XCH_LN + rl, part, ep);
+            }
+        }
+        if (wv < B && lane < I / 16)
+            ehks[wv][lane] = k1_gather_run(lehx + (size_t)wv * I, I, lane, ep, dead, A.spin, ehk[wv] + 16 * lane);
+        K1_SYNC_DEAD();
+        {
+            QChunk cur[2], nxt[2];
+            auto dn_load = [&](int b, QChunk (&ch)[2]) {
+                const int e = ids_s[min(b, B - 1)][grp];
+                const size_t ee = e >= 0 ? (size_t)e : 0;
+                const uint8_t *de = L.down + ee * L.eb[2];
+#pragma unroll
+                for (int f = 0; f < 2; f++) {
+                    const int task = min(wv + f * K1_W, ndt - 1);
+                    ch[f] = q_load_t(1, de, (size_t)min(gi * RD + task * rpw + rw_, H - 1), nbi, lbd, lr & 7);
+                }
+            };
+            dn_load(0, cur);
+            for (int b = 0; b < B; b++) {
+                const bool live_slot = ids_s[b][grp] >= 0;
+                dn_load(b + 1, nxt);
+#pragma unroll
+                for (int f = 0; f < 2; f++) {
+                    const int task = wv + f * K1_W;
+                    if (task < ndt) {
+                        const int rl = task * rpw + rw_, row = gi * RD + rl;
+                        const bool live = rl < RD && lbd < nbi;
+                        const float part = k1_down_row(1, cur[f], ehk[b], ehks[b], live, lpr, lane);
+                        if (live && lr == 0) xch_put(xdx + ((size_t)b * 8 + grp) * H + row, live_slot ? part : 0.0f, ep);
+                    }
+                }
+#pragma unroll
+                for (int f = 0; f < 2; f++) cur[f] = nxt[f];
+            }
+        }
+
+        /* ---- 5. wave b: token b's owned rows combined (model.c:1139-1144) --- */
+        if (wv < B) {
+            const int b = wv;
+            const int row = gi * RD + min(lane, RD - 1);
+            const uint64_t *q[RTOPK + 1];
+            float d[RTOPK + 1];
+#pragma unroll
+            for (int k = 0; k < RTOPK; k++) q[k] = xdx + ((size_t)b * 8 + k) * H + row;
+            q[RTOPK] = xdsh + ((size_t)b * 256 + row / RO) * XCH_LN + row % RO;
+            xch_gather<RTOPK + 1>(q, lane < RD ? 0x1FFu : 0u, ep, dead, A.spin, d);
+            if (lane < RD) {
+                float y = 0.0f;
+#pragma unroll
+                for (int k = 0; k < RTOPK; k++) y = fmaf(w_s[b][k], d[k], y);
+                y = fmaf(w_s[b][RTOPK], d[RTOPK], y);
+                const float hn = hown[b][lane] + y;
+                if (!last) xch_put_xcd(lh + (size_t)b * H + (size_t)(row & 3) * HU + (row >> 2), hn, ep, l2);
+                else if (grp == 0) {
+                    if (A.y) A.y[(size_t)b * H + row] = y;
+                    else A.h[(size_t)b * H + row] = hn;
+                }
+            }
+        }
+    }
+    if (tid == 0 && (dead || s_dead)) atomicOr(A.err, 2);
+}
+
+extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stackB2_kernel(DecArgs A) { stackB_body<2>(A); }
+extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stackB4_kernel(DecArgs A) { stackB_body<4>(A); }
+extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stackB8_kernel(DecArgs A) { stackB_body<8>(A); }
+
 /* Every workgroup's XCC_ID, in a grid of the stack kernel's shape. */
 extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_xcd_probe_kernel(unsigned *out)
 {
@@ -1807,6 +2200,15 @@ bool dec_layer1_ok(int E, int H, int I, int B)
            H <= K1_MAXH && I % RQK == 0 && I <= K1_MAXI;
 }
 
+/* The batched kernel's shapes: inter 512 (two gate/up rows and two down
+ * tasks per wave), hidden 512..2048 in whole 256-row blocks, at most 256
+ * experts (one logit per lane of a wave's 64 for 8 tokens). */
+bool dec_layerB_ok(int E, int H, int I, int B)
+{
+    return g_layer1 && B >= 2 && B <= K1B_MAXB && rt().n_cu >= K1_NWG && E >= RTOPK && E <= 256 && E % K1_GW == 0 &&
+           I == 512 && H % 256 == 0 && H >= 512 && H <= K1_MAXH;
+}
+
 static DecXch g_xch;
 
 void dec_release()
@@ -1819,7 +2221,7 @@ void dec_release()
 
 DecXch *dec_xch_default(int E, int H, int I)
 {
-    const size_t n = (size_t)XCH_U64(E, H, I);
+    const size_t n = std::max((size_t)XCH_U64(E, H, I), (size_t)XCHB_U64(K1B_MAXB, E, H, I));
     if (g_xch.p && g_xch.n >= n) return &g_xch;
     if (g_xch.p) {
         (void)hipStreamSynchronize(rt().stream);
@@ -1902,6 +2304,45 @@ static int launch_stack1(DecArgs &A0)
     return 0;
 }
 
+/* One launch per run of up to K1_MAXL layers of B = 2..8 tokens
+ * (dec_stackB*_kernel, the smallest of 2, 4, 8 slots that holds B), when
+ * every layer has Q4_K gate/up and Q6_K down matrices, routed and shared;
+ * else 1 (the caller runs the three-kernel path). */
+static int launch_stackB(DecArgs &A0)
+{
+    if (!A0.layers_h) return 1;
+    for (int l = A0.layer0; l < A0.layer0 + A0.nlayers; l++) {
+        const DecLayer *Lh = A0.layers_h + l;
+        if (Lh->q6[0] || Lh->q6[1] || !Lh->q6[2] || Lh->sq6[0] || Lh->sq6[1] || !Lh->sq6[2]) return 1;
+    }
+    DecXch &X = *A0.xbuf;
+    if (X.n < (size_t)XCHB_U64(K1B_MAXB, A0.E, A0.H, A0.I)) return 1;
+    for (int c0 = A0.layer0; c0 < A0.layer0 + A0.nlayers; c0 += K1_MAXL) {
+        const int cn = min(K1_MAXL, A0.layer0 + A0.nlayers - c0), off = c0 - A0.layer0;
+        DecArgs A = A0;
+        A.xch = X.p;
+        A.layer0 = c0;
+        A.nlayers = cn;
+        if (A.ids_out) A.ids_out += (size_t)off * A.B * RTOPK;
+        if (A.w_out) A.w_out += (size_t)off * A.B * RTOPK;
+        if (A.norm_w) A.norm_w += (size_t)off * A.H;
+        if (X.epoch > 0xFFFFFFFFu - (uint32_t)cn - 1u) {  /* epochs start again on cleared slots */
+            hipLaunchKernelGGL(dec_xch_clear_kernel, dim3(64), dim3(256), 0, rt().stream, X.p, X.n);
+            if (rt_check(hipGetLastError(), "exchange buffer clear")) return ROASTER_EDEVICE;
+            X.epoch = 0;
+        }
+        A.epoch = X.epoch + 1;
+        X.epoch += (uint32_t)cn;
+        A.spin = g_spin;
+        A.xl2 = g_xl2 == 1;
+        if (A.B <= 2) hipLaunchKernelGGL(dec_stackB2_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
+        else if (A.B <= 4) hipLaunchKernelGGL(dec_stackB4_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
+        else hipLaunchKernelGGL(dec_stackB8_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
+        if (rt_check(hipGetLastError(), "stack launch")) return ROASTER_EDEVICE;
+    }
+    return 0;
+}
+
 int dec_launch(DecArgs &A)
 {
     A.xswz = A.H % 512 == 0;
@@ -1913,6 +2354,8 @@ int dec_launch(DecArgs &A)
         A.err = (int *)(ctrl + 16);
     }
     if (A.xbuf && !A.ffn_out && dec_layer1_ok(A.E, A.H, A.I, A.B)) return launch_stack1(A);
+    if (A.xbuf && !A.ffn_out && dec_layerB_ok(A.E, A.H, A.I, A.B))
+        if (int rc = launch_stackB(A); rc <= 0) return rc;
     for (int l = A.layer0; l < A.layer0 + A.nlayers; l++)
         if (int rc = launch_layer(A, l, true)) return rc;
     return 0;
