@@ -1763,15 +1763,15 @@ extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stack1_2x2_kernel(DecA
  * with the three-kernel path within float rounding (the sums of squares are
  * added in a different order). */
 template <int NB>
-__device__ __forceinline__ void k1b_gather_h(const uint64_t *lh, int H, int HU, int u, int B, uint32_t ep, int &dead,
-                                             uint32_t spin, float4 (&hv)[NB])
+__device__ __forceinline__ void k1b_gather_h(const uint64_t *lh, int H, int HU, int u, int b0, int B, uint32_t ep,
+                                             int &dead, uint32_t spin, float (*xn)[K1_MAXH])
 {
     uint64_t r[NB][4];
     const int uc = min(u, HU - 1);
 #pragma unroll
     for (int b = 0; b < NB; b++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) r[b][i] = xch_load(lh + (size_t)b * H + (size_t)i * HU + uc);
+        for (int i = 0; i < 4; i++) r[b][i] = xch_load(lh + (size_t)(b0 + b) * H + (size_t)i * HU + uc);
     unsigned it = 0;
     for (;;) {
         unsigned miss = 0;
@@ -1779,7 +1779,7 @@ __device__ __forceinline__ void k1b_gather_h(const uint64_t *lh, int H, int HU, 
         for (int b = 0; b < NB; b++)
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                miss |= b < B && u < HU && (uint32_t)(r[b][i] >> 32) != ep ? 1u << (4 * b + i) : 0u;
+                miss |= b0 + b < B && u < HU && (uint32_t)(r[b][i] >> 32) != ep ? 1u << (4 * b + i) : 0u;
         if (!miss || dead) break;
         if (++it > spin) {
             dead = 1;
@@ -1790,12 +1790,16 @@ __device__ __forceinline__ void k1b_gather_h(const uint64_t *lh, int H, int HU, 
         for (int b = 0; b < NB; b++)
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                if ((miss >> (4 * b + i)) & 1u) r[b][i] = xch_load(lh + (size_t)b * H + (size_t)i * HU + uc);
+                if ((miss >> (4 * b + i)) & 1u) r[b][i] = xch_load(lh + (size_t)(b0 + b) * H + (size_t)i * HU + uc);
     }
+    if (u < HU) {
 #pragma unroll
-    for (int b = 0; b < NB; b++)
-        hv[b] = make_float4(__builtin_bit_cast(float, (uint32_t)r[b][0]), __builtin_bit_cast(float, (uint32_t)r[b][1]),
-                            __builtin_bit_cast(float, (uint32_t)r[b][2]), __builtin_bit_cast(float, (uint32_t)r[b][3]));
+        for (int b = 0; b < NB; b++)
+            if (b0 + b < B)
+                ((float4 *)xn[b0 + b])[u] =
+                    make_float4(__builtin_bit_cast(float, (uint32_t)r[b][0]), __builtin_bit_cast(float, (uint32_t)r[b][1]),
+                                __builtin_bit_cast(float, (uint32_t)r[b][2]), __builtin_bit_cast(float, (uint32_t)r[b][3]));
+    }
 }
 
 template <int NB>
@@ -1816,6 +1820,7 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
     __shared__ float4 rrow_s[8][64];                          /* router row gw */
     __shared__ float4 gin_s[8][64];                           /* shared-gate vector */
     __shared__ QChunk2 shc_s[2][64];                          /* this workgroup's shared gate/up pairs */
+    __shared__ QChunk sdc_s[2][64];                           /* its shared down rows (H <= 2048: 2 tasks) */
     __shared__ int s_dead, s_err;
 
     constexpr int I = 512, nbi = 2, SP = 2, RGP = I / K1_GW;
@@ -1840,6 +1845,13 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
     const int ndt = (RD + rpw - 1) / rpw;
     const bool rrow = gw < E && !A.logits_in;
     const int n = A.nlayers;
+#ifdef ROASTER_PHASE_TS
+    unsigned long long tsv[2][16] = {};
+    int tsl = 0;
+#define K1_TS(i) asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(tsv[tsl][i]) : : "memory")
+#else
+#define K1_TS(i) ((void)0)
+#endif
     if (tid == 0) {
         s_dead = 0;
         s_err = 0;
@@ -1858,6 +1870,10 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
         const uint32_t ep = A.epoch + (uint32_t)li;
         const bool last = li + 1 == n;
         const DecLayer L = k1_layer(Ls, li);
+#ifdef ROASTER_PHASE_TS
+        tsl = li + 1 == n ? 1 : 0;
+#endif
+        K1_TS(0);
         const float *nwg = A.do_norm && A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * H : NULL;
 
         /* ---- 1. this layer's own weights first (they do not depend on h),
@@ -1878,13 +1894,17 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
         if (sdt >= 0) sdc = q_load_t(1, L.sdown, (size_t)min(gw * RO + sdt * rpw + rw_, H - 1), nbi, lr >> 3, lr & 7);
         const int u = tid;
         const float4 nwv = nwg ? ((const float4 *)nwg)[min(u, HU - 1)] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-        float4 hv[NB];
+        /* h, raw, into xn (unit order) */
         if (li == 0) {
-#pragma unroll
-            for (int b = 0; b < NB; b++) hv[b] = ((const float4 *)A.h)[(size_t)min(b, B - 1) * HU + min(u, HU - 1)];
+            if (u < HU)
+                for (int b = 0; b < B; b++) ((float4 *)xn[b])[u] = ((const float4 *)A.h)[(size_t)b * HU + u];
         } else {
-            k1b_gather_h<NB>(lh, H, HU, u, B, ep - 1, dead, A.spin, hv);
+            constexpr int NG = NB < 4 ? NB : 4;           /* tokens per polling round (registers) */
+#pragma unroll
+            for (int b0 = 0; b0 < NB; b0 += NG)
+                if (b0 < B) k1b_gather_h<NG>(lh, H, HU, u, b0, B, ep - 1, dead, A.spin, xn);
         }
+        K1_TS(1);
         /* parked for the per-token dots of phase 2 (their loads were issued
          * before the gather's and have completed with it) */
         if ((wv == K1_WR && rrow) || wv == K1_WGI) {
@@ -1893,27 +1913,17 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
             for (int m = 0; m < 8; m++) dst[m][lane] = rw[m];
         }
         if (wv >= K1_W - SP) shc_s[wv - (K1_W - SP)][lane] = shc;
-        /* the raw h (read back for the sums of squares) and the owned rows'
-         * residual: units gi RD / 4 .. + RD / 4 */
-        if (u < HU) {
-#pragma unroll
-            for (int b = 0; b < NB; b++)
-                if (b < B) ((float4 *)xn[b])[u] = hv[b];
-        }
-        {
-            const int o = u - gi * (RD / 4);
-            if (o >= 0 && o < RD / 4) {
-#pragma unroll
-                for (int b = 0; b < NB; b++) {
-                    hown[b][4 * o] = hv[b].x;
-                    hown[b][4 * o + 1] = hv[b].y;
-                    hown[b][4 * o + 2] = hv[b].z;
-                    hown[b][4 * o + 3] = hv[b].w;
-                }
-            }
-        }
+        if (sdt >= 0) sdc_s[sdt][lane] = sdc;
         K1_SYNC_DEAD();
         if (dead) break;                                  /* workgroup-uniform */
+        /* the owned rows' residual (rows gi RD .. + RD), each unit's own h */
+        if (tid < RD) {
+            for (int b = 0; b < B; b++) hown[b][tid] = xn[b][gi * RD + tid];
+        }
+        float4 hv[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+            hv[b] = b < B ? ((const float4 *)xn[b])[min(u, HU - 1)] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         /* sums of squares in the one-token order: lane t adds units t and
          * t + 256, waves 0..3, the four wave sums in wave order */
         if (A.do_norm && tid < 256) {
@@ -1935,15 +1945,20 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
             }
         }
         __syncthreads();
+        /* 1 / rms of token b in lane b of every wave, then broadcast */
+        float inv_l = 1.0f;
+        if (A.do_norm && lane < B) {
+            float s2 = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) s2 += red_s[w][lane];
+            inv_l = 1.0f / sqrtf(s2 / (float)H + A.eps);
+        }
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             if (b >= B) break;
             float4 v = hv[b];
             if (A.do_norm) {
-                float s2 = 0.0f;
-#pragma unroll
-                for (int w = 0; w < 4; w++) s2 += red_s[w][b];
-                const float inv = 1.0f / sqrtf(s2 / (float)H + A.eps);
+                const float inv = lane_f(inv_l, b);
                 v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
                 if (nwg) { v.x *= nwv.x; v.y *= nwv.y; v.z *= nwv.z; v.w *= nwv.w; }
             }
@@ -1957,6 +1972,7 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
         }
         __syncthreads();
 
+        K1_TS(2);
         /* ---- 2. per token b, on wave b: router logit gw, then the shared-gate
          * logit; the 2 B shared SiLU*up values (pair t & 1 of token t >> 1)
          * dealt to the waves in turn ------------------------------------------ */
@@ -1985,6 +2001,7 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
             if (lane == 0) w_s[b][RTOPK] = 1.0f / (1.0f + expf(-s));
         }
 
+        K1_TS(3);
         /* ---- 3. relays into the XCD's region; token b's top 8 (wave b) and its
          * shared SiLU*up values -------------------------------------------------- */
         if (wv == 0 && !A.logits_in && lane < B * LPW) {
@@ -2020,7 +2037,9 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
             topk8_fast(v4, E, ids_s[b], w_s[b], &s_err, &tks[b]);
             if (lane < I / 16) ehshs[b][lane] = k1_gather_run(lehs + (size_t)b * I, I, lane, ep, dead, A.spin, ehsh[b] + 16 * lane);
         }
+        K1_TS(13);
         K1_SYNC_DEAD();
+        K1_TS(4);
         if (gw == 0) {
             if (tid < B * RTOPK) {
                 const size_t o = ((size_t)li * B + (tid >> 3)) * RTOPK + (tid & 7);
@@ -2032,9 +2051,10 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
 
         /* ---- 4. the slot experts of the B tokens -------------------------- */
         {
-            QChunk2 cur[2], nxt[2];
+            constexpr int DG = 2;                            /* tokens' gate/up rows in flight */
+            QChunk2 st[DG][2];
             auto gu_load = [&](int b, QChunk2 (&ch)[2]) {
-                const int e = ids_s[min(b, B - 1)][grp];
+                const int e = __builtin_amdgcn_readfirstlane(ids_s[min(b, B - 1)][grp]);   /* wave-uniform */
                 const size_t ee = e >= 0 ? (size_t)e : 0;
                 const uint8_t *ge = L.gate + ee * L.eb[0], *ue = L.up + ee * L.eb[1];
 #pragma unroll
@@ -2042,37 +2062,58 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
 #pragma unroll
                 for (int f = 0; f < 2; f++) ch[f].u = q_load_t(0, ue, (size_t)gi * RGP + wv + f * K1_W, nbh, lb, c);
             };
-            gu_load(0, cur);
-            for (int b = 0; b < B; b++) {
+#pragma unroll
+            for (int b = 0; b < DG - 1; b++) gu_load(b, st[b]);
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                if (b >= B) break;
                 const bool live_slot = ids_s[b][grp] >= 0;
-                gu_load(b + 1, nxt);                 /* the next token's rows in flight (past the last: unused) */
+                if (b + DG - 1 < NB) gu_load(b + DG - 1, st[(b + DG - 1) % DG]);   /* past the last token: unused */
+                QChunk2 (&cur)[2] = st[b % DG];
+                /* the wave's four rows share one read of the token's x
+                 * (k1_q_row's arithmetic per row) */
+                float pg[2] = {0.0f, 0.0f}, pu[2] = {0.0f, 0.0f};
+                if (lb < nbh) {
+                    const int xa = lb * RQK + q_run_a_t(0, c), xb = xa + 32;
+                    float4 x0[4], x1[4];
+                    load_x16(xn[b], xa, x0, swz);
+                    load_x16(xn[b], xb, x1, swz);
+                    const float sa = xsum[b][xa >> 4], sb = xsum[b][xb >> 4];
+#pragma unroll
+                    for (int f = 0; f < 2; f++) {
+                        pg[f] = q_chunk_dot_r<false>(cur[f].g, c, x0, x1, sa, sb);
+                        pu[f] = q_chunk_dot_r<false>(cur[f].u, c, x0, x1, sa, sb);
+                    }
+                }
 #pragma unroll
                 for (int f = 0; f < 2; f++) {
                     const int pj = wv + f * K1_W;
-                    const float pg = k1_q_row(0, cur[f].g, xn[b], xsum[b], swz, nbh, lane);
-                    const float eh = silu_mul(pg, k1_q_row(0, cur[f].u, xn[b], xsum[b], swz, nbh, lane));
+                    const float eh = silu_mul(group_sum<64>(pg[f]), group_sum<64>(pu[f]));
                     if (lane == 0) xch_put_xcd(lehx + (size_t)b * I + k1_run_slot(gi * RGP + pj, I), live_slot ? eh : 0.0f, ep, l2);
                 }
-#pragma unroll
-                for (int f = 0; f < 2; f++) cur[f] = nxt[f];
             }
         }
-        /* the shared expert's down rows [gw RO, (gw + 1) RO) for every token */
-        if (sdt >= 0) {
-            const int rl = sdt * rpw + rw_;
+        K1_TS(5);
+        /* the shared expert's down rows [gw RO, (gw + 1) RO) for every token:
+         * task t (rows of chunk t % nsd, token t / nsd) on wave t % 8 */
+        for (int t = wv; t < nsd * B; t += K1_W) {
+            const int k = t % nsd, b = t / nsd;
+            const int rl = k * rpw + rw_;
             const bool live = rl < RO && lbd < nbi;
-            for (int b = 0; b < B; b++) {
-                const float part = k1_down_row(1, sdc, ehsh[b], ehshs[b], live, lpr, lane);
-                if (live && lr == 0) xch_put(xdsh + ((size_t)b * 256 + gw) * XCH_LN + rl, part, ep);
-            }
+            const float part = k1_down_row(1, sdc_s[k][lane], ehsh[b], ehshs[b], live, lpr, lane);
+            if (live && lr == 0) xch_put(xdsh + ((size_t)b * 256 + gw) * XCH_LN + rl, part, ep);
         }
+        K1_TS(6);
         if (wv < B && lane < I / 16)
             ehks[wv][lane] = k1_gather_run(lehx + (size_t)wv * I, I, lane, ep, dead, A.spin, ehk[wv] + 16 * lane);
+        K1_TS(10);
         K1_SYNC_DEAD();
+        K1_TS(7);
         {
-            QChunk cur[2], nxt[2];
+            constexpr int DD = 2;                            /* tokens' down rows in flight */
+            QChunk st[DD][2];
             auto dn_load = [&](int b, QChunk (&ch)[2]) {
-                const int e = ids_s[min(b, B - 1)][grp];
+                const int e = __builtin_amdgcn_readfirstlane(ids_s[min(b, B - 1)][grp]);   /* wave-uniform */
                 const size_t ee = e >= 0 ? (size_t)e : 0;
                 const uint8_t *de = L.down + ee * L.eb[2];
 #pragma unroll
@@ -2081,10 +2122,14 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
                     ch[f] = q_load_t(1, de, (size_t)min(gi * RD + task * rpw + rw_, H - 1), nbi, lbd, lr & 7);
                 }
             };
-            dn_load(0, cur);
-            for (int b = 0; b < B; b++) {
+#pragma unroll
+            for (int b = 0; b < DD - 1; b++) dn_load(b, st[b]);
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                if (b >= B) break;
                 const bool live_slot = ids_s[b][grp] >= 0;
-                dn_load(b + 1, nxt);
+                if (b + DD - 1 < NB) dn_load(b + DD - 1, st[(b + DD - 1) % DD]);
+                QChunk (&cur)[2] = st[b % DD];
 #pragma unroll
                 for (int f = 0; f < 2; f++) {
                     const int task = wv + f * K1_W;
@@ -2095,11 +2140,10 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
                         if (live && lr == 0) xch_put(xdx + ((size_t)b * 8 + grp) * H + row, live_slot ? part : 0.0f, ep);
                     }
                 }
-#pragma unroll
-                for (int f = 0; f < 2; f++) cur[f] = nxt[f];
             }
         }
 
+        K1_TS(8);
         /* ---- 5. wave b: token b's owned rows combined (model.c:1139-1144) --- */
         if (wv < B) {
             const int b = wv;
@@ -2123,8 +2167,15 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
                 }
             }
         }
+        K1_TS(9);
     }
     if (tid == 0 && (dead || s_dead)) atomicOr(A.err, 2);
+#ifdef ROASTER_PHASE_TS
+    if (threadIdx.x == 0 || threadIdx.x == 64 || threadIdx.x == 448)
+        for (int k = 0; k < 2; k++)
+            for (int i = 0; i < 16; i++) g_k1_ts[k][blockIdx.x][min((int)threadIdx.x >> 6, 2)][i] = tsv[k][i];
+#endif
+#undef K1_TS
 }
 
 extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stackB2_kernel(DecArgs A) { stackB_body<2>(A); }
