@@ -1973,9 +1973,10 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
         __syncthreads();
 
         K1_TS(2);
-        /* ---- 2. per token b, on wave b: router logit gw, then the shared-gate
-         * logit; the 2 B shared SiLU*up values (pair t & 1 of token t >> 1)
-         * dealt to the waves in turn ------------------------------------------ */
+        /* ---- 2. per token b, on wave b: router logit gw; the 2 B shared
+         * SiLU*up values (pair t % SP of token t / SP), then the B shared-gate
+         * logits, dealt to waves 1..7 in turn (wave 0 goes on to relay the
+         * logits) ------------------------------------------------------------- */
         for (int b = wv; b < B; b += K1_W) {
             float4 r4[8];
             if (rrow) {
@@ -1988,12 +1989,12 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
                 }
             }
         }
-        for (int t = wv; t < SP * B; t += K1_W) {
+        for (int t = wv - 1; wv > 0 && t < SP * B; t += K1_W - 1) {
             const int pr = t % SP, b = t / SP;
             const float eh = k1_gu_pair(0, 0, shc_s[pr][lane], xn[b], xsum[b], swz, nbh, lane);
             if (lane == 0) xch_put(xehs + ((size_t)b * 256 + gw) * XCH_LN + pr, eh, ep);
         }
-        for (int b = wv; b < B; b += K1_W) {
+        for (int b = wv - 1; wv > 0 && b < B; b += K1_W - 1) {
             float4 r4[8];
 #pragma unroll
             for (int m = 0; m < 8; m++) r4[m] = gin_s[m][lane];
@@ -2035,7 +2036,6 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
             for (int i = 0; i < 4; i++)
                 if (lane + 64 * i >= E) v4[i] = -INFINITY;
             topk8_fast(v4, E, ids_s[b], w_s[b], &s_err, &tks[b]);
-            if (lane < I / 16) ehshs[b][lane] = k1_gather_run(lehs + (size_t)b * I, I, lane, ep, dead, A.spin, ehsh[b] + 16 * lane);
         }
         K1_TS(13);
         K1_SYNC_DEAD();
@@ -2094,18 +2094,13 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
             }
         }
         K1_TS(5);
-        /* the shared expert's down rows [gw RO, (gw + 1) RO) for every token:
-         * task t (rows of chunk t % nsd, token t / nsd) on wave t % 8 */
-        for (int t = wv; t < nsd * B; t += K1_W) {
-            const int k = t % nsd, b = t / nsd;
-            const int rl = k * rpw + rw_;
-            const bool live = rl < RO && lbd < nbi;
-            const float part = k1_down_row(1, sdc_s[k][lane], ehsh[b], ehshs[b], live, lpr, lane);
-            if (live && lr == 0) xch_put(xdsh + ((size_t)b * 256 + gw) * XCH_LN + rl, part, ep);
-        }
         K1_TS(6);
-        if (wv < B && lane < I / 16)
+        /* wave b: token b's shared SiLU*up values (relayed during the top 8)
+         * and its slot expert's */
+        if (wv < B && lane < I / 16) {
+            ehshs[wv][lane] = k1_gather_run(lehs + (size_t)wv * I, I, lane, ep, dead, A.spin, ehsh[wv] + 16 * lane);
             ehks[wv][lane] = k1_gather_run(lehx + (size_t)wv * I, I, lane, ep, dead, A.spin, ehk[wv] + 16 * lane);
+        }
         K1_TS(10);
         K1_SYNC_DEAD();
         K1_TS(7);
@@ -2124,6 +2119,16 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
             };
 #pragma unroll
             for (int b = 0; b < DD - 1; b++) dn_load(b, st[b]);
+            /* the shared expert's down rows [gw RO, (gw + 1) RO) for every
+             * token while the first routed rows arrive: task t (rows of chunk
+             * t % nsd, token t / nsd) on wave t % 8 */
+            for (int t = wv; t < nsd * B; t += K1_W) {
+                const int k = t % nsd, b = t / nsd;
+                const int rl = k * rpw + rw_;
+                const bool live = rl < RO && lbd < nbi;
+                const float part = k1_down_row(1, sdc_s[k][lane], ehsh[b], ehshs[b], live, lpr, lane);
+                if (live && lr == 0) xch_put(xdsh + ((size_t)b * 256 + gw) * XCH_LN + rl, part, ep);
+            }
 #pragma unroll
             for (int b = 0; b < NB; b++) {
                 if (b >= B) break;
