@@ -1745,23 +1745,26 @@ extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stack1_2x2_kernel(DecA
  * carried one, and the expert rows of the B tokens are streamed back to back.
  * Per layer:
  *   1. every thread u < H/4: unit u of each token's h (this XCD's copy, or the
- *      caller's h in the first layer), RMSNorm per token (the sums of squares
- *      as lane partials, wave sums in wave order), the normalised inputs and
- *      their run sums in LDS, and the owned rows' residuals;
- *   2. router row gw (wave K1_WR), the shared-gate logits (K1_WGI) and this
- *      workgroup's shared SiLU*up pairs (the last SP waves) for every token;
+ *      caller's h in the first layer) into LDS; the sums of squares in the
+ *      one-token order (lane t: units t and t + 256, waves 0..3, the wave sums
+ *      in wave order), 1/rms per token, the normalised inputs and their run
+ *      sums, the owned rows' residuals;
+ *   2. router row gw for token b on wave b; the shared expert's SiLU*up pairs
+ *      of this workgroup and the shared-gate logits on waves 1..7;
  *   3. wave 0 relays the logits, wave K1_WN the shared values, into the XCD's
- *      region; wave b ranks token b's top 8 and gathers its shared SiLU*up;
+ *      region; wave b ranks token b's top 8;
  *   4. the slot experts' gate/up rows token after token (the next token's rows
- *      in flight while the current one's are dotted), SiLU*up within the XCD,
- *      wave b gathers token b's; the down rows likewise; the shared expert's
- *      down rows;
+ *      in flight while the current one's are dotted; a wave's four rows share
+ *      one read of the token's activations), SiLU*up within the XCD; wave b
+ *      gathers token b's shared and slot SiLU*up values; the shared expert's
+ *      down rows, then the slot experts' down rows token after token;
  *   5. wave b combines token b's owned rows (model.c:1139-1144 order) and
  *      publishes them within the XCD.
- * Shapes: inter 512, hidden 1280..2048; gate/up Q4_K and down Q6_K, routed
- * and shared (dec_layerB_ok and the launch check the rest).  Results agree
- * with the three-kernel path within float rounding (the sums of squares are
- * added in a different order). */
+ * Every dot, sum, softmax and combine is the one-token kernel's, in its order,
+ * so each token's results equal its one-token results bit for bit.  Shapes:
+ * inter 512, hidden 512..2048 in whole 256-row blocks, at most 256 experts;
+ * gate/up Q4_K and down Q6_K, routed and shared (dec_layerB_ok and the launch
+ * check the rest). */
 template <int NB>
 __device__ __forceinline__ void k1b_gather_h(const uint64_t *lh, int H, int HU, int u, int b0, int B, uint32_t ep,
                                              int &dead, uint32_t spin, float (*xn)[K1_MAXH])
