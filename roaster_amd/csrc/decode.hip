@@ -2097,16 +2097,6 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
             }
         }
         K1_TS(5);
-        K1_TS(6);
-        /* wave b: token b's shared SiLU*up values (relayed during the top 8)
-         * and its slot expert's */
-        if (wv < B && lane < I / 16) {
-            ehshs[wv][lane] = k1_gather_run(lehs + (size_t)wv * I, I, lane, ep, dead, A.spin, ehsh[wv] + 16 * lane);
-            ehks[wv][lane] = k1_gather_run(lehx + (size_t)wv * I, I, lane, ep, dead, A.spin, ehk[wv] + 16 * lane);
-        }
-        K1_TS(10);
-        K1_SYNC_DEAD();
-        K1_TS(7);
         {
             constexpr int DD = 2;                            /* tokens' down rows in flight */
             QChunk st[DD][2];
@@ -2120,8 +2110,27 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
                     ch[f] = q_load_t(1, de, (size_t)min(gi * RD + task * rpw + rw_, H - 1), nbi, lbd, lr & 7);
                 }
             };
+            /* 2 slots: the first token's down rows in flight through the
+             * gathers and the barrier (with more tokens the gathers' polls,
+             * queued behind them, measured slower) */
+            if constexpr (NB == 2) {
 #pragma unroll
-            for (int b = 0; b < DD - 1; b++) dn_load(b, st[b]);
+                for (int b = 0; b < DD - 1; b++) dn_load(b, st[b]);
+            }
+            K1_TS(6);
+            /* wave b: token b's shared SiLU*up values (relayed during the top
+             * 8) and its slot expert's */
+            if (wv < B && lane < I / 16) {
+                ehshs[wv][lane] = k1_gather_run(lehs + (size_t)wv * I, I, lane, ep, dead, A.spin, ehsh[wv] + 16 * lane);
+                ehks[wv][lane] = k1_gather_run(lehx + (size_t)wv * I, I, lane, ep, dead, A.spin, ehk[wv] + 16 * lane);
+            }
+            K1_TS(10);
+            K1_SYNC_DEAD();
+            K1_TS(7);
+            if constexpr (NB != 2) {
+#pragma unroll
+                for (int b = 0; b < DD - 1; b++) dn_load(b, st[b]);
+            }
             /* the shared expert's down rows [gw RO, (gw + 1) RO) for every
              * token while the first routed rows arrive: task t (rows of chunk
              * t % nsd, token t / nsd) on wave t % 8 */
