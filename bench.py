@@ -6,11 +6,12 @@ Headline (value): batch-1 decode through the 40-layer MoE-FFN stack -- hidden
 between layers -- with every expert resident in HBM (21.05 GB in the GGML layout
 the decode kernels read, plus the 22.9 GB MFMA tile-layout copy the prefill
 GEMMs read).  A step is one token through all 40 layers (one library call: one
-launch for the whole stack at batch 1, three kernels per layer at batch 8).  Inputs
+launch for the whole stack, at batch 1 and at batches 2-8).  Inputs
 and weights are synthetic (seeded) and already in HBM when timing starts.
 
 Also reported in the same JSON line:
-  batch8   -- 8 slots, one token each, through the same stack;
+  batch2, batch4, batch8 -- 2, 4, 8 slots, one token each, through the same
+              stack (the batched one-launch kernels);
   prefill  -- the MoE block over T tokens: 2048 tokens through 4 all-Q6_K
               layers with N(0,1) logits given (its value, MFMA roofline and CPU
               baseline), and 512 tokens through one Q4_K/Q6_K layer with the
@@ -604,7 +605,7 @@ def dense_leg(torch, L, R, dev, stream):
 
 def decode_legs(args, torch, L, R, dev, stream):
     """The headline: batch-`args.batch` decode through the 40-layer stack (host
-    wall clock over --steps steps, device time from HIP events), batch 8 and
+    wall clock over --steps steps, device time from HIP events), batches 2, 4, 8 and
     the reference CPU decode beside it."""
     seed = 3
     desc = R.table_desc(N_LAYERS)
@@ -662,20 +663,24 @@ def decode_legs(args, torch, L, R, dev, stream):
                    "gate_up": "Q4_K", "down": "Q6_K", "resident_table_bytes": int(L.roaster_table_bytes(t))},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("decode_b%d_step" % B),
-                     "kernel": "decode stack: %s" % ("dec_stack1_kernel, one launch for all 40 layers"
-                                                     if B == 1 and L.roaster_decode_fused_layer(-1)
+                     "kernel": "decode stack: %s" % (("dec_stack1_kernel, one launch for all 40 layers" if B == 1 else
+                                                      "dec_stackB%d_kernel, one launch for all 40 layers"
+                                                      % (2 if B <= 2 else 4 if B <= 4 else 8))
+                                                     if L.roaster_decode_fused_layer(-1)
                                                      else "router, gate/up and down kernels per layer"),
                      "kernel_ms": round(kern_ms, 5), "algorithmic_bytes_per_launch": int(nbytes)},
     }
     if B == 1:
-        h8_0, h8, ids8 = stack_setup(8)
-        warm(L, R, lambda: stack_step(8, h8_0, h8, ids8), 10, "batch8 warmup")
-        ms8 = event_ms(torch, stream, lambda: stack_step(8, h8_0, h8, ids8), 20)
-        R.check(L.roaster_sync(), "batch8")
-        b8 = decode_bytes(ids8.cpu().numpy())
-        line["batch8"] = {"tokens_per_s": round(8 / (ms8 * 1e-3), 1), "ms_per_step": round(ms8, 4),
-                          "hbm_GBps": round(b8 / (ms8 * 1e-3) / 1e9, 1),
-                          "frac_hbm_peak": round(b8 / (ms8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        for nb in (2, 4, 8):              # the batched one-launch stack (dec_stackB<nb>_kernel)
+            hb_0, hb, idsb = stack_setup(nb)
+            warm(L, R, lambda: stack_step(nb, hb_0, hb, idsb), 10, "batch%d warmup" % nb)
+            msb = event_ms(torch, stream, lambda: stack_step(nb, hb_0, hb, idsb), 20)
+            R.check(L.roaster_sync(), "batch%d" % nb)
+            bb = decode_bytes(idsb.cpu().numpy())
+            line["batch%d" % nb] = {"tokens_per_s": round(nb / (msb * 1e-3), 1), "ms_per_step": round(msb, 4),
+                                    "hbm_GBps": round(bb / (msb * 1e-3) / 1e9, 1),
+                                    "frac_hbm_peak": round(bb / (msb * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                    "kernel": "dec_stackB%d_kernel" % nb}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(seed, args.cpu_tokens, t)
     L.roaster_table_destroy(t)
