@@ -8,10 +8,12 @@ ids and routing weights must equal, bit for bit, both the three-kernel path's
 for the whole batch and the one-token launch's for that token alone; the
 oracle bars of the decode tests (ids exact, max|d|/max|ffn| <= 2e-3 and the
 1e-4 regression bound) are held as well.  Cases: 8 tokens (8 token slots), 3
-and 5 tokens (4 and 8 slots, some unused), 2 tokens; the 256-expert shape
-with norm weights and hidden 768 / 64 experts (activations stored plainly in
-LDS) and hidden 1280 / 128 experts; one layer through roaster_moe_decode with
-the router and with given logits holding ties and NaN; fewer than 8 routable
+and 5 tokens (4 and 8 slots, some unused), 2, 4 and 6 tokens; the 256-expert
+shape with norm weights, hidden 768 / 64 experts (activations stored plainly
+in LDS), hidden 1280 / 128 experts, hidden 512 / 32 experts (the smallest
+shape taken: one logit per workgroup of a group) and hidden 1024; one layer
+through roaster_moe_decode with the router and with given logits holding
+ties and NaN; fewer than 8 routable
 experts for one token of four; per-layer matrix types the launch does not
 take (the three-kernel path runs); a wait that gives up (spin limit forced to
 1 poll from the host, so every kernel still ends)."""
@@ -28,7 +30,8 @@ from test_gpu_decode_layer1 import _stack, _both, _same
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("shape", [(256, 2048, 8, 4), (256, 2048, 3, 3), (64, 768, 2, 2), (128, 1280, 5, 2)])
+@pytest.mark.parametrize("shape", [(256, 2048, 8, 4), (256, 2048, 3, 3), (64, 768, 2, 2), (128, 1280, 5, 2),
+                                   (32, 512, 4, 2), (256, 1024, 6, 2)])
 def test_stackB_matches_three_kernels_one_token_and_oracle(shape):
     E, H, B, NL = shape
     log(f"batched one-launch stack: E={E} H={H} B={B}, {NL} layers")
