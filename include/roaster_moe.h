@@ -160,11 +160,14 @@ int roaster_moe_decode(RoasterTable *t, int layer, const float *x, int B, float 
 int roaster_moe_decode_stack(RoasterTable *t, float *h, int B, int layer0, int n_layers,
                              const float *norm_w, float eps, int *ids_out, float *w_out);
 
-/* Decode of one token (B = 1) runs each layer as one launch (router, top-8,
- * experts and combine in 256 workgroups that exchange values through memory)
- * wherever the shapes allow it (experts a multiple of 32 up to 256, hidden up
- * to 2048, inter up to 1024, a device with at least 256 CUs); otherwise, and
- * for B > 1, as three launches.  Both give bit-identical results.
+/* Decode runs a call's layers as one launch (router, top-8, experts and
+ * combine in 256 workgroups that exchange values through memory) wherever the
+ * shapes allow it: a device with at least 256 CUs and experts a multiple of 32
+ * up to 256; for one token hidden up to 2048 and inter up to 1024; for 2..8
+ * tokens inter 512, hidden 512..2048 in multiples of 256, and gate/up Q4_K and
+ * down Q6_K in every layer of the call.  Otherwise each layer runs as three
+ * launches.  All give bit-identical results, each token's equal to its
+ * one-token result.
  * roaster_decode_fused_layer: 1 = one launch where possible (default), 0 =
  * always three, -1 = query; returns the mode in force. */
 int roaster_decode_fused_layer(int enable);
@@ -176,8 +179,9 @@ unsigned roaster_decode_spin_limit(unsigned polls);
 
 /* No counterpart in the reference: roaster_moe_decode_stack for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
- * loops, harnesses that forbid hipMalloc).  Same arguments, kernels and
- * results; every intermediate lives in a fixed 512 KiB device array that the
+ * loops, harnesses that forbid hipMalloc).  Same arguments and results (one
+ * token: the same one-launch kernel; 2..8 tokens: three launches per layer);
+ * every intermediate lives in a fixed 512 KiB device array that the
  * library sets up in roaster_init (call it first) and keeps until the process
  * ends, so the call itself makes no allocation.  Calls whose intermediates
  * exceed it -- about 8 tokens x hidden 2048 x inter 1024 or more -- return
