@@ -1864,6 +1864,16 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
     if (tid < n * DQ) ((uint4 *)Ls)[tid] = ((const uint4 *)(A.layers + A.layer0))[tid];
     __syncthreads();
 
+    /* each layer's router row, shared-gate vector and shared expert rows:
+     * with 2 token slots waves 4..7 combine nothing and load the next layer's
+     * at the end of a layer (so no wave's h gather queues behind them); with
+     * 4 or 8 (measured slower that way: registers), the waves K1_WR, K1_WGI
+     * and the last ones load them at the start of the layer */
+    float4 rw[8];
+    QChunk2 shc;
+    QChunk sdc;
+    constexpr bool EARLY = NB == 2;
+    const int wR = EARLY ? 4 : K1_WR, wG = EARLY ? 5 : K1_WGI;
     for (int li = 0; li < n; li++) {
         int tid_v = (int)threadIdx.x;
         asm volatile("" : "+v"(tid_v));
@@ -1881,20 +1891,20 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
 
         /* ---- 1. this layer's own weights first (they do not depend on h),
          * then h, normalised per token ---------------------------------------- */
-        float4 rw[8];
-        QChunk2 shc;
-        QChunk sdc;
-        if ((wv == K1_WR && rrow) || wv == K1_WGI) {
-            const float *row = wv == K1_WR ? L.router + (size_t)gw * H : L.gate_inp;
+        auto wload = [&](const DecLayer &Lx) {
+            if ((wv == wR && rrow) || wv == wG) {
+                const float *row = wv == wR ? Lx.router + (size_t)gw * H : Lx.gate_inp;
 #pragma unroll
-            for (int m = 0; m < 8; m++) rw[m] = gld_f4(row + min(4 * lane + 256 * m, H - 4));
-        }
-        if (wv >= K1_W - SP) {
-            const size_t j = (size_t)gw * SP + (wv - (K1_W - SP));
-            shc.g = q_load_t(0, L.sgate, j, nbh, lb, c);
-            shc.u = q_load_t(0, L.sup, j, nbh, lb, c);
-        }
-        if (sdt >= 0) sdc = q_load_t(1, L.sdown, (size_t)min(gw * RO + sdt * rpw + rw_, H - 1), nbi, lr >> 3, lr & 7);
+                for (int m = 0; m < 8; m++) rw[m] = gld_f4(row + min(4 * lane + 256 * m, H - 4));
+            }
+            if (wv >= K1_W - SP) {
+                const size_t j = (size_t)gw * SP + (wv - (K1_W - SP));
+                shc.g = q_load_t(0, Lx.sgate, j, nbh, lb, c);
+                shc.u = q_load_t(0, Lx.sup, j, nbh, lb, c);
+            }
+            if (sdt >= 0) sdc = q_load_t(1, Lx.sdown, (size_t)min(gw * RO + sdt * rpw + rw_, H - 1), nbi, lr >> 3, lr & 7);
+        };
+        if (!EARLY || li == 0) wload(L);
         const int u = tid;
         const float4 nwv = nwg ? ((const float4 *)nwg)[min(u, HU - 1)] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
         /* h, raw, into xn (unit order) */
@@ -1910,8 +1920,8 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
         K1_TS(1);
         /* parked for the per-token dots of phase 2 (their loads were issued
          * before the gather's and have completed with it) */
-        if ((wv == K1_WR && rrow) || wv == K1_WGI) {
-            float4 (*dst)[64] = wv == K1_WR ? rrow_s : gin_s;
+        if ((wv == wR && rrow) || wv == wG) {
+            float4 (*dst)[64] = wv == wR ? rrow_s : gin_s;
 #pragma unroll
             for (int m = 0; m < 8; m++) dst[m][lane] = rw[m];
         }
@@ -2160,6 +2170,9 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
             }
         }
 
+        if constexpr (EARLY) {
+            if (!last) wload(k1_layer(Ls, li + 1));
+        }
         K1_TS(8);
         /* ---- 5. wave b: token b's owned rows combined (model.c:1139-1144) --- */
         if (wv < B) {
