@@ -1825,6 +1825,7 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
     __shared__ QChunk2 shc_s[2][64];                          /* this workgroup's shared gate/up pairs */
     __shared__ QChunk sdc_s[2][64];                           /* its shared down rows (H <= 2048: 2 tasks) */
     __shared__ int s_dead, s_err;
+    __shared__ int s_ids_rdy[NB];                             /* layer index + 1 once token b's ids are in */
 
     constexpr int I = 512, nbi = 2, SP = 2, RGP = I / K1_GW;
     const int H = A.H, E = A.E, B = A.B, HU = H / 4, nbh = H / RQK;
@@ -1859,6 +1860,7 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
         s_dead = 0;
         s_err = 0;
     }
+    if (tid < NB) s_ids_rdy[tid] = 0;
     int dead = (gld_u32(A.err) & 2u) != 0;
     constexpr int DQ = (int)(sizeof(DecLayer) / 16);
     if (tid < n * DQ) ((uint4 *)Ls)[tid] = ((const uint4 *)(A.layers + A.layer0))[tid];
@@ -2048,25 +2050,27 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
 #pragma unroll
             for (int i = 0; i < 4; i++)
                 if (lane + 64 * i >= E) v4[i] = -INFINITY;
-            topk8_fast(v4, E, ids_s[b], w_s[b], &s_err, &tks[b]);
+            topk8_fast(v4, E, ids_s[b], w_s[b], &s_err, &tks[b], &s_ids_rdy[b], li + 1);
+            if (gw == 0) {
+                if (lane < RTOPK) {
+                    const size_t o = ((size_t)li * B + b) * RTOPK + lane;
+                    if (A.ids_out) A.ids_out[o] = ids_s[b][lane];
+                    if (A.w_out) A.w_out[o] = w_s[b][lane];
+                }
+                if (lane == 0 && s_err) atomicOr(A.err, 1);
+            }
         }
         K1_TS(13);
-        K1_SYNC_DEAD();
         K1_TS(4);
-        if (gw == 0) {
-            if (tid < B * RTOPK) {
-                const size_t o = ((size_t)li * B + (tid >> 3)) * RTOPK + (tid & 7);
-                if (A.ids_out) A.ids_out[o] = ids_s[tid >> 3][tid & 7];
-                if (A.w_out) A.w_out[o] = w_s[tid >> 3][tid & 7];
-            }
-            if (tid == 0 && s_err) atomicOr(A.err, 1);
-        }
+        /* no barrier: each wave takes token b's rows as soon as wave b has
+         * stored its ids (an LDS flag set before the softmax weights) */
 
         /* ---- 4. the slot experts of the B tokens -------------------------- */
         {
             constexpr int DG = 2;                            /* tokens' gate/up rows in flight */
             QChunk2 st[DG][2];
             auto gu_load = [&](int b, QChunk2 (&ch)[2]) {
+                k1_flag_wait(&s_ids_rdy[min(b, B - 1)], li + 1);
                 const int e = __builtin_amdgcn_readfirstlane(ids_s[min(b, B - 1)][grp]);   /* wave-uniform */
                 const size_t ee = e >= 0 ? (size_t)e : 0;
                 const uint8_t *ge = L.gate + ee * L.eb[0], *ue = L.up + ee * L.eb[1];
