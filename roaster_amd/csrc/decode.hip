@@ -1823,9 +1823,13 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
     __shared__ float4 rrow_s[8][64];                          /* router row gw */
     __shared__ float4 gin_s[8][64];                           /* shared-gate vector */
     __shared__ QChunk2 shc_s[2][64];                          /* this workgroup's shared gate/up pairs */
-    __shared__ QChunk sdc_s[2][64];                           /* its shared down rows (H <= 2048: 2 tasks) */
+    /* its shared down rows (H <= 2048: 2 tasks), by layer parity: a wave
+     * parks the next layer's once its own h units are in, which need not be
+     * after every other wave's reads of this layer's */
+    __shared__ QChunk sdc_s[2][2][64];
     __shared__ int s_dead, s_err;
     __shared__ int s_ids_rdy[NB];                             /* layer index + 1 once token b's ids are in */
+    __shared__ int s_eh_rdy[NB];                              /* ... once its SiLU*up vectors are in */
 
     constexpr int I = 512, nbi = 2, SP = 2, RGP = I / K1_GW;
     const int H = A.H, E = A.E, B = A.B, HU = H / 4, nbh = H / RQK;
@@ -1860,7 +1864,10 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
         s_dead = 0;
         s_err = 0;
     }
-    if (tid < NB) s_ids_rdy[tid] = 0;
+    if (tid < NB) {
+        s_ids_rdy[tid] = 0;
+        s_eh_rdy[tid] = 0;
+    }
     int dead = (gld_u32(A.err) & 2u) != 0;
     constexpr int DQ = (int)(sizeof(DecLayer) / 16);
     if (tid < n * DQ) ((uint4 *)Ls)[tid] = ((const uint4 *)(A.layers + A.layer0))[tid];
@@ -1928,7 +1935,7 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
             for (int m = 0; m < 8; m++) dst[m][lane] = rw[m];
         }
         if (wv >= K1_W - SP) shc_s[wv - (K1_W - SP)][lane] = shc;
-        if (sdt >= 0) sdc_s[sdt][lane] = sdc;
+        if (sdt >= 0) sdc_s[li & 1][sdt][lane] = sdc;
         K1_SYNC_DEAD();
         if (dead) break;                                  /* workgroup-uniform */
         /* the owned rows' residual (rows gi RD .. + RD), each unit's own h */
@@ -1989,9 +1996,8 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
 
         K1_TS(2);
         /* ---- 2. per token b, on wave b: router logit gw; the 2 B shared
-         * SiLU*up values (pair t % SP of token t / SP), then the B shared-gate
-         * logits, dealt to waves 1..7 in turn (wave 0 goes on to relay the
-         * logits) ------------------------------------------------------------- */
+         * SiLU*up values (pair t % SP of token t / SP) dealt to waves 1..7 in
+         * turn (wave 0 goes on to relay the logits) --------------------------- */
         for (int b = wv; b < B; b += K1_W) {
             float4 r4[8];
             if (rrow) {
@@ -2008,13 +2014,6 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
             const int pr = t % SP, b = t / SP;
             const float eh = k1_gu_pair(0, 0, shc_s[pr][lane], xn[b], xsum[b], swz, nbh, lane);
             if (lane == 0) xch_put(xehs + ((size_t)b * 256 + gw) * XCH_LN + pr, eh, ep);
-        }
-        for (int b = wv - 1; wv > 0 && b < B; b += K1_W - 1) {
-            float4 r4[8];
-#pragma unroll
-            for (int m = 0; m < 8; m++) r4[m] = gin_s[m][lane];
-            const float s = k1_row_dot(r4, (const float4 *)xn[b], H, swz, lane);
-            if (lane == 0) w_s[b][RTOPK] = 1.0f / (1.0f + expf(-s));
         }
 
         K1_TS(3);
@@ -2066,6 +2065,7 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
          * stored its ids (an LDS flag set before the softmax weights) */
 
         /* ---- 4. the slot experts of the B tokens -------------------------- */
+        float sg = 0.0f;
         {
             constexpr int DG = 2;                            /* tokens' gate/up rows in flight */
             QChunk2 st[DG][2];
@@ -2081,6 +2081,17 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
             };
 #pragma unroll
             for (int b = 0; b < DG - 1; b++) gu_load(b, st[b]);
+            /* wave b: token b's shared-gate logit while the first rows arrive
+             * (kept in a register for the combine; xn[b] is read here, before
+             * this wave's gate/up outputs, which every next-layer h value
+             * waits for) */
+            if (wv < B) {
+                float4 r4[8];
+#pragma unroll
+                for (int m = 0; m < 8; m++) r4[m] = gin_s[m][lane];
+                sg = 1.0f / (1.0f + expf(-k1_row_dot(r4, (const float4 *)xn[wv], H, swz, lane)));
+                asm volatile("" ::"v"(sg) : "memory");    /* computed here, before the wave's stores */
+            }
 #pragma unroll
             for (int b = 0; b < NB; b++) {
                 if (b >= B) break;
@@ -2125,8 +2136,8 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
                 }
             };
             /* 2 slots: the first token's down rows in flight through the
-             * gathers and the barrier (with more tokens the gathers' polls,
-             * queued behind them, measured slower) */
+             * gathers (with more tokens the gathers' polls, queued behind
+             * them, measured slower) */
             if constexpr (NB == 2) {
 #pragma unroll
                 for (int b = 0; b < DD - 1; b++) dn_load(b, st[b]);
@@ -2138,8 +2149,9 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
                 ehshs[wv][lane] = k1_gather_run(lehs + (size_t)wv * I, I, lane, ep, dead, A.spin, ehsh[wv] + 16 * lane);
                 ehks[wv][lane] = k1_gather_run(lehx + (size_t)wv * I, I, lane, ep, dead, A.spin, ehk[wv] + 16 * lane);
             }
+            /* no barrier: a token's down rows wait for its own flag */
+            if (wv < B && lane == 0) __hip_atomic_store(&s_eh_rdy[wv], li + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             K1_TS(10);
-            K1_SYNC_DEAD();
             K1_TS(7);
             if constexpr (NB != 2) {
 #pragma unroll
@@ -2152,7 +2164,8 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
                 const int k = t % nsd, b = t / nsd;
                 const int rl = k * rpw + rw_;
                 const bool live = rl < RO && lbd < nbi;
-                const float part = k1_down_row(1, sdc_s[k][lane], ehsh[b], ehshs[b], live, lpr, lane);
+                k1_flag_wait(&s_eh_rdy[b], li + 1);
+                const float part = k1_down_row(1, sdc_s[li & 1][k][lane], ehsh[b], ehshs[b], live, lpr, lane);
                 if (live && lr == 0) xch_put(xdsh + ((size_t)b * 256 + gw) * XCH_LN + rl, part, ep);
             }
 #pragma unroll
@@ -2161,6 +2174,7 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
                 const bool live_slot = ids_s[b][grp] >= 0;
                 if (b + DD - 1 < NB) dn_load(b + DD - 1, st[(b + DD - 1) % DD]);
                 QChunk (&cur)[2] = st[b % DD];
+                k1_flag_wait(&s_eh_rdy[b], li + 1);
 #pragma unroll
                 for (int f = 0; f < 2; f++) {
                     const int task = wv + f * K1_W;
@@ -2192,7 +2206,7 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
                 float y = 0.0f;
 #pragma unroll
                 for (int k = 0; k < RTOPK; k++) y = fmaf(w_s[b][k], d[k], y);
-                y = fmaf(w_s[b][RTOPK], d[RTOPK], y);
+                y = fmaf(sg, d[RTOPK], y);
                 const float hn = hown[b][lane] + y;
                 if (!last) xch_put_xcd(lh + (size_t)b * H + (size_t)(row & 3) * HU + (row >> 2), hn, ep, l2);
                 else if (grp == 0) {
@@ -2203,7 +2217,9 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
         }
         K1_TS(9);
     }
-    if (tid == 0 && (dead || s_dead)) atomicOr(A.err, 2);
+    /* a wait that gave up after the layer's last barrier is known only to
+     * its own thread: every such thread reports it */
+    if (dead || (tid == 0 && s_dead)) atomicOr(A.err, 2);
 #ifdef ROASTER_PHASE_TS
     if (threadIdx.x == 0 || threadIdx.x == 64 || threadIdx.x == 448)
         for (int k = 0; k < 2; k++)
