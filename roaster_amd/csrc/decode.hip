@@ -1750,16 +1750,23 @@ extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stack1_2x2_kernel(DecA
  *      in wave order), 1/rms per token, the normalised inputs and their run
  *      sums, the owned rows' residuals;
  *   2. router row gw for token b on wave b; the shared expert's SiLU*up pairs
- *      of this workgroup and the shared-gate logits on waves 1..7;
+ *      of this workgroup on waves 1..7;
  *   3. wave 0 relays the logits, wave K1_WN the shared values, into the XCD's
- *      region; wave b ranks token b's top 8;
- *   4. the slot experts' gate/up rows token after token (the next token's rows
- *      in flight while the current one's are dotted; a wave's four rows share
- *      one read of the token's activations), SiLU*up within the XCD; wave b
- *      gathers token b's shared and slot SiLU*up values; the shared expert's
- *      down rows, then the slot experts' down rows token after token;
+ *      region; wave b ranks token b's top 8 and raises token b's ids flag;
+ *   4. the slot experts' gate/up rows token after token, each token's once its
+ *      ids flag is up (the next token's rows in flight while the current one's
+ *      are dotted; a wave's four rows share one read of the token's
+ *      activations), SiLU*up within the XCD; wave b takes token b's
+ *      shared-gate logit while its first rows arrive, gathers token b's shared
+ *      and slot SiLU*up values and raises its flag; the shared expert's down
+ *      rows, then the slot experts' down rows token after token, each token's
+ *      once its flag is up;
  *   5. wave b combines token b's owned rows (model.c:1139-1144 order) and
  *      publishes them within the XCD.
+ * The workgroup barriers are those of step 1; later handoffs are LDS flags,
+ * and the one LDS buffer a wave may rewrite for the next layer before another
+ * wave has read it for this one (the shared down rows) is double-buffered by
+ * layer parity.
  * Every dot, sum, softmax and combine is the one-token kernel's, in its order,
  * so each token's results equal its one-token results bit for bit.  Shapes:
  * inter 512, hidden 512..2048 in whole 256-row blocks, at most 256 experts;
