@@ -1840,7 +1840,7 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
 
     constexpr int I = 512, nbi = 2, SP = 2, RGP = I / K1_GW;
     const int H = A.H, E = A.E, B = A.B, HU = H / 4, nbh = H / RQK;
-    const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
+    const int tid = threadIdx.x, wv = wave_id();
     unsigned xcc;
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
     xcc &= 0xFu;
