@@ -71,6 +71,9 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill legs")
     ap.add_argument("--cpu-tokens", type=int, default=160)
     ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--fused-mode", type=int, default=None,
+                    help="roaster_decode_fused_layer mode: 1 default one-launch kernels, 2 the one-token kernel "
+                         "with the three-kernel path's arithmetic, 0 three kernels per layer")
     ap.add_argument("--three-kernel", action="store_true",
                     help="decode one token's layers with three launches each instead of one (for comparison)")
     ap.add_argument("--legs", default="decode,prefill,config1,config2,dense",
@@ -702,6 +705,8 @@ def main():
     stream = torch.cuda.ExternalStream(L.roaster_stream(), device=dev)
     if args.three_kernel:
         L.roaster_decode_fused_layer(0)
+    if args.fused_mode is not None:
+        L.roaster_decode_fused_layer(args.fused_mode)
     legs = set(args.legs.split(","))
     line = {"metric": "partial run: legs %s" % sorted(legs)}
     if "decode" in legs:

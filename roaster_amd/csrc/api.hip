@@ -553,7 +553,7 @@ extern "C" int roaster_moe_decode_stack(RoasterTable *t, float *h, int B, int la
  * device memory can call it.  In host code `scratch` names a host-side
  * stand-in, not the device array: its device address is looked up once per
  * device at initialisation (noalloc_setup) and only that address is used. */
-#define NOALLOC_BYTES (512u << 10)
+#define NOALLOC_BYTES (576u << 10)
 static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
 
 #define NOALLOC_MAX_DEV 64
@@ -584,10 +584,12 @@ extern "C" int roaster_moe_decode_stack_noalloc(RoasterTable *t, float *h, int B
     DecArgs A;
     fill_table_args(A, t);
     const size_t E = (size_t)A.E, Bz = (size_t)B, H = (size_t)A.H, I = (size_t)A.I;
-    const bool one = dec_layer1_ok(A.E, A.H, A.I, B);
     const size_t o_plan = 256, o_log = o_plan + al256(sizeof(DecPlan)), o_sg = o_log + al256(Bz * E * 4),
-                 o_eh = o_sg + al256(Bz * 4), o_xn = o_eh + al256(Bz * 9 * I * 4), o_x = o_xn + al256(Bz * (H + H / 16) * 4),
-                 end = o_x + (one ? al256((size_t)XCH_U64(E, H, I) * 8) : 0);
+                 o_eh = o_sg + al256(Bz * 4), o_xn = o_eh + al256(Bz * 9 * I * 4), o_x = o_xn + al256(Bz * (H + H / 16) * 4);
+    /* one token runs the one-launch kernel when its exchange slots fit behind
+     * the intermediates, else three kernels per layer */
+    const bool one = dec_layer1_ok(A.E, A.H, A.I, B) && o_x + al256(dec_xch_need1(A.E, A.H, A.I) * 8) <= NOALLOC_BYTES;
+    const size_t end = o_x + (one ? al256(dec_xch_need1(A.E, A.H, A.I) * 8) : 0);
     if (end > NOALLOC_BYTES)
         return rt_fail(ROASTER_EINVAL,
                        "roaster_moe_decode_stack_noalloc: %d tokens x hidden %zu x inter %zu x %zu experts need %zu "
@@ -604,22 +606,30 @@ extern "C" int roaster_moe_decode_stack_noalloc(RoasterTable *t, float *h, int B
     A.ids_out = ids_out;
     A.w_out = w_out;
     A.err = (int *)base;
+    A.cnt = (uint32_t *)(base + 64);     /* the one-token kernel's completion counter */
     rt_aux_err_used();
     A.plan_g = (DecPlan *)(base + o_plan);
     A.logits = (float *)(base + o_log);
     A.sgate_raw = (float *)(base + o_sg);
     A.eh = (float *)(base + o_eh);
     A.xn_g = (float *)(base + o_xn);
+    /* The exchange slots keep their own epoch counter; the array was
+     * zero-filled at load.  Its bytes past o_x are the exchange of the shape
+     * that last ran the one-launch kernel; any other call (another shape, or
+     * the three-kernel path of 2-8 tokens) may store plain intermediates there,
+     * whose bits could later match an epoch: then the region is cleared by a
+     * fill kernel (no allocation) and epochs start again. */
+    static DecXch xb[NOALLOC_MAX_DEV];
+    static uint64_t xkey[NOALLOC_MAX_DEV];   /* shape of the last call that ran the one-launch kernel; 0: none or dirty */
+    DecXch &X = xb[rt().device];
+    const uint64_t key = one ? (E << 44) ^ (H << 24) ^ (I << 4) ^ 1u : 0u;
     if (one) {
-        /* the exchange slots keep their own epoch counter; the array was
-         * zero-filled at load and is never cleared by the host, so it needs no
-         * allocation or memset here */
-        static DecXch xb[NOALLOC_MAX_DEV];
-        DecXch &X = xb[rt().device];
         X.p = (uint64_t *)(base + o_x);
-        X.n = (size_t)XCH_U64(E, H, I);
+        X.n = dec_xch_need1(A.E, A.H, A.I);
+        if (xkey[rt().device] != key && dec_xch_clear(X)) return ROASTER_EDEVICE;
         A.xbuf = &X;
     }
+    xkey[rt().device] = key;
     return dec_launch(A);
 }
 

@@ -78,6 +78,7 @@ struct DecArgs {
     uint32_t spin;              /* polls before a wait gives up (set by the launch code) */
     int xl2;                    /* 1: slots read only within the writer's XCD stay in its L2 */
     struct DecXch *xbuf;        /* host side: the buffer behind xch and its epoch counter, or NULL */
+    uint32_t *cnt;              /* dec_stack1r_kernel: completion counter (a multiple of 256 between launches), or NULL */
 };
 
 /* Exchange regions of the one-launch stack, in u64 slots; every region
@@ -124,6 +125,31 @@ struct DecArgs {
 #define XCHB_U64(NB, E, H, I) (XCHB_LOC0(NB, E, H, I) + 8 * XCHB_LOCN(NB, E, H, I))
 #define K1B_MAXB 8                                  /* tokens of the batched one-launch stack */
 
+/* Regions of the one-token stack whose router is folded into the combine
+ * (dec_stack1r_kernel: 256 experts, hidden 2048, inter 512).  Read across
+ * XCDs: the router partials [8][32][32] (XCD k's workgroup gi writes the 32
+ * partial logits of experts 32k..32k+31 over its 64 combined rows, two lines
+ * of its own), workgroup b's shared SiLU*up values [256][16], the routed
+ * down outputs [8][H], the shared down outputs [256][16] and the staged
+ * final hidden state [H].  Then one region
+ * per XCD: its logits [256], the row sums of squares of its 32 workgroups
+ * [32], its copies of the shared and routed SiLU*up values [I] each, and its
+ * copy of the hidden state [H] (SiLU*up and hidden rows in the run-major
+ * layouts above). */
+#define XR_PL(E, H, I) ((size_t)0)
+#define XR_EHS(E, H, I) ((size_t)8 * 32 * 32)
+#define XR_DX(E, H, I) (XR_EHS(E, H, I) + (size_t)256 * XCH_LN)
+#define XR_DSH(E, H, I) (XR_DX(E, H, I) + 8 * (size_t)(H))
+#define XR_HST(E, H, I) (XR_DSH(E, H, I) + (size_t)256 * XCH_LN)
+#define XR_LOC0(E, H, I) (XR_HST(E, H, I) + (size_t)(H))
+#define XR_LOCN(E, H, I) ((size_t)256 + 32 + 2 * (size_t)(I) + (size_t)(H))
+#define XR_LLG(I) ((size_t)0)
+#define XR_LSS(I) ((size_t)256)
+#define XR_LEHS(I) ((size_t)256 + 32)
+#define XR_LEHX(I) ((size_t)256 + 32 + (size_t)(I))
+#define XR_LH(I) ((size_t)256 + 32 + 2 * (size_t)(I))
+#define XR_U64(E, H, I) (XR_LOC0(E, H, I) + 8 * XR_LOCN(E, H, I))
+
 /* Exchange buffer of the one-launch stack: the slots and the last epoch
  * written into them.  Epochs grow by one per layer; before the 32-bit epoch
  * would wrap, the slots are cleared (by a fill kernel) and epochs start
@@ -138,9 +164,13 @@ int dec_ffn_launch(DecArgs &A);      /* kernel_ffn_fused: gate/up + down kernels
 /* Whether one token's layers can run as one launch (dec_stack1_kernel) for
  * these shapes on this device. */
 bool dec_layer1_ok(int E, int H, int I, int B);
+/* The exchange slots a one-token launch of these shapes uses (0: none). */
+size_t dec_xch_need1(int E, int H, int I);
 /* Whether B = 2..8 tokens' layers can run as one launch (dec_stackB_kernel)
  * for these shapes on this device (the matrix types are checked per launch). */
 bool dec_layerB_ok(int E, int H, int I, int B);
+/* Clears X's slots on the library stream (a fill kernel) and restarts its epochs. */
+int dec_xch_clear(DecXch &X);
 /* The library's exchange buffer (allocated and cleared on first use). */
 DecXch *dec_xch_default(int E, int H, int I);
 

@@ -1738,6 +1738,553 @@ extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stack1_kernel(DecArgs 
  * gate/up Q4_K and down Q6_K, routed and shared (types 0b100100) */
 extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stack1_2x2_kernel(DecArgs A) { stack1_body<2, 2, 0x24>(A); }
 
+/* ---- one token, the router folded into the combine (dec_stack1r_kernel) ----
+ * 256 experts, hidden 2048, inter 512, gate/up Q4_K and down Q6_K (routed and
+ * shared).  Groups and slots as in dec_stack1_kernel (XCD k serves routed
+ * slot k; workgroup gi of every XCD combines rows [64 gi, 64 gi + 64)), but
+ * each layer's router logits come from the rows the workgroups have just
+ * combined, by linearity of the norm once 1/rms is known:
+ *   logit_e = inv_rms * sum_gi P[e][gi],   P[e][gi] = sum_{r in rows(gi)} W_r[e][r] (nw[r] h[r]),
+ *   inv_rms = 1 / sqrt(sum_gi S[gi] / H + eps),  S[gi] = sum_{r in rows(gi)} h[r]^2.
+ * XCD k's workgroup gi computes P for experts 32k .. 32k + 31 (its 8 KB slice
+ * of the router, in LDS), so the chain from a combine to the next layer's top
+ * 8 is: the partials (one wave: products, then a reduce-scatter over its
+ * lanes) -> across XCDs -> each workgroup sums the partials of 8 experts ->
+ * within the XCD -> top 8.  The hidden state's gather and normalisation,
+ * which only the gate/up dots need, run beside that chain.  Per layer:
+ *   wave 0: partials, row sum of squares and its 64 rows of h published; the
+ *     logits of experts 8 gi .. 8 gi + 7 into the XCD's copy; all 256 logits
+ *     gathered, the top 8 (ids flag); its share of the slot expert's rows; the
+ *     XCD's SiLU*up gather; the combine of its 64 rows (h kept in registers);
+ *   waves 1..4: this XCD's copy of h (first layer: the caller's h), 1/rms from
+ *     the 32 row sums, the normalised input and its run sums (xn counter);
+ *     wave 2 then the shared-gate logit, wave 3 the shared SiLU*up relay and
+ *     gather;
+ *   wave 5: the next layer's router slice and norm weights into LDS (two
+ *     buffers by layer parity, a counter for wave 0), then its rows;
+ *   waves 6, 7: the shared expert's gate/up pairs and down rows.
+ * One workgroup barrier per layer (before the down dots).  The final hidden
+ * state is staged in the exchange buffer; the last workgroup to finish copies
+ * it over the caller's h only when no wait gave up anywhere, so a call that
+ * reports ROASTER_EDEVICE leaves h as it was.  The dots, the routed and shared
+ * SiLU*up values, the softmax and the combine are the three-kernel path's;
+ * the logits and 1/rms differ from it in their summation order only. */
+#define R1_H 2048
+#define R1_I 512
+#define R1_E 256
+#define R1_RD (R1_H / K1_GW)        /* rows combined per workgroup */
+#define R1_EX (R1_E / K1_G)         /* experts whose partials one XCD computes */
+#define R1_RSP (R1_EX + 4)          /* LDS pitch (floats) of a router-slice row */
+#define R1_WPF 5                    /* wave that prefetches the router slice and norm weights */
+
+/* Sums over the 64 lanes of v[0..31]: lanes 2j and 2j + 1 receive value j's
+ * sum.  A reduce-scatter: permlane32 / permlane16 swaps exchange halves of
+ * the values, then row mirrors and quad swaps; the order is fixed, so the
+ * sums are deterministic. */
+__device__ __forceinline__ float wave_rs32(float (&v)[32])
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v[j]),
+                                                        __builtin_bit_cast(uint32_t, v[j + 16]), false, false);
+        v[j] = __builtin_bit_cast(float, (uint32_t)p[0]) + __builtin_bit_cast(float, (uint32_t)p[1]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v[j]),
+                                                        __builtin_bit_cast(uint32_t, v[j + 8]), false, false);
+        v[j] = __builtin_bit_cast(float, (uint32_t)p[0]) + __builtin_bit_cast(float, (uint32_t)p[1]);
+    }
+    const bool b3 = (lane & 8) != 0, b2 = (lane & 4) != 0, b1 = (lane & 2) != 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float keep = b3 ? v[j + 4] : v[j], send = b3 ? v[j] : v[j + 4];
+        v[j] = keep + dpp_f<DPP_MIRROR>(send);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const float keep = b2 ? v[j + 2] : v[j], send = b2 ? v[j] : v[j + 2];
+        v[j] = keep + dpp_f<DPP_HALF_MIRROR>(send);
+    }
+    const float keep = b1 ? v[1] : v[0], send = b1 ? v[0] : v[1];
+    const float s = keep + dpp_f<DPP_XOR2>(send);
+    return s + dpp_f<DPP_XOR1>(s);
+}
+
+#define DPP_ROR8 0x128         /* row_ror:8 (lane i <- lane i ^ 8 within 16) */
+
+/* LDS position of run r (values 16r .. 16r + 15) of a SiLU*up vector in the
+ * folded-router kernel: run r moved up by ((r >> 3) & 3) 16-byte granules, so
+ * that the 16 lanes of a down row (runs {0..3, 8..11} + 16 lb and those + 4)
+ * read 16 different bank groups in each ds_read_b128 pass instead of four
+ * lanes per group.  off is a multiple of 16; the vector needs 12 floats more. */
+__device__ __forceinline__ int r1_ehpos(int off) { return off + 4 * ((off >> 7) & 3); }
+
+/* k1_gather_run into the rotated layout (dst + r1_ehpos(16 r)). */
+__device__ __forceinline__ float r1_gather_run(const uint64_t *base, int I, int r, uint32_t ep, int &dead,
+                                               uint32_t spin, float *dst)
+{
+    return k1_gather_run(base, I, r, ep, dead, spin, dst + r1_ehpos(16 * r));
+}
+
+/* k1_down_row's arithmetic on a rotated SiLU*up vector. */
+__device__ __forceinline__ float r1_down_row(const QChunk &ch, const float *eh, const float *ehs, bool live, int lane)
+{
+    const int lr = lane & 15, c = lr & 7, lb = lr >> 3;
+    float part = 0.0f;
+    if (live) {
+        const int ca = lb * RQK + q_run_a<true>(c), cb = ca + 64;
+        part = q_chunk_dot<true>(ch, c, eh + r1_ehpos(ca), eh + r1_ehpos(cb), ehs[ca >> 4], ehs[cb >> 4]);
+    }
+    return group_sum<16>(part);
+}
+
+/* The sum over the 8 lanes l, l ^ 8, ..., l ^ 56 (fixed order; the same value
+ * in each of them). */
+__device__ __forceinline__ float sum_over_l8(float s)
+{
+    s += dpp_f<DPP_ROR8>(s);
+    auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, s), __builtin_bit_cast(uint32_t, s), false, false);
+    s = __builtin_bit_cast(float, (uint32_t)p[0]) + __builtin_bit_cast(float, (uint32_t)p[1]);
+    p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, s), __builtin_bit_cast(uint32_t, s), false, false);
+    return __builtin_bit_cast(float, (uint32_t)p[0]) + __builtin_bit_cast(float, (uint32_t)p[1]);
+}
+
+/* 1/rms from the 32 row sums of squares of an XCD (lanes 0..31 hold them). */
+__device__ __forceinline__ float r1_inv_rms(const DecArgs &A, float ssv)
+{
+    const int lane = threadIdx.x & 63;
+    const float ss = group_sum<64>(lane < 32 ? ssv : 0.0f);
+    return A.do_norm ? 1.0f / sqrtf(ss / (float)R1_H + A.eps) : 1.0f;
+}
+
+/* Layer l's router slice (experts 32 grp .., rows 64 gi ..; stored [row][expert]
+ * with pitch R1_RSP) and norm weights into LDS buffer b (wave R1_WPF). */
+__device__ __forceinline__ void r1_prefetch_rs(const DecArgs &A, const DecLayer &L, int l, int grp, int gi,
+                                               float (*rsl)[R1_RD * R1_RSP], float (*nws)[R1_H], int b, bool router)
+{
+    const int lane = threadIdx.x & 63;
+    float4 r[8], w[8];
+    const float *nw = A.do_norm && A.norm_w ? A.norm_w + (size_t)(l - A.layer0) * R1_H : NULL;
+    /* both loads unconditional (without norm weights the first 8 KB of the
+     * router stand in, never stored): conditionally filled arrays are kept in
+     * scratch memory by the compiler */
+    const float *nwp = nw ? nw : L.router;
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        const int q = lane + 64 * m, e = q >> 4, c4 = q & 15;
+        r[m] = gld_f4(L.router + (size_t)(R1_EX * grp + e) * R1_H + R1_RD * gi + 4 * c4);
+    }
+#pragma unroll
+    for (int m = 0; m < 8; m++) w[m] = gld_f4(nwp + 4 * (lane + 64 * m));
+    if (router) {
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const int q = lane + 64 * m, e = q >> 4, c4 = q & 15;
+            float *d = rsl[b] + (4 * c4) * R1_RSP + e;
+            d[0] = r[m].x;
+            d[R1_RSP] = r[m].y;
+            d[2 * R1_RSP] = r[m].z;
+            d[3 * R1_RSP] = r[m].w;
+        }
+    }
+    if (nw) {
+#pragma unroll
+        for (int m = 0; m < 8; m++) ((float4 *)nws[b])[lane + 64 * m] = w[m];
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stack1r_kernel(DecArgs A)
+{
+    constexpr int H = R1_H, I = R1_I, E = R1_E, HU = H / 4, nbh = H / RQK, nbi = I / RQK;
+    constexpr int RD = R1_RD, SP = I / 256, RO = H / 256, RGP = I / K1_GW;
+    constexpr int lpr = 16, rpw = 64 / lpr, ndt = RD / rpw, nsd = (RO + rpw - 1) / rpw, SPW = I / K1_GW;
+    static_assert(RGP == 2 * K1_W && ndt == 2 * K1_W && SP == 2 && nsd == 2, "two gate/up pairs and two down tasks per wave");
+    __shared__ __align__(16) float xn[H];
+    __shared__ float xsum[H / 16];
+    __shared__ __align__(16) float nw_s[2][H];
+    __shared__ __align__(16) float rsl_s[2][RD * R1_RSP];
+    __shared__ __align__(16) float ehk[I + 16];
+    __shared__ float ehks[I / 16];
+    __shared__ __align__(16) float ehsh[I + 16];
+    __shared__ float ehshs[I / 16];
+    __shared__ TopkScratch tks;
+    __shared__ int ids_s[RTOPK];
+    __shared__ float w_s[RTOPK + 1];
+    __shared__ __align__(16) DecLayer Ls[K1_MAXL];
+    __shared__ float4 gin_s[8][64];
+    __shared__ QChunk2 shc_s[SP][64];
+    __shared__ QChunk sdc_s[nsd][64];
+    __shared__ int s_dead, s_err, s_last;
+    __shared__ int s_ids_ready, s_xn, s_pre;
+
+    const int tid = threadIdx.x, wv = wave_id();
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 0xFu;
+    const bool l2 = A.xl2 && xcc < (unsigned)K1_G;
+    if (A.xl2 && !l2 && threadIdx.x == 0) atomicOr(A.err, 4);
+    const int grp = l2 ? (int)xcc : (int)(blockIdx.x % K1_G), gi = blockIdx.x / K1_G, gw = blockIdx.x;
+    const bool swz = A.xswz;
+    uint64_t *xpl = A.xch + XR_PL(E, H, I);                   /* across XCDs */
+    uint64_t *xehs = A.xch + XR_EHS(E, H, I);
+    uint64_t *xdx = A.xch + XR_DX(E, H, I);
+    uint64_t *xdsh = A.xch + XR_DSH(E, H, I);
+    uint64_t *xhst = A.xch + XR_HST(E, H, I);
+    uint32_t *xcnt = A.cnt;
+    uint64_t *loc = A.xch + XR_LOC0(E, H, I) + (size_t)grp * XR_LOCN(E, H, I);   /* this XCD's */
+    uint64_t *llg = loc + XR_LLG(I), *lss = loc + XR_LSS(I), *lehs = loc + XR_LEHS(I), *lehx = loc + XR_LEHX(I),
+             *lh = loc + XR_LH(I);
+    const int n = A.nlayers;
+    const bool given = A.logits_in != NULL;
+    const bool stage = A.y == NULL;                          /* stack mode: h is updated in place */
+#ifdef ROASTER_PHASE_TS
+    unsigned long long tsv[2][16] = {};
+    int tsl = 0;
+#define R1_TS(i) asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(tsv[tsl][i]) : : "memory")
+#else
+#define R1_TS(i) ((void)0)
+#endif
+#define R1_TSW(w, i)            \
+    do {                        \
+        if (wv == (w)) R1_TS(i); \
+    } while (0)
+    if (tid == 0) {
+        s_dead = 0;
+        s_err = 0;
+        s_ids_ready = 0;
+        s_xn = 0;
+        s_pre = 1;                                           /* the first layer's slice: before the second barrier */
+    }
+    /* error bit 2 from an earlier launch that gave up: wait for nothing */
+    int dead = (gld_u32(A.err) & 2u) != 0;
+    constexpr int DQ = (int)(sizeof(DecLayer) / 16);
+    if (tid < n * DQ) ((uint4 *)Ls)[tid] = ((const uint4 *)(A.layers + A.layer0))[tid];
+    __syncthreads();
+    DecLayer L = k1_layer(Ls, 0);
+    /* the first layer's loads that depend on nothing computed */
+    {
+        const int lane = tid & 63, c = lane & 7, lb = lane >> 3, rw_ = lane / lpr, lr = lane % lpr;
+        if (wv == R1_WPF) r1_prefetch_rs(A, L, A.layer0, grp, gi, rsl_s, nw_s, 0, !given);
+        if (wv == K1_WGI) {
+#pragma unroll
+            for (int m = 0; m < 8; m++) gin_s[m][lane] = gld_f4(L.gate_inp + 4 * lane + 256 * m);
+        }
+        if (wv >= K1_W - SP) {
+            const size_t j = (size_t)gw * SP + (wv - (K1_W - SP));
+            QChunk2 ch;
+            ch.g = q_load_t(0, L.sgate, j, nbh, lb, c);
+            ch.u = q_load_t(0, L.sup, j, nbh, lb, c);
+            shc_s[wv - (K1_W - SP)][lane] = ch;
+            const int sdt = wv - (K1_W - nsd);
+            sdc_s[sdt][lane] = q_load_t(1, L.sdown, (size_t)min(gw * RO + sdt * rpw + rw_, H - 1), nbi, lr >> 3, lr & 7);
+        }
+    }
+    __syncthreads();
+    float hcur = 0.0f;                                       /* wave 0, lane r: h of row 64 gi + r */
+    if (wv == 0) hcur = A.h[RD * gi + (tid & 63)];
+
+    for (int li = 0; li < n; li++) {
+        int tid_v = (int)threadIdx.x;
+        asm volatile("" : "+v"(tid_v));
+        const int lane = tid_v & 63, c = lane & 7, lb = lane >> 3;
+        const int rw_ = lane / lpr, lr = lane % lpr, lbd = lr >> 3;
+        const int l = A.layer0 + li, par = li & 1;
+        const uint32_t ep = A.epoch + (uint32_t)li;
+        const bool last = li + 1 == n;
+        const bool nwl = A.do_norm && A.norm_w;
+        float4 *x4 = (float4 *)xn;
+#ifdef ROASTER_PHASE_TS
+        tsl = last ? 1 : 0;
+#endif
+        R1_TSW(6, 0);
+        R1_TSW(3, 0);
+        if (wv == 0) {
+            R1_TS(0);
+            /* ---- A. partials of XCD grp's experts over rows 64 gi .. ------------ */
+            const int row = RD * gi + lane;
+            const float ss = group_sum<64>(hcur * hcur);
+            if (lane == 0) xch_put_xcd(lss + gi, ss, ep, l2);
+            if (li > 0) xch_put_xcd(lh + (size_t)(row & 3) * HU + (row >> 2), hcur, ep, l2);
+            if (li > 0) k1_flag_wait(&s_pre, li + 1);
+            R1_TS(10);
+            if (!given) {
+                const float hn = nwl ? nw_s[par][row] * hcur : hcur;
+                float v[32];
+                const float4 *rs = (const float4 *)(rsl_s[par] + lane * R1_RSP);
+#pragma unroll
+                for (int m = 0; m < 8; m++) {
+                    const float4 w = rs[m];
+                    v[4 * m] = w.x * hn;
+                    v[4 * m + 1] = w.y * hn;
+                    v[4 * m + 2] = w.z * hn;
+                    v[4 * m + 3] = w.w * hn;
+                }
+                const float p = wave_rs32(v);
+                R1_TS(11);
+                if ((lane & 1) == 0) xch_put(xpl + (size_t)(grp * K1_GW + gi) * R1_EX + (lane >> 1), p, ep);
+            }
+            R1_TS(1);
+            /* ---- B. logits of experts 8 gi .. 8 gi + 7 ------------------------- */
+            float lg4[4];
+            if (!given) {
+                const int kx = gi >> 2, ex = 8 * (gi & 3) + (lane & 7);
+                const uint64_t *q[5];
+#pragma unroll
+                for (int i = 0; i < 4; i++) q[i] = xpl + (size_t)(kx * K1_GW + (lane >> 3) + 8 * i) * R1_EX + ex;
+                q[4] = lss + (lane & 31);
+                float v[5];
+                xch_gather<5>(q, lane < 32 ? 0x1Fu : 0x0Fu, ep, dead, A.spin, v);
+                const float s = sum_over_l8((v[0] + v[1]) + (v[2] + v[3]));
+                const float lgt = s * r1_inv_rms(A, v[4]);
+                if (lane < 8) {
+                    xch_put_xcd(llg + 8 * gi + lane, lgt, ep, l2);
+                    if (last && grp == 0) A.logits[8 * gi + lane] = lgt;
+                }
+                R1_TS(2);
+                /* ---- C. the 256 logits from this XCD's copy, top 8 ------------- */
+                const uint64_t *q4[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) q4[i] = llg + lane + 64 * i;
+                xch_gather<4>(q4, 0xFu, ep, dead, A.spin, lg4);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) lg4[i] = A.logits_in[lane + 64 * i];
+            }
+            R1_TS(3);
+            topk8_fast(lg4, E, ids_s, w_s, &s_err, &tks, &s_ids_ready, li + 1);
+            R1_TS(4);
+            asm volatile("; R1MARK topk done" ::: "memory");
+            if (gw == 0) {
+                if (lane < RTOPK) {
+                    const size_t o = (size_t)li * RTOPK + lane;
+                    if (A.ids_out) A.ids_out[o] = ids_s[lane];
+                    if (A.w_out) A.w_out[o] = w_s[lane];
+                }
+                if (lane == 0 && s_err) atomicOr(A.err, 1);
+            }
+        } else if (wv <= 4) {
+            /* ---- h of the layer, 1/rms, the normalised input --------------------- */
+            const int t = tid_v - 64;                        /* units t and t + 256 */
+            float4 hq[2];
+            float ssv;
+            if (li == 0) {
+                const uint64_t *q[1] = {lss + (lane & 31)};
+                float v[1];
+#pragma unroll
+                for (int k = 0; k < 2; k++) hq[k] = ((const float4 *)A.h)[t + 256 * k];
+                xch_gather<1>(q, lane < 32 ? 1u : 0u, ep, dead, A.spin, v);
+                ssv = v[0];
+            } else {
+                /* the h units and (lanes < 32) the row sums in one gather */
+                const uint64_t *q[9];
+                float v[9];
+#pragma unroll
+                for (int i = 0; i < 8; i++) q[i] = lh + (size_t)(i & 3) * HU + t + 256 * (i >> 2);
+                q[8] = lss + (lane & 31);
+                xch_gather<9>(q, lane < 32 ? 0x1FFu : 0xFFu, ep, dead, A.spin, v);
+                hq[0] = make_float4(v[0], v[1], v[2], v[3]);
+                hq[1] = make_float4(v[4], v[5], v[6], v[7]);
+                ssv = v[8];
+            }
+            R1_TSW(6, 1);
+            R1_TSW(3, 1);
+            const float inv = r1_inv_rms(A, ssv);
+            if (li > 0 && nwl) k1_flag_wait(&s_pre, li + 1);    /* this layer's norm weights */
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int u = t + k * 256;
+                float4 v = hq[k];
+                if (A.do_norm) {
+                    v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
+                    if (nwl) {
+                        const float4 wq = ((const float4 *)nw_s[par])[u];
+                        v.x *= wq.x; v.y *= wq.y; v.z *= wq.z; v.w *= wq.w;
+                    }
+                }
+                float r = (v.x + v.y) + (v.z + v.w);
+                r += dpp_f<DPP_XOR1>(r);
+                r += dpp_f<DPP_XOR2>(r);
+                x4[xpos(u, swz)] = v;
+                if ((t & 3) == 0) xsum[u >> 2] = r;
+            }
+            if (lane == 0) __hip_atomic_fetch_add(&s_xn, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            R1_TSW(6, 2);
+            R1_TSW(3, 2);
+            if (wv == K1_WGI) {
+                k1_flag_wait(&s_xn, 4 * (li + 1));
+                float4 rw[8];
+#pragma unroll
+                for (int m = 0; m < 8; m++) rw[m] = gin_s[m][lane];
+                const float s = k1_row_dot(rw, x4, H, swz, lane);
+                if (lane == 0) w_s[RTOPK] = 1.0f / (1.0f + expf(-s));
+            }
+        } else if (wv == R1_WPF) {
+            if (!last) {
+                const DecLayer Ln = k1_layer(Ls, li + 1);
+                r1_prefetch_rs(A, Ln, l + 1, grp, gi, rsl_s, nw_s, par ^ 1, !given);
+                if (lane == 0) __hip_atomic_store(&s_pre, li + 2, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        } else {
+            /* ---- the shared expert's gate/up pairs of this workgroup ------------ */
+            k1_flag_wait(&s_xn, 4 * (li + 1));
+            R1_TSW(6, 1);
+            const int pr = wv - (K1_W - SP);
+            const float eh = k1_gu_pair(0, 0, shc_s[pr][lane], xn, xsum, swz, nbh, lane);
+            if (lane == 0) xch_put(xehs + (size_t)gw * XCH_LN + pr, eh, ep);
+            R1_TSW(6, 2);
+        }
+        if (wv != 0) k1_flag_wait(&s_ids_ready, li + 1);
+        R1_TSW(6, 4);
+        R1_TSW(3, 4);
+
+        /* ---- D. the slot's expert ------------------------------------------------ */
+        R1_TSW(0, 14);
+        const int e = ids_s[grp];
+        const bool live_slot = e >= 0;
+        const size_t ee = live_slot ? (size_t)e : 0;          /* an unselected slot reads expert 0, unused */
+        const uint8_t *ge = L.gate + ee * L.eb[0], *ue = L.up + ee * L.eb[1], *de = L.down + ee * L.eb[2];
+        QChunk2 gch[2];
+        QChunk dch[2];
+        R1_TSW(0, 15);
+#pragma unroll
+        for (int f = 0; f < 2; f++) gch[f].g = q_load_t(0, ge, (size_t)gi * RGP + wv + f * K1_W, nbh, lb, c);
+#pragma unroll
+        for (int f = 0; f < 2; f++) gch[f].u = q_load_t(0, ue, (size_t)gi * RGP + wv + f * K1_W, nbh, lb, c);
+        const int sdt = wv - (K1_W - nsd);
+        asm volatile("; R1MARK before xn wait" ::: "memory");
+        R1_TSW(0, 12);
+        k1_flag_wait(&s_xn, 4 * (li + 1));
+        R1_TS(5);
+        float pgs[2];
+#pragma unroll
+        for (int f = 0; f < 2; f++) pgs[f] = k1_q_row(0, gch[f].g, xn, xsum, swz, nbh, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("; gate rows dotted" ::"v"(pgs[0]) : "memory");
+        R1_TSW(0, 13);
+#pragma unroll
+        for (int f = 0; f < 2; f++)
+            dch[f] = q_load_t(1, de, (size_t)(gi * RD + (wv + f * K1_W) * rpw + rw_), nbi, lbd, lr & 7);
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+            const int pj = wv + f * K1_W;
+            const float eh = silu_mul(pgs[f], k1_q_row(0, gch[f].u, xn, xsum, swz, nbh, lane));
+            if (lane == 0) xch_put_xcd(lehx + k1_run_slot(gi * RGP + pj, I), live_slot ? eh : 0.0f, ep, l2);
+        }
+        R1_TSW(6, 6);
+        R1_TSW(3, 6);
+        if (wv == K1_WN) {
+            /* the shared SiLU*up values: this workgroup's share relayed from the
+             * producing workgroups (published before the top 8) into the XCD's
+             * copy, then all of them from there (the shared down rows use them
+             * after the barrier) */
+            if (lane < SPW) {                                /* shared value j: slot j % SP of line j / SP */
+                const int j = gi * SPW + lane;
+                const uint64_t *q[1] = {xehs + (size_t)(j / SP) * XCH_LN + j % SP};
+                float v[1];
+                xch_gather<1>(q, 1u, ep, dead, A.spin, v);
+                xch_put_xcd(lehs + k1_run_slot(j, I), v[0], ep, l2);
+            }
+            R1_TS(8);
+            if (lane < I / 16) ehshs[lane] = r1_gather_run(lehs, I, lane, ep, dead, A.spin, ehsh);
+            R1_TS(3);
+        }
+        if (wv == 0) {
+            R1_TS(6);
+            if (lane < I / 16) ehks[lane] = r1_gather_run(lehx, I, lane, ep, dead, A.spin, ehk);
+        }
+        K1_SYNC_DEAD();
+        if (dead) break;                                      /* workgroup-uniform */
+        R1_TS(7);
+        if (sdt >= 0) {
+            /* the shared expert's down rows [gw RO, (gw + 1) RO): slot 8 of the
+             * down outputs (their SiLU*up values came in before the barrier) */
+            const int rl = sdt * rpw + rw_;
+            const bool live = rl < RO && lbd < nbi;
+            const float part = r1_down_row(sdc_s[sdt][lane], ehsh, ehshs, live, lane);
+            if (live && lr == 0) xch_put(xdsh + (size_t)gw * XCH_LN + rl, part, ep);
+        }
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+            const int rl = (wv + f * K1_W) * rpw + rw_, row = gi * RD + rl;
+            const float part = r1_down_row(dch[f], ehk, ehks, true, lane);
+            if (lr == 0) xch_put(xdx + (size_t)grp * H + row, live_slot ? part : 0.0f, ep);
+        }
+
+        /* ---- E. the next layer's loads; the combine of rows 64 gi .. ------------ */
+        if (!last) {
+            L = k1_layer(Ls, li + 1);
+            if (wv == K1_WGI) {
+                float4 r1[8];
+#pragma unroll
+                for (int m = 0; m < 8; m++) r1[m] = gld_f4(L.gate_inp + 4 * lane + 256 * m);
+#pragma unroll
+                for (int m = 0; m < 8; m++) gin_s[m][lane] = r1[m];
+            } else if (wv >= K1_W - SP) {
+                const size_t j = (size_t)gw * SP + (wv - (K1_W - SP));
+                QChunk2 ch;
+                ch.g = q_load_t(0, L.sgate, j, nbh, lb, c);
+                ch.u = q_load_t(0, L.sup, j, nbh, lb, c);
+                const QChunk sd = q_load_t(1, L.sdown, (size_t)min(gw * RO + sdt * rpw + rw_, H - 1), nbi, lbd, lr & 7);
+                shc_s[wv - (K1_W - SP)][lane] = ch;
+                sdc_s[sdt][lane] = sd;
+            }
+        }
+        if (wv == 0) {
+            R1_TS(8);
+            const int row = gi * RD + lane;
+            const uint64_t *q[RTOPK + 1];
+            float d[RTOPK + 1];
+#pragma unroll
+            for (int k = 0; k < RTOPK; k++) q[k] = xdx + (size_t)k * H + row;
+            q[RTOPK] = xdsh + (size_t)(row / RO) * XCH_LN + row % RO;
+            xch_gather<RTOPK + 1>(q, 0x1FFu, ep, dead, A.spin, d);
+            R1_TS(9);
+            float y = 0.0f;
+#pragma unroll
+            for (int k = 0; k < RTOPK; k++) y = fmaf(w_s[k], d[k], y);
+            y = fmaf(w_s[RTOPK], d[RTOPK], y);
+            hcur += y;
+            if (last && grp == 0) {
+                if (!stage) A.y[row] = y;
+                else xch_put(xhst + row, hcur, ep);
+            }
+        }
+    }
+    /* every workgroup counts itself done after reporting a wait that gave up;
+     * the last one copies the staged h over the caller's when none did */
+    if (dead) s_dead = 1;
+    __syncthreads();
+    if (tid == 0) {
+        if (s_dead) atomicOr(A.err, 2);
+        __threadfence();
+        const uint32_t old = __hip_atomic_fetch_add(xcnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (old + 1u) % (uint32_t)K1_NWG == 0u;
+    }
+    __syncthreads();
+    if (s_last && stage) {
+        const int ef = __hip_atomic_load(A.err, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+        if (!(ef & 2)) {
+            const uint32_t epl = A.epoch + (uint32_t)(n - 1);
+#pragma unroll
+            for (int k = 0; k < H / K1_T; k++) {
+                const int r = tid + k * K1_T;
+                const uint64_t v = xch_load(xhst + r);
+                if ((uint32_t)(v >> 32) == epl) A.h[r] = __builtin_bit_cast(float, (uint32_t)v);
+                else atomicOr(A.err, 2);
+            }
+        }
+    }
+#ifdef ROASTER_PHASE_TS
+    if (threadIdx.x == 0 || threadIdx.x == 192 || threadIdx.x == 384)
+        for (int k = 0; k < 2; k++)
+            for (int i = 0; i < 16; i++) g_k1_ts[k][blockIdx.x][threadIdx.x == 0 ? 0 : threadIdx.x == 192 ? 1 : 2][i] = tsv[k][i];
+#endif
+#undef R1_TS
+#undef R1_TSW
+}
+
 /* ---- the batched one-launch stack: 2..8 tokens --------------------------------
  * The one-token stack's groups and exchanges with a token index: group k (an
  * XCD) serves slot k of every token (the token's k-th expert), so the chain
@@ -2311,8 +2858,17 @@ extern "C" unsigned roaster_decode_spin_limit(unsigned polls)
 extern "C" int roaster_decode_fused_layer(int enable)
 {
     std::lock_guard<std::recursive_mutex> g(rt_lock());
-    if (enable == 0 || enable == 1) g_layer1 = enable;
+    if (enable >= 0 && enable <= 2) g_layer1 = enable;
     return g_layer1;
+}
+
+/* The router-folded one-token kernel's shapes (dec_stack1r_kernel); the
+ * matrix types are checked per launch. */
+static bool dec_r1_shape(int E, int H, int I) { return g_layer1 == 1 && E == R1_E && H == R1_H && I == R1_I; }
+
+size_t dec_xch_need1(int E, int H, int I)
+{
+    return std::max((size_t)XCH_U64(E, H, I), dec_r1_shape(E, H, I) ? (size_t)XR_U64(E, H, I) : (size_t)0);
 }
 
 bool dec_layer1_ok(int E, int H, int I, int B)
@@ -2340,9 +2896,17 @@ void dec_release()
     g_xch.epoch = 0;
 }
 
+int dec_xch_clear(DecXch &X)
+{
+    hipLaunchKernelGGL(dec_xch_clear_kernel, dim3(64), dim3(256), 0, rt().stream, X.p, X.n);
+    if (rt_check(hipGetLastError(), "exchange buffer clear")) return ROASTER_EDEVICE;
+    X.epoch = 0;
+    return 0;
+}
+
 DecXch *dec_xch_default(int E, int H, int I)
 {
-    const size_t n = std::max((size_t)XCH_U64(E, H, I), (size_t)XCHB_U64(K1B_MAXB, E, H, I));
+    const size_t n = std::max(dec_xch_need1(E, H, I), (size_t)XCHB_U64(K1B_MAXB, E, H, I));
     if (g_xch.p && g_xch.n >= n) return &g_xch;
     if (g_xch.p) {
         (void)hipStreamSynchronize(rt().stream);
@@ -2418,7 +2982,9 @@ static int launch_stack1(DecArgs &A0)
             const DecLayer *Lh = A.layers_h + l;
             ty = !Lh->q6[0] && !Lh->q6[1] && Lh->q6[2] && !Lh->sq6[0] && !Lh->sq6[1] && Lh->sq6[2];
         }
-        if (npg == 2 && nd == 2 && ty) hipLaunchKernelGGL(dec_stack1_2x2_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
+        if (ty && A.cnt && dec_r1_shape(A.E, A.H, A.I) && X.n >= (size_t)XR_U64(A.E, A.H, A.I))
+            hipLaunchKernelGGL(dec_stack1r_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
+        else if (npg == 2 && nd == 2 && ty) hipLaunchKernelGGL(dec_stack1_2x2_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
         else hipLaunchKernelGGL(dec_stack1_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
         if (rt_check(hipGetLastError(), "stack launch")) return ROASTER_EDEVICE;
     }
@@ -2473,6 +3039,7 @@ int dec_launch(DecArgs &A)
         A.plan_g = (DecPlan *)rt_scratch(SCR_C, sizeof(DecPlan));
         if (!ctrl || !A.plan_g) return ROASTER_ENOMEM;
         A.err = (int *)(ctrl + 16);
+        A.cnt = ctrl + 32;
     }
     if (A.xbuf && !A.ffn_out && dec_layer1_ok(A.E, A.H, A.I, A.B)) return launch_stack1(A);
     if (A.xbuf && !A.ffn_out && dec_layerB_ok(A.E, A.H, A.I, A.B))

@@ -3,9 +3,10 @@ against the three-kernel path (roaster_decode_fused_layer(0)), the one-token
 launch and the oracle.
 
 The batched launch computes every dot, sum of squares, softmax and combine of
-each token in the one-token launch's order, so each token's hidden state,
+each token in the three-kernel path's order, so each token's hidden state,
 ids and routing weights must equal, bit for bit, both the three-kernel path's
-for the whole batch and the one-token launch's for that token alone; the
+for the whole batch and the bit-compatible one-token launch's
+(roaster_decode_fused_layer(2)) for that token alone; the
 oracle bars of the decode tests (ids exact, max|d|/max|ffn| <= 2e-3 and the
 1e-4 regression bound) are held as well.  Cases: 8 tokens (8 token slots), 3
 and 5 tokens (4 and 8 slots, some unused), 2, 4 and 6 tokens; the 256-expert
@@ -25,7 +26,7 @@ import pytest
 import roaster_amd as R
 from gpu_util import Dev, SynthTable, log, rel_err
 from test_gpu_decode import oracle_stack, decode
-from test_gpu_decode_layer1 import _stack, _both, _same
+from test_gpu_decode_layer1 import _stack, _both, _same, _in_mode
 
 pytestmark = pytest.mark.gpu
 
@@ -43,7 +44,8 @@ def test_stackB_matches_three_kernels_one_token_and_oracle(shape):
         _same(a, b)
         h, ids, w = a
         for tok in range(B):
-            h1, ids1, w1 = _stack(t, h0[tok:tok + 1], NL, nw)
+            # the one-token launch with the three-kernel path's arithmetic
+            h1, ids1, w1 = _in_mode(2, lambda: _stack(t, h0[tok:tok + 1], NL, nw))
             _same((h[tok:tok + 1], ids[:, tok:tok + 1], w[:, tok:tok + 1]), (h1, ids1, w1))
         h_ref, ids_ref = oracle_stack(t, h0, NL, norm_w=nw)
         assert np.array_equal(ids, ids_ref)

@@ -59,9 +59,29 @@ def test_noalloc_stack_matches_allocating_entry_twice():
         t.destroy()
 
 
+def test_noalloc_one_token_after_eight():
+    """A call of 8 tokens (three kernels per layer, their intermediates over
+    the bytes where the one-token launch keeps its exchange slots), then one
+    token (the one-launch kernel on those slots), then 8 again and one again:
+    each equal to the allocating entry bit for bit."""
+    L = R.lib()
+    R.check(L.roaster_init(), "init")
+    t = SynthTable(3, n_layers=4)
+    try:
+        for B, NL in ((8, 2), (1, 4), (8, 1), (1, 3)):
+            log(f"noalloc call B={B} layers={NL}")
+            h0 = np.stack([R.synth_normal(4, R.synth_stream(0, b + 10 * NL, 5), 2048) for b in range(B)])
+            got = _run(L.roaster_moe_decode_stack_noalloc, t, h0, B, NL, None)
+            ref = _run(L.roaster_moe_decode_stack, t, h0, B, NL, None)
+            for x, y in zip(got, ref):
+                assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+    finally:
+        t.destroy()
+
+
 def test_noalloc_rejects_sizes_beyond_its_array():
     """inter 2048 at 8 tokens needs 8 x 9 x 2048 x 4 B of SiLU*up rows alone,
-    more than the 512 KiB array: the call is refused before any launch (the
+    more than the 576 KiB array: the call is refused before any launch (the
     table is created but never filled, so no kernel runs in this test)."""
     L = R.lib()
     R.check(L.roaster_init(), "init")
