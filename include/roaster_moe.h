@@ -162,20 +162,34 @@ int roaster_moe_decode_stack(RoasterTable *t, float *h, int B, int layer0, int n
 
 /* Decode runs a call's layers as one launch (router, top-8, experts and
  * combine in 256 workgroups that exchange values through memory) wherever the
- * shapes allow it: a device with at least 256 CUs and experts a multiple of 32
- * up to 256; for one token hidden up to 2048 and inter up to 1024; for 2..8
- * tokens inter 512, hidden 512..2048 in multiples of 256, and gate/up Q4_K and
- * down Q6_K in every layer of the call.  Otherwise each layer runs as three
- * launches.  All give bit-identical results, each token's equal to its
- * one-token result.
- * roaster_decode_fused_layer: 1 = one launch where possible (default), 0 =
- * always three, -1 = query; returns the mode in force. */
+ * shapes allow it: a device with at least 256 CUs on which each one-launch
+ * kernel fits one workgroup per CU, experts a multiple of 32 up to 256; for
+ * one token hidden up to 2048 and inter up to 1024; for 2..8 tokens inter 512,
+ * hidden 512..2048 in multiples of 256, and gate/up Q4_K and down Q6_K in
+ * every layer of the call.  Otherwise each layer runs as three launches.
+ * One token at 256 experts, hidden 2048, inter 512 with gate/up Q4_K and down
+ * Q6_K folds the router into the previous layer's combine: its logits and
+ * 1/rms are sums of per-workgroup partials, equal to the three-kernel path's
+ * up to fp32 summation order, and its ids equal given identical logits.
+ * Every other one-launch case gives results bit-identical to the three-kernel
+ * path, each token's equal to its one-token result.
+ * roaster_decode_fused_layer: 1 = one launch where possible (default), 2 = the
+ * same but one token always with the three-kernel path's arithmetic (no folded
+ * router), 0 = always three, -1 = query; returns the mode in force. */
 int roaster_decode_fused_layer(int enable);
 /* Polls a one-launch layer's wait makes before it gives up (sets error bit 2,
  * reported by roaster_sync as ROASTER_EDEVICE, and the launch ends with
- * unusable outputs); 0 = query.  Default 2^20 (about a second); tests set it
- * tiny to exercise that path. */
+ * unusable outputs; the folded-router kernel leaves a stack call's h as it
+ * was); 0 = query.  Default 2^20 (about a second); tests set it tiny to
+ * exercise that path. */
 unsigned roaster_decode_spin_limit(unsigned polls);
+/* The one-launch kernels' 256 workgroups wait on each other, so they must all
+ * be resident at once.  1: launch them cooperatively, so that the runtime
+ * guarantees it or refuses the launch (ROASTER_EDEVICE) -- for a GPU shared
+ * with other work; it measured 0.5 us per layer slower on an idle MI355X.
+ * 0 (default): ordinary launches, whose waits give up after the spin limit if
+ * other work holds CUs.  -1 = query; returns the mode in force. */
+int roaster_decode_cooperative_launch(int enable);
 
 /* No counterpart in the reference: roaster_moe_decode_stack for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving

@@ -104,7 +104,10 @@ struct DecArgs {
 #define XCH_LEHS(I) ((size_t)256)
 #define XCH_LEHX(I) ((size_t)256 + (size_t)(I))
 #define XCH_LH(I) ((size_t)256 + 2 * (size_t)(I))
-#define XCH_U64(E, H, I) (XCH_LOC0(E, H, I) + 8 * XCH_LOCN(E, H, I))
+/* then the staged final hidden state [H] (a stack call's h is written only
+ * when no wait gave up) */
+#define XCH_HST(E, H, I) (XCH_LOC0(E, H, I) + 8 * XCH_LOCN(E, H, I))
+#define XCH_U64(E, H, I) (XCH_HST(E, H, I) + (size_t)(H))
 
 /* The same regions for the batched one-launch stack (2..8 tokens, sized for
  * NB >= B tokens), each with a token index outermost: logits [NB][256][16],
@@ -122,7 +125,8 @@ struct DecArgs {
 #define XCHB_LEHS(NB, I) ((size_t)(NB) * 256)
 #define XCHB_LEHX(NB, I) ((size_t)(NB) * ((size_t)256 + (size_t)(I)))
 #define XCHB_LH(NB, I) ((size_t)(NB) * ((size_t)256 + 2 * (size_t)(I)))
-#define XCHB_U64(NB, E, H, I) (XCHB_LOC0(NB, E, H, I) + 8 * XCHB_LOCN(NB, E, H, I))
+#define XCHB_HST(NB, E, H, I) (XCHB_LOC0(NB, E, H, I) + 8 * XCHB_LOCN(NB, E, H, I))   /* staged h [NB][H] */
+#define XCHB_U64(NB, E, H, I) (XCHB_HST(NB, E, H, I) + (size_t)(NB) * (H))
 #define K1B_MAXB 8                                  /* tokens of the batched one-launch stack */
 
 /* Regions of the one-token stack whose router is folded into the combine

@@ -1366,6 +1366,40 @@ __device__ __forceinline__ DecLayer k1_layer(const DecLayer *Ls, int i)
     return L;
 }
 
+/* End of a one-launch stack kernel.  A stack call (A.y NULL) stages its final
+ * hidden state, nh epoch-tagged values at hst written by other workgroups,
+ * instead of writing the caller's h.  Every workgroup reports a wait that gave
+ * up (error bit 2) and then counts itself done on A.cnt (the report ordered
+ * before the count by thread 0's fence); the last of the K1_NWG, which then
+ * sees every report, copies the staged state over A.h only when none gave up:
+ * it first waits (bounded, like every exchange) until each staged value
+ * carries the layer's epoch, then writes them all, so a call that failed
+ * leaves h as it was.  The count stays a multiple of K1_NWG between launches.
+ * Called by every thread; dead_any workgroup-uniform; s_last is LDS. */
+__device__ __forceinline__ void k1_finish(const DecArgs &A, bool dead_any, int *s_last, const uint64_t *hst, int nh,
+                                          uint32_t epl)
+{
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (dead_any) atomicOr(A.err, 2);
+        __threadfence();
+        const uint32_t old = __hip_atomic_fetch_add(A.cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = (old + 1u) % (uint32_t)K1_NWG == 0u;
+        *s_last = last && !A.y && !(__hip_atomic_load(A.err, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) & 2) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!*s_last) return;                                     /* workgroup-uniform */
+    int dead = 0;
+    for (int r = threadIdx.x; r < nh; r += blockDim.x) (void)xch_get(hst + r, epl, dead, A.spin);
+    if (dead) *s_last = 2;
+    __syncthreads();
+    if (*s_last == 2) {
+        if (threadIdx.x == 0) atomicOr(A.err, 2);
+        return;
+    }
+    for (int r = threadIdx.x; r < nh; r += blockDim.x) A.h[r] = __builtin_bit_cast(float, (uint32_t)xch_load(hst + r));
+}
+
 template <int NPG, int ND, int TY>
 __device__ __forceinline__ void stack1_body(const DecArgs &A)
 {
@@ -1718,13 +1752,16 @@ __device__ __forceinline__ void stack1_body(const DecArgs &A)
                 if (!last) xch_put_xcd(lh + (size_t)(row & 3) * (H / 4) + (row >> 2), hn, ep, l2);
                 else if (grp == 0) {
                     if (A.y) A.y[row] = y;
-                    else A.h[row] = hn;
+                    else xch_put(A.xch + XCH_HST(E, H, I) + row, hn, ep);
                 }
             }
         }
         K1_TS(9);
     }
-    if (tid == 0 && (dead || s_dead)) atomicOr(A.err, 2);
+    __shared__ int s_last;
+    if (dead) s_dead = 1;
+    __syncthreads();
+    k1_finish(A, s_dead != 0, &s_last, A.xch + XCH_HST(E, H, I), H, A.epoch + (uint32_t)(n - 1));
 #ifdef ROASTER_PHASE_TS
     if (threadIdx.x == 0 || threadIdx.x == 64 || threadIdx.x == 192)
         for (int k = 0; k < 2; k++)
@@ -1932,7 +1969,6 @@ extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stack1r_kernel(DecArgs
     uint64_t *xdx = A.xch + XR_DX(E, H, I);
     uint64_t *xdsh = A.xch + XR_DSH(E, H, I);
     uint64_t *xhst = A.xch + XR_HST(E, H, I);
-    uint32_t *xcnt = A.cnt;
     uint64_t *loc = A.xch + XR_LOC0(E, H, I) + (size_t)grp * XR_LOCN(E, H, I);   /* this XCD's */
     uint64_t *llg = loc + XR_LLG(I), *lss = loc + XR_LSS(I), *lehs = loc + XR_LEHS(I), *lehx = loc + XR_LEHX(I),
              *lh = loc + XR_LH(I);
@@ -2252,30 +2288,10 @@ extern "C" __global__ void __launch_bounds__(K1_T, 1) dec_stack1r_kernel(DecArgs
             }
         }
     }
-    /* every workgroup counts itself done after reporting a wait that gave up;
-     * the last one copies the staged h over the caller's when none did */
+    /* the staged h over the caller's only when no wait gave up anywhere */
     if (dead) s_dead = 1;
     __syncthreads();
-    if (tid == 0) {
-        if (s_dead) atomicOr(A.err, 2);
-        __threadfence();
-        const uint32_t old = __hip_atomic_fetch_add(xcnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (old + 1u) % (uint32_t)K1_NWG == 0u;
-    }
-    __syncthreads();
-    if (s_last && stage) {
-        const int ef = __hip_atomic_load(A.err, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-        if (!(ef & 2)) {
-            const uint32_t epl = A.epoch + (uint32_t)(n - 1);
-#pragma unroll
-            for (int k = 0; k < H / K1_T; k++) {
-                const int r = tid + k * K1_T;
-                const uint64_t v = xch_load(xhst + r);
-                if ((uint32_t)(v >> 32) == epl) A.h[r] = __builtin_bit_cast(float, (uint32_t)v);
-                else atomicOr(A.err, 2);
-            }
-        }
-    }
+    k1_finish(A, s_dead != 0, &s_last, xhst, H, A.epoch + (uint32_t)(n - 1));
 #ifdef ROASTER_PHASE_TS
     if (threadIdx.x == 0 || threadIdx.x == 192 || threadIdx.x == 384)
         for (int k = 0; k < 2; k++)
@@ -2778,7 +2794,7 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
                 if (!last) xch_put_xcd(lh + (size_t)b * H + (size_t)(row & 3) * HU + (row >> 2), hn, ep, l2);
                 else if (grp == 0) {
                     if (A.y) A.y[(size_t)b * H + row] = y;
-                    else A.h[(size_t)b * H + row] = hn;
+                    else xch_put(A.xch + XCHB_HST(NB, E, H, I) + (size_t)b * H + row, hn, ep);
                 }
             }
         }
@@ -2786,7 +2802,10 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
     }
     /* a wait that gave up after the layer's last barrier is known only to
      * its own thread: every such thread reports it */
-    if (dead || (tid == 0 && s_dead)) atomicOr(A.err, 2);
+    __shared__ int s_last;
+    if (dead) s_dead = 1;
+    __syncthreads();
+    k1_finish(A, s_dead != 0, &s_last, A.xch + XCHB_HST(NB, E, H, I), B * H, A.epoch + (uint32_t)(n - 1));
 #ifdef ROASTER_PHASE_TS
     if (threadIdx.x == 0 || threadIdx.x == 64 || threadIdx.x == 448)
         for (int k = 0; k < 2; k++)
@@ -2846,6 +2865,54 @@ static int launch_layer(const DecArgs &A0, int l, bool with_router)
 }
 
 static int g_layer1 = 1;            /* roaster_decode_fused_layer */
+static int g_coop = 0;              /* roaster_decode_cooperative_launch */
+
+extern "C" int roaster_decode_cooperative_launch(int enable)
+{
+    std::lock_guard<std::recursive_mutex> g(rt_lock());
+    if (enable == 0 || enable == 1) g_coop = enable;
+    return g_coop;
+}
+
+/* Whether every one-launch stack kernel fits one workgroup per CU on at least
+ * K1_NWG CUs (registers and LDS as compiled), checked once per process: else
+ * their grids could never be resident at once and the three-kernel path runs. */
+static int g_k1_fits = -1;
+
+static bool k1_fits()
+{
+    if (g_k1_fits >= 0) return g_k1_fits == 1;
+    const void *fns[] = {(const void *)dec_stack1_kernel, (const void *)dec_stack1_2x2_kernel,
+                         (const void *)dec_stack1r_kernel, (const void *)dec_stackB2_kernel,
+                         (const void *)dec_stackB4_kernel, (const void *)dec_stackB8_kernel};
+    bool ok = rt().n_cu >= K1_NWG;
+    for (const void *f : fns) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, K1_T, 0) != hipSuccess) {
+            (void)hipGetLastError();
+            nb = 0;
+        }
+        ok = ok && nb >= 1;
+    }
+    g_k1_fits = ok ? 1 : 0;
+    return ok;
+}
+
+/* A one-launch stack kernel on the library stream.  Its 256 workgroups wait
+ * on each other, so all of them must be resident at once: a cooperative
+ * launch makes the runtime guarantee that (or refuse the launch, reported as
+ * ROASTER_EDEVICE) instead of leaving the waits to give up when other work
+ * holds some of the CUs. */
+static int launch_k1(const void *fn, DecArgs &A)
+{
+    if (g_coop) {
+        void *args[] = {&A};
+        return rt_check(hipLaunchCooperativeKernel(fn, dim3(K1_NWG), dim3(K1_T), args, 0, rt().stream),
+                        "stack launch (cooperative)") ? ROASTER_EDEVICE : 0;
+    }
+    hipLaunchKernel(fn, dim3(K1_NWG), dim3(K1_T), (void **)(void *[]){&A}, 0, rt().stream);
+    return rt_check(hipGetLastError(), "stack launch") ? ROASTER_EDEVICE : 0;
+}
 static uint32_t g_spin = K1_SPIN;   /* roaster_decode_spin_limit */
 
 extern "C" unsigned roaster_decode_spin_limit(unsigned polls)
@@ -2873,7 +2940,7 @@ size_t dec_xch_need1(int E, int H, int I)
 
 bool dec_layer1_ok(int E, int H, int I, int B)
 {
-    return g_layer1 && B == 1 && rt().n_cu >= K1_NWG && E >= RTOPK && E <= 256 && E % K1_GW == 0 && H % RQK == 0 &&
+    return g_layer1 && B == 1 && k1_fits() && E >= RTOPK && E <= 256 && E % K1_GW == 0 && H % RQK == 0 &&
            H <= K1_MAXH && I % RQK == 0 && I <= K1_MAXI;
 }
 
@@ -2882,7 +2949,7 @@ bool dec_layer1_ok(int E, int H, int I, int B)
  * experts (one logit per lane of a wave's 64 for 8 tokens). */
 bool dec_layerB_ok(int E, int H, int I, int B)
 {
-    return g_layer1 && B >= 2 && B <= K1B_MAXB && rt().n_cu >= K1_NWG && E >= RTOPK && E <= 256 && E % K1_GW == 0 &&
+    return g_layer1 && B >= 2 && B <= K1B_MAXB && k1_fits() && E >= RTOPK && E <= 256 && E % K1_GW == 0 &&
            I == 512 && H % 256 == 0 && H >= 512 && H <= K1_MAXH;
 }
 
@@ -2982,11 +3049,11 @@ static int launch_stack1(DecArgs &A0)
             const DecLayer *Lh = A.layers_h + l;
             ty = !Lh->q6[0] && !Lh->q6[1] && Lh->q6[2] && !Lh->sq6[0] && !Lh->sq6[1] && Lh->sq6[2];
         }
-        if (ty && A.cnt && dec_r1_shape(A.E, A.H, A.I) && X.n >= (size_t)XR_U64(A.E, A.H, A.I))
-            hipLaunchKernelGGL(dec_stack1r_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
-        else if (npg == 2 && nd == 2 && ty) hipLaunchKernelGGL(dec_stack1_2x2_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
-        else hipLaunchKernelGGL(dec_stack1_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
-        if (rt_check(hipGetLastError(), "stack launch")) return ROASTER_EDEVICE;
+        const void *fn = ty && A.cnt && dec_r1_shape(A.E, A.H, A.I) && X.n >= (size_t)XR_U64(A.E, A.H, A.I)
+                             ? (const void *)dec_stack1r_kernel
+                         : npg == 2 && nd == 2 && ty ? (const void *)dec_stack1_2x2_kernel
+                                                     : (const void *)dec_stack1_kernel;
+        if (int rc = launch_k1(fn, A)) return rc;
     }
     return 0;
 }
@@ -3022,10 +3089,9 @@ static int launch_stackB(DecArgs &A0)
         X.epoch += (uint32_t)cn;
         A.spin = g_spin;
         A.xl2 = g_xl2 == 1;
-        if (A.B <= 2) hipLaunchKernelGGL(dec_stackB2_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
-        else if (A.B <= 4) hipLaunchKernelGGL(dec_stackB4_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
-        else hipLaunchKernelGGL(dec_stackB8_kernel, dim3(K1_NWG), dim3(K1_T), 0, rt().stream, A);
-        if (rt_check(hipGetLastError(), "stack launch")) return ROASTER_EDEVICE;
+        const void *fn = A.B <= 2 ? (const void *)dec_stackB2_kernel
+                         : A.B <= 4 ? (const void *)dec_stackB4_kernel : (const void *)dec_stackB8_kernel;
+        if (int rc = launch_k1(fn, A)) return rc;
     }
     return 0;
 }
@@ -3039,6 +3105,11 @@ int dec_launch(DecArgs &A)
         A.plan_g = (DecPlan *)rt_scratch(SCR_C, sizeof(DecPlan));
         if (!ctrl || !A.plan_g) return ROASTER_ENOMEM;
         A.err = (int *)(ctrl + 16);
+        A.cnt = ctrl + 32;
+    }
+    if (!A.cnt) {                       /* the one-launch kernels' completion counter */
+        unsigned *ctrl = rt_ctrl();
+        if (!ctrl) return ROASTER_ENOMEM;
         A.cnt = ctrl + 32;
     }
     if (A.xbuf && !A.ffn_out && dec_layer1_ok(A.E, A.H, A.I, A.B)) return launch_stack1(A);

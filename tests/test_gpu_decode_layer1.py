@@ -18,7 +18,8 @@ layouts and task counts); per-layer matrix types (Q6_K gate/up, Q4_K down);
 given logits with ties; fewer than 8 routable experts; a wait that gives up
 (spin limit forced to 1 poll from the host, so every kernel still ends)
 reported as ROASTER_EDEVICE, then normal results again, and a stack call
-that gives up leaving the caller's h as it was."""
+that gives up leaving the caller's h as it was (every one-launch kernel);
+cooperative launches giving the same results.""" 
 import ctypes as C
 
 import numpy as np
@@ -198,22 +199,24 @@ def test_layer1_wait_gives_up_and_recovers(cfg2):
     _same(decode(cfg2, x, 1), ref)
 
 
-@pytest.mark.parametrize("mode", [1, 2])
-def test_layer1_stack_gives_up_leaves_h(mode):
-    """A 4-layer stack call whose waits give up (spin limit of one poll):
-    ROASTER_EDEVICE, and with the folded-router kernel (mode 1) the caller's h
-    is left as it was (its final state is staged and copied only when no wait
-    anywhere gave up), so the call can be run again from the same input."""
+@pytest.mark.parametrize("mode,B", [(1, 1), (2, 1), (1, 3), (1, 8)])
+def test_stack_gives_up_leaves_h(mode, B):
+    """A 4-layer stack call whose waits give up (spin limit of one poll) in
+    each one-launch kernel (one token folded-router and bit-compatible, 3 and
+    8 tokens batched): ROASTER_EDEVICE, and the caller's h is left as it was
+    (the final state is staged and copied only when no wait anywhere gave
+    up), so the call can be run again from the same input; with the default
+    limit restored the next call is exact again."""
     L = R.lib()
     t = SynthTable(3, n_layers=4)
     try:
-        h0 = R.synth_normal(3, R.synth_stream(0, 0, 5), 2048)[None, :]
+        h0 = np.stack([R.synth_normal(3, R.synth_stream(0, b, 5), 2048) for b in range(B)])
         ref = _in_mode(mode, lambda: _stack(t, h0, 4))
         old = L.roaster_decode_spin_limit(0)
         L.roaster_decode_spin_limit(1)
         try:
             dh = Dev(h0)
-            _in_mode(mode, lambda: R.check(L.roaster_moe_decode_stack(t.t, dh.p, 1, 0, 4, None, EPS, None, None)))
+            _in_mode(mode, lambda: R.check(L.roaster_moe_decode_stack(t.t, dh.p, B, 0, 4, None, EPS, None, None)))
             rc = L.roaster_sync()
         finally:
             L.roaster_decode_spin_limit(old)
@@ -221,9 +224,29 @@ def test_layer1_stack_gives_up_leaves_h(mode):
             pytest.skip("every slot was already published at the first poll (no wait gave up)")
         assert rc == R.EDEVICE and "timed out" in R.last_error()
         assert L.roaster_sync() == 0
-        if mode == 1:
-            assert np.array_equal(dh.get().view(np.uint32), h0.view(np.uint32))
+        assert np.array_equal(dh.get().view(np.uint32), h0.view(np.uint32))
         _same(_in_mode(mode, lambda: _stack(t, h0, 4)), ref)
+    finally:
+        t.destroy()
+
+
+def test_cooperative_launch_same_results():
+    """roaster_decode_cooperative_launch(1): the one-launch kernels (one token
+    and 4 tokens) launched cooperatively give the results of ordinary launches
+    bit for bit."""
+    L = R.lib()
+    t = SynthTable(3, n_layers=4)
+    try:
+        for B in (1, 4):
+            h0 = np.stack([R.synth_normal(3, R.synth_stream(0, b, 5), 2048) for b in range(B)])
+            ref = _stack(t, h0, 4)
+            assert L.roaster_decode_cooperative_launch(-1) == 0
+            L.roaster_decode_cooperative_launch(1)
+            try:
+                got = _stack(t, h0, 4)
+            finally:
+                L.roaster_decode_cooperative_launch(0)
+            _same(got, ref)
     finally:
         t.destroy()
 
