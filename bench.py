@@ -34,10 +34,17 @@ import os
 import sys
 import time
 
+# The prefill CPU baselines run the reference's OpenMP kernels: threads bound
+# close to each other, one per physical core (BASELINE's method).  Set before
+# torch or any OpenMP runtime loads, since the runtime reads them once.
+os.environ.setdefault("OMP_PROC_BIND", "close")
+os.environ.setdefault("OMP_PLACES", "cores")
+
 import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
+TRAFFIC_SOURCE = "profiles/traffic_per_step.md (rocprofv3 FETCH_SIZE / WRITE_SIZE passes, copy-calibrated)"
 
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0          # dense fp16 / bf16
@@ -120,6 +127,40 @@ def omp_threads():
         return int(C.CDLL("libgomp.so.1").omp_get_max_threads())
     except OSError:
         return int(os.environ.get("OMP_NUM_THREADS", "1"))
+
+
+def socket_cores():
+    """Physical cores of one socket among the CPUs this process may run on
+    (the socket with the most of them): the prefill CPU baseline's thread
+    count."""
+    try:
+        cpus = sorted(os.sched_getaffinity(0))
+    except AttributeError:
+        cpus = list(range(os.cpu_count() or 1))
+    per_pkg = {}
+    for c in cpus:
+        base = "/sys/devices/system/cpu/cpu%d/topology/" % c
+        try:
+            with open(base + "physical_package_id") as f:
+                pkg = int(f.read())
+            with open(base + "core_id") as f:
+                core = int(f.read())
+        except (OSError, ValueError):
+            pkg, core = 0, c
+        per_pkg.setdefault(pkg, set()).add(core)
+    return max(len(v) for v in per_pkg.values()) if per_pkg else 1
+
+
+def set_omp_threads(n):
+    """The reference kernels' OpenMP team size (omp_set_num_threads on the
+    loaded runtime, before its parallel regions run); returns the team size in
+    force."""
+    try:
+        g = C.CDLL("libgomp.so.1")
+        g.omp_set_num_threads(int(n))
+        return int(g.omp_get_max_threads())
+    except OSError:
+        return omp_threads()
 
 
 def host_cpu():
@@ -254,6 +295,7 @@ def cpu_baseline_prefill(table, desc, seed, X, ids, layer=0, with_router=True, r
     Ds = np.empty((T, H), np.float32)
     lg = np.empty(E, np.float32)
     X = np.ascontiguousarray(X, np.float32)
+    threads = set_omp_threads(socket_cores())
     best = None
     for _ in range(reps):
         t0 = time.perf_counter()
@@ -264,9 +306,12 @@ def cpu_baseline_prefill(table, desc, seed, X, ids, layer=0, with_router=True, r
         Rf.ref_moe_cpu(C.cast(exs, C.c_void_p), len(groups), Xg.ctypes.data, Dg.ctypes.data, I, H)
         dt = time.perf_counter() - t0
         best = dt if best is None else min(best, dt)
-    out = {"value": round(T / best, 1), "unit": "tokens/s", "cores": omp_threads(), "kind": "reference",
+    out = {"value": round(T / best, 1), "unit": "tokens/s", "cores": threads, "kind": "reference",
            "sample": f"one {T}-token {label} layer ({'router + ' if with_router else ''}{len(groups)} expert groups "
-                     f"+ shared expert via the reference moe_cpu), best of {reps}: {best:.3f} s"}
+                     f"+ shared expert via the reference moe_cpu), best of {reps}: {best:.3f} s",
+           "threads": f"{threads} OpenMP threads = physical cores of one socket among the "
+                      f"{len(os.sched_getaffinity(0))} CPUs this process may use; OMP_PROC_BIND="
+                      f"{os.environ.get('OMP_PROC_BIND')}, OMP_PLACES={os.environ.get('OMP_PLACES')}"}
     out.update(host_cpu())
     return out
 
@@ -301,7 +346,14 @@ def prefill_legs(torch, L, R, dev, stream, reps, with_cpu, parts=("q6", "zipf", 
     if "q6" in parts:
         out = prefill_q6_leg(torch, L, R, dev, stream, reps, with_cpu)
     if "zipf" in parts:
-        out["zipf_512x1"] = prefill_zipf_leg(torch, L, R, dev, stream, reps, with_cpu, "api" in parts)
+        z = prefill_zipf_leg(torch, L, R, dev, stream, reps, with_cpu, "api" in parts)
+        out["zipf_512x1"] = z
+        # scalar copies of the Zipf layer's figures
+        out["zipf_tokens_per_s"] = z["tokens_per_s"]
+        out["zipf_roofline_frac"] = z["roofline"]["frac"]
+        out["zipf_traffic_bytes"] = z["roofline"]["traffic"]
+        if "cpu_baseline" in z:
+            out["zipf_cpu_baseline_tok_s"] = z["cpu_baseline"]["value"]
     return out
 
 
@@ -357,11 +409,18 @@ def prefill_q6_leg(torch, L, R, dev, stream, reps, with_cpu):
                          "algorithmic_bytes_per_layer": int(nbytes // NL), "arithmetic_intensity": round(ai, 1),
                          "frac_of_min_peak_ai_bw": round(tf / min(MFMA_PEAK_TFLOPS, ai * HBM_PEAK_GBS / 1000), 4)},
             "hbm_GBps_algorithmic": round(gbs, 1)}
+        # scalar copies (a parser keeping only scalar fields keeps these)
+        out["roofline_frac"] = out["roofline"]["frac"]
+        out["achieved_TFLOPs"] = out["roofline"]["achieved"]
+        out["frac_of_min_peak_ai_bw"] = out["roofline"]["frac_of_min_peak_ai_bw"]
+        out["traffic_bytes_per_layer"] = out["roofline"]["traffic"]
         if with_cpu:
             cb = cpu_baseline_prefill(t, desc, seed, Xh5, ids0.cpu().numpy(), layer=0, with_router=False,
                                       label="all-Q6_K (logits given)")
             if cb:
                 out["cpu_baseline"] = cb
+                out["cpu_baseline_tok_s"] = cb["value"]
+                out["cpu_threads"] = cb["cores"]
     finally:
         L.roaster_table_destroy(t)
     return out
@@ -509,7 +568,8 @@ def config1_leg(torch, L, R, dev, stream, with_cpu):
     out = {"workload": "Q4_K [512 x 2048] matvec, seed 0", "algorithmic_bytes": int(nbytes),
            "us_per_call_cache_resident": round(hot_ms * 1e3, 3), "us_per_call_rotating_512_copies": round(rot_ms * 1e3, 3),
            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("config1_matvec"),
+                        "traffic_source": TRAFFIC_SOURCE,
                         "kernel": "dense_mv_kernel (one launch per matvec, 512 rotated copies)"},
            "streaming_512_copies_one_launch": {"us": round(one_ms * 1e3, 1), "GBps": round(gbs_one, 1),
                                                "frac_hbm_peak": round(gbs_one / HBM_PEAK_GBS, 4)}}
@@ -561,9 +621,17 @@ def config2_leg(torch, L, R, dev, stream, with_cpu):
             run()
             R.check(L.roaster_sync(), "config2")
             lat.append(time.perf_counter() - t0)
+        nbytes = ROUTER_BYTES + 9 * EXPERT_BYTES
+        gbs = nbytes / (dev_ms * 1e-3) / 1e9
         out = {"workload": "one decode MoE block, 1 token, hidden 2048, 256 experts top-8 + shared, seed 1",
                "us_per_block_device": round(dev_ms * 1e3, 2), "us_per_block_isolated_median": round(
-                   float(np.median(lat)) * 1e6, 1), "algorithmic_bytes": ROUTER_BYTES + 9 * EXPERT_BYTES}
+                   float(np.median(lat)) * 1e6, 1), "algorithmic_bytes": nbytes,
+               "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("config2_block"),
+                            "traffic_source": TRAFFIC_SOURCE,
+                            "kernel": L.roaster_decode_stack_kernel(t, 1, 0, 1).decode() + " (one launch per block)",
+                            "note": "the block's 20.5 MB stay in the 256 MB Infinity Cache between calls: "
+                                    "a latency figure, not an HBM rate"}}
         if with_cpu:
             out["cpu_baseline"] = cpu_baseline_decode(seed, 200, t, n_layers=1, x_stream=0)
     finally:
@@ -666,11 +734,8 @@ def decode_legs(args, torch, L, R, dev, stream):
                    "gate_up": "Q4_K", "down": "Q6_K", "resident_table_bytes": int(L.roaster_table_bytes(t))},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("decode_b%d_step" % B),
-                     "kernel": "decode stack: %s" % (("dec_stack1_kernel, one launch for all 40 layers" if B == 1 else
-                                                      "dec_stackB%d_kernel, one launch for all 40 layers"
-                                                      % (2 if B <= 2 else 4 if B <= 4 else 8))
-                                                     if L.roaster_decode_fused_layer(-1)
-                                                     else "router, gate/up and down kernels per layer"),
+                     "traffic_source": TRAFFIC_SOURCE,
+                     "kernel": "decode stack: %s" % L.roaster_decode_stack_kernel(t, B, 0, N_LAYERS).decode(),
                      "kernel_ms": round(kern_ms, 5), "algorithmic_bytes_per_launch": int(nbytes)},
     }
     if B == 1:
@@ -683,7 +748,7 @@ def decode_legs(args, torch, L, R, dev, stream):
             line["batch%d" % nb] = {"tokens_per_s": round(nb / (msb * 1e-3), 1), "ms_per_step": round(msb, 4),
                                     "hbm_GBps": round(bb / (msb * 1e-3) / 1e9, 1),
                                     "frac_hbm_peak": round(bb / (msb * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                    "kernel": "dec_stackB%d_kernel" % nb}
+                                    "kernel": L.roaster_decode_stack_kernel(t, nb, 0, N_LAYERS).decode()}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(seed, args.cpu_tokens, t)
     L.roaster_table_destroy(t)

@@ -190,6 +190,9 @@ unsigned roaster_decode_spin_limit(unsigned polls);
  * 0 (default): ordinary launches, whose waits give up after the spin limit if
  * other work holds CUs.  -1 = query; returns the mode in force. */
 int roaster_decode_cooperative_launch(int enable);
+/* The kernel(s) roaster_moe_decode_stack(t, ., B, layer0, n_layers, ...) would
+ * launch in the current modes, as a static string ("" for bad arguments). */
+const char *roaster_decode_stack_kernel(RoasterTable *t, int B, int layer0, int n_layers);
 
 /* No counterpart in the reference: roaster_moe_decode_stack for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving

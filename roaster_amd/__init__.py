@@ -136,6 +136,7 @@ _SIG = {
     "roaster_decode_fused_layer": (C.c_int, [C.c_int]),
     "roaster_decode_spin_limit": (C.c_uint, [C.c_uint]),
     "roaster_decode_cooperative_launch": (C.c_int, [C.c_int]),
+    "roaster_decode_stack_kernel": (C.c_char_p, [_P, C.c_int, C.c_int, C.c_int]),
     "roaster_dense_mfma_min_tokens": (C.c_int, [C.c_int]),
     "roaster_moe_prefill": (C.c_int, [_P, C.c_int, _P, C.c_int, _P, C.POINTER(RoasterPrefillOpts)]),
     "roaster_prefill_balanced_down": (C.c_int, [C.c_int]),

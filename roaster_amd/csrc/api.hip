@@ -545,6 +545,19 @@ extern "C" int roaster_moe_decode_stack(RoasterTable *t, float *h, int B, int la
     return dec_launch(A);
 }
 
+extern "C" const char *roaster_decode_stack_kernel(RoasterTable *t, int B, int layer0, int n_layers)
+{
+    Guard g(rt_lock());
+    if (rt_init_locked()) return "";
+    if (!t || B < 1 || B > RMAX_B || layer0 < 0 || n_layers < 1 || layer0 + n_layers > t->d.n_layers) return "";
+    DecArgs A;
+    fill_table_args(A, t);
+    A.layer0 = layer0;
+    A.nlayers = n_layers;
+    A.B = B;
+    return dec_kernel_names(A);
+}
+
 /* ---- the layer stack without allocation -------------------------------------
  * roaster_moe_decode_stack_noalloc runs the kernels of roaster_moe_decode_stack
  * with every intermediate (error word, plan, logits, shared-gate logits,

@@ -168,6 +168,8 @@ int dec_ffn_launch(DecArgs &A);      /* kernel_ffn_fused: gate/up + down kernels
 /* Whether one token's layers can run as one launch (dec_stack1_kernel) for
  * these shapes on this device. */
 bool dec_layer1_ok(int E, int H, int I, int B);
+/* The kernels a decode call of A would launch (a static string). */
+const char *dec_kernel_names(const DecArgs &A);
 /* The exchange slots a one-token launch of these shapes uses (0: none). */
 size_t dec_xch_need1(int E, int H, int I);
 /* Whether B = 2..8 tokens' layers can run as one launch (dec_stackB_kernel)

@@ -3019,6 +3019,22 @@ int dec_probe_placement()
 
 void dec_placement_failed() { g_xl2 = 0; }
 
+/* Which one-token kernel runs layers [c0, c0 + cn) of A on an exchange
+ * buffer of xn slots: 0 dec_stack1r_kernel, 1 dec_stack1_2x2_kernel, 2
+ * dec_stack1_kernel. */
+static int stack1_choice(const DecArgs &A, int c0, int cn, size_t xn)
+{
+    const int nbi = A.I / RQK, rpw = 64 / lanes_per_row(nbi);
+    const int npg = (A.I / K1_GW + K1_W - 1) / K1_W, nd = ((A.H / K1_GW + rpw - 1) / rpw + K1_W - 1) / K1_W;
+    bool ty = A.layers_h != nullptr;
+    for (int l = c0; ty && l < c0 + cn; l++) {
+        const DecLayer *Lh = A.layers_h + l;
+        ty = !Lh->q6[0] && !Lh->q6[1] && Lh->q6[2] && !Lh->sq6[0] && !Lh->sq6[1] && Lh->sq6[2];
+    }
+    if (ty && A.cnt && dec_r1_shape(A.E, A.H, A.I) && xn >= (size_t)XR_U64(A.E, A.H, A.I)) return 0;
+    return npg == 2 && nd == 2 && ty ? 1 : 2;
+}
+
 /* One launch per run of up to K1_MAXL layers (dec_stack1_kernel) on the
  * exchange buffer A.xbuf. */
 static int launch_stack1(DecArgs &A0)
@@ -3042,17 +3058,9 @@ static int launch_stack1(DecArgs &A0)
         X.epoch += (uint32_t)cn;
         A.spin = g_spin;
         A.xl2 = g_xl2 == 1;
-        const int nbi = A.I / RQK, rpw = 64 / lanes_per_row(nbi);
-        const int npg = (A.I / K1_GW + K1_W - 1) / K1_W, nd = ((A.H / K1_GW + rpw - 1) / rpw + K1_W - 1) / K1_W;
-        bool ty = A.layers_h != nullptr;
-        for (int l = c0; ty && l < c0 + cn; l++) {
-            const DecLayer *Lh = A.layers_h + l;
-            ty = !Lh->q6[0] && !Lh->q6[1] && Lh->q6[2] && !Lh->sq6[0] && !Lh->sq6[1] && Lh->sq6[2];
-        }
-        const void *fn = ty && A.cnt && dec_r1_shape(A.E, A.H, A.I) && X.n >= (size_t)XR_U64(A.E, A.H, A.I)
-                             ? (const void *)dec_stack1r_kernel
-                         : npg == 2 && nd == 2 && ty ? (const void *)dec_stack1_2x2_kernel
-                                                     : (const void *)dec_stack1_kernel;
+        const int ch = stack1_choice(A, c0, cn, X.n);
+        const void *fn = ch == 0 ? (const void *)dec_stack1r_kernel
+                         : ch == 1 ? (const void *)dec_stack1_2x2_kernel : (const void *)dec_stack1_kernel;
         if (int rc = launch_k1(fn, A)) return rc;
     }
     return 0;
@@ -3094,6 +3102,27 @@ static int launch_stackB(DecArgs &A0)
         if (int rc = launch_k1(fn, A)) return rc;
     }
     return 0;
+}
+
+/* The kernels a decode call of A (table fields, B, layers, y) would launch,
+ * on the library's own exchange buffer. */
+const char *dec_kernel_names(const DecArgs &A)
+{
+    if (dec_layer1_ok(A.E, A.H, A.I, A.B)) {
+        DecArgs C = A;
+        if (!C.cnt) C.cnt = (uint32_t *)&C;               /* only its presence matters here */
+        const int ch = stack1_choice(C, A.layer0, std::min(A.nlayers, K1_MAXL), dec_xch_need1(A.E, A.H, A.I));
+        return ch == 0 ? "dec_stack1r_kernel" : ch == 1 ? "dec_stack1_2x2_kernel" : "dec_stack1_kernel";
+    }
+    bool tyB = A.layers_h != nullptr;
+    for (int l = A.layer0; tyB && l < A.layer0 + A.nlayers; l++) {
+        const DecLayer *Lh = A.layers_h + l;
+        tyB = !Lh->q6[0] && !Lh->q6[1] && Lh->q6[2] && !Lh->sq6[0] && !Lh->sq6[1] && Lh->sq6[2];
+    }
+    if (tyB && dec_layerB_ok(A.E, A.H, A.I, A.B))
+        return A.B <= 2 ? "dec_stackB2_kernel" : A.B <= 4 ? "dec_stackB4_kernel" : "dec_stackB8_kernel";
+    return A.B == 1 ? "dec_router1_kernel + dec_gu1_kernel + dec_down_kernel per layer"
+                    : "dec_router_kernel + dec_gu_kernel + dec_down_kernel per layer";
 }
 
 int dec_launch(DecArgs &A)
