@@ -4,12 +4,17 @@ model.c:1671-1791) against the oracle.
 Bars: top-8 ids bit-exact given identical router logits (the oracle is fed the
 GPU's biased logits); expert counts equal the histogram of the ids; FFN
 outputs within max|d| / max|y| <= 2e-3 in the default fp16-operand mode, and
-<= 2e-4 in the bf16x3 split mode.  At 2048 tokens the oracle is run on a
-sample of tokens only: a token's output depends on its own input and logits
-alone (model.c computes every (token, expert) row independently), which the
-permutation test checks bit for bit on the GPU.
+<= 2e-4 in the bf16x3 split mode.  The all-Q6_K 2048-token case is checked
+on every token of its first layer (the oracle's grouped products run on a
+thread pool, one expert group or 128-token chunk of the shared expert per
+task) and on a token sample of the other three; a token's output depends on
+its own input and logits alone (model.c computes every (token, expert) row
+independently), which the permutation tests check bit for bit on the GPU,
+at T = 300 on the Q4_K / Q6_K table and at T = 2048 on the all-Q6_K one.
 """
 import ctypes as C
+import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
@@ -199,5 +204,76 @@ def test_prefill_all_q6k_2048_tokens_4_layers():
             err = rel_err(Y[sample], Y_ref)
             log(f"all-Q6_K layer {layer}: rows/expert {counts.min()}..{counts.max()}, sample max|d|/max|y| = {err:.3e}")
             assert err <= TOL
+    finally:
+        tab.destroy()
+
+
+def oracle_prefill_all_tokens(tab, layer, X, ids, w):
+    """The oracle's MoE block for every token with the given routing (ids, w
+    [T x 8]: the oracle's select_top8 of the logits, equal to the GPU's ids): the
+    reference's grouped products (orc_moe_groups: per expert its tokens in
+    ascending order, model.c:1713-1771; the shared expert over all tokens,
+    1694-1711) as independent tasks on a thread pool, then the combine in
+    the reference order -- sigmoid(gate_inp . x) times the shared row, then
+    each expert's weighted row in ascending expert id (1707-1711, 1776-1788)."""
+    T, H = X.shape
+    I, E = tab.desc.inter, tab.desc.n_experts
+    X = np.ascontiguousarray(X, np.float32)
+    groups = []
+    for e in range(E):
+        rows = np.nonzero((ids == e).any(axis=1))[0]
+        if len(rows):
+            groups.append((e, rows))
+    shared = tab.expert(layer, E)
+    chunks = [np.arange(a, min(a + 128, T)) for a in range(0, T, 128)]
+    tasks = [(tab.expert(layer, e), rows, tuple(tab.desc.q6)) for e, rows in groups] + \
+            [(shared, rows, tuple(tab.desc.sh_q6)) for rows in chunks]
+
+    def run(task):
+        (g, u, d), rows, q6 = task
+        Xg = np.ascontiguousarray(X[rows])
+        Dg = np.empty((len(rows), H), np.float32)
+        grp = (O.OrcMoeGroup * 1)()
+        grp[0] = O.OrcMoeGroup(g.ctypes.data, u.ctypes.data, d.ctypes.data, q6[0], q6[1], q6[2], len(rows))
+        O.orc().orc_moe_groups(grp, 1, Xg.ctypes.data, Dg.ctypes.data, I, H)
+        return Dg
+
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as pool:
+        outs = list(pool.map(run, tasks))
+    _, gate_inp = tab.router(layer)
+    Y = np.empty((T, H), np.float32)
+    sd = np.concatenate(outs[len(groups):])
+    for t in range(T):
+        raw = O.orc().orc_dot_f32(gate_inp.ctypes.data, X[t].ctypes.data, H)
+        Y[t] = np.float32(1.0 / (1.0 + np.exp(-np.float32(raw)))) * sd[t]
+    for (e, rows), D in zip(groups, outs):
+        k = np.argmax(ids[rows] == e, axis=1)
+        Y[rows] = Y[rows] + w[rows, k][:, None].astype(np.float32) * D
+    return Y
+
+
+def test_prefill_all_q6k_2048_every_token():
+    """The all-Q6_K 2048-token layer (config 5's first layer, seed 4) checked
+    on all 2048 tokens against the oracle's grouped products, and its outputs
+    invariant, bit for bit, under a permutation of the tokens."""
+    T = 2048
+    tab = SynthTable(4, n_layers=1, q6=(1, 1, 1), sh_q6=(1, 1, 1))
+    try:
+        X = tokens(4, T, start=0)
+        lg_in = np.stack([R.synth_normal(4, R.synth_stream(0, t, 7), 256) for t in range(T)])
+        Y, lg, ids, w, counts = prefill(tab, X, layer=0, logits_in=lg_in)
+        check_routing(lg, ids, w, counts, 256)
+        w_ref = np.stack([O.select_top8(np.ascontiguousarray(lg_in[t]))[1] for t in range(T)])
+        Y_ref = oracle_prefill_all_tokens(tab, 0, X, ids, w_ref)
+        err = rel_err(Y, Y_ref)
+        per_tok = np.max(np.abs(Y.astype(np.float64) - Y_ref), axis=1) / np.max(np.abs(Y_ref))
+        log(f"all-Q6_K 2048 tokens, every token: max|d|/max|y| = {err:.3e} "
+            f"(worst token {int(np.argmax(per_tok))}), rows/expert {counts.min()}..{counts.max()}")
+        assert err <= TOL
+        perm = np.random.default_rng(44).permutation(T)
+        Yp, _, idsp, _, _ = prefill(tab, np.ascontiguousarray(X[perm]), layer=0,
+                                    logits_in=np.ascontiguousarray(lg_in[perm]))
+        np.testing.assert_array_equal(idsp, ids[perm])
+        np.testing.assert_array_equal(Yp.view(np.uint32), Y[perm].view(np.uint32))
     finally:
         tab.destroy()
