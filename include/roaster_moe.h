@@ -198,11 +198,13 @@ const char *roaster_decode_stack_kernel(RoasterTable *t, int B, int layer0, int 
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  Same arguments and results (one
  * token: the same one-launch kernel; 2..8 tokens: three launches per layer);
- * every intermediate lives in a fixed 512 KiB device array that the
+ * every intermediate lives in a fixed 576 KiB device array that the
  * library sets up in roaster_init (call it first) and keeps until the process
- * ends, so the call itself makes no allocation.  Calls whose intermediates
- * exceed it -- about 8 tokens x hidden 2048 x inter 1024 or more -- return
- * ROASTER_EINVAL.  Every call on a device shares that device's array and
+ * ends, so the call itself makes no allocation.  Calls whose three-kernel
+ * intermediates exceed it -- about 8 tokens x hidden 2048 x inter 2048 or
+ * more -- return ROASTER_EINVAL before anything runs; one token whose
+ * one-launch exchange slots do not fit beside them runs three kernels per
+ * layer instead (same results).  Every call on a device shares that device's array and
  * leaves its contents behind: calls on the library stream run one after the
  * other, but two processes' or streams' calls that overlapped would race. */
 int roaster_moe_decode_stack_noalloc(RoasterTable *t, float *h, int B, int layer0, int n_layers,

@@ -4,9 +4,27 @@
  * Reference path: model.c:1059-1146 (moe_forward) and kernels.c:1703-1830
  * (kernel_ffn_fused); the layer carry h += MoE(RMSNorm(h)) is model.c:1349-1358.
  *
- * A layer is three kernels on one stream (a kernel boundary is the cheapest
- * device-wide dependency on MI355X, ~2.5 us, well below a cooperative grid
- * barrier across 8 XCDs):
+ * Two ways to run a call's layers:
+ *
+ * One launch for the whole call (a run of up to 64 layers): 256 workgroups,
+ * one per CU, that pass values to each other through exchange slots in
+ * memory (64-bit (epoch, value) words, every wait bounded).  XCD k's 32
+ * workgroups serve routed slot k of every token (the k-th selected expert);
+ * the shared expert and the router are spread over all 256.
+ *   dec_stack1r_kernel   one token, 256 experts / hidden 2048 / inter 512,
+ *                        gate/up Q4_K and down Q6_K: the router folded into
+ *                        the previous layer's combine (partial logits over
+ *                        each workgroup's combined rows, summed across XCDs);
+ *   dec_stack1_kernel,   one token, any other shape the launch takes (2x2:
+ *   dec_stack1_2x2_kernel  two gate/up pairs and two down tasks per wave),
+ *                        with the three-kernel path's arithmetic;
+ *   dec_stackB2/4/8_kernel  2..8 tokens, each token's results equal to its
+ *                        one-token result on the three-kernel arithmetic.
+ * A stack call's final h is staged and copied over the caller's only when no
+ * wait gave up anywhere (k1_finish).
+ *
+ * Three kernels per layer (kernels.h calls, other shapes, or
+ * roaster_decode_fused_layer(0)):
  *   R   RMSNorm of h into LDS (each workgroup, redundantly), router logits
  *       W_r x (f32), the shared-gate logit gate_inp . x and the shared
  *       expert's gate/up rows (they need no routing): eh_shared = silu(g)*u.
@@ -20,13 +38,13 @@
  *       SiLU*up vectors staged in LDS, and combines them in the reference
  *       order y = sum_{k=0..7} w_k d_k + sigmoid(s) d_shared
  *       (model.c:1139-1144).
- * Every wave issues all loads of its task set before consuming any (one
- * memory round trip per dependency instead of one per loop iteration).
  *
  * Weights are read in their native GGML layout: each super-block is read once
  * per call by 8 lanes (16-byte chunks), scales decoded in registers, lane
  * partials reduced with cross-lane shuffles.  A row is at most 8 super-blocks
- * (hidden, inter <= 2048), so one wave pass covers it.
+ * (hidden, inter <= 2048), so one wave pass covers it.  Every wave issues all
+ * loads of its task set before consuming any (one memory round trip per
+ * dependency instead of one per loop iteration).
  */
 #include "internal.h"
 #include "qdot.h"
