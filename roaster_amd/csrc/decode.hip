@@ -1387,23 +1387,37 @@ __device__ __forceinline__ DecLayer k1_layer(const DecLayer *Ls, int i)
 /* End of a one-launch stack kernel.  A stack call (A.y NULL) stages its final
  * hidden state, nh epoch-tagged values at hst written by other workgroups,
  * instead of writing the caller's h.  Every workgroup reports a wait that gave
- * up (error bit 2) and then counts itself done on A.cnt (the report ordered
- * before the count by thread 0's fence); the last of the K1_NWG, which then
+ * up (error bit 2) and then counts itself done on A.cnt (thread 0 waits for the
+ * report to be performed before counting); the last of the K1_NWG, which then
  * sees every report, copies the staged state over A.h only when none gave up:
  * it first waits (bounded, like every exchange) until each staged value
  * carries the layer's epoch, then writes them all, so a call that failed
- * leaves h as it was.  The count stays a multiple of K1_NWG between launches.
- * Called by every thread; dead_any workgroup-uniform; s_last is LDS. */
+ * leaves h as it was.  The count stays a multiple of K1_NWG between launches
+ * (layer-output calls, A.y set, only report).  Called by every thread;
+ * dead_any workgroup-uniform; s_last is LDS. */
 __device__ __forceinline__ void k1_finish(const DecArgs &A, bool dead_any, int *s_last, const uint64_t *hst, int nh,
                                           uint32_t epl)
 {
     __syncthreads();
+    if (A.y) {                           /* layer output written directly: nothing staged, no count */
+        if (threadIdx.x == 0 && dead_any) atomicOr(A.err, 2);
+        return;
+    }
     if (threadIdx.x == 0) {
-        if (dead_any) atomicOr(A.err, 2);
-        __threadfence();
-        const uint32_t old = __hip_atomic_fetch_add(A.cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = (old + 1u) % (uint32_t)K1_NWG == 0u;
-        *s_last = last && !A.y && !(__hip_atomic_load(A.err, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) & 2) ? 1 : 0;
+        /* The report is performed at the device-coherent point before this
+         * workgroup counts itself, so the last to count reads every report.
+         * No release fence: the staged values carry their epoch and are polled
+         * for it, so their stores need no ordering (an agent-scope release
+         * writes back the XCD's whole L2, ~7 us per launch). */
+        if (dead_any) __hip_atomic_fetch_or(A.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const uint32_t old = __hip_atomic_fetch_add(A.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int sl = 0;
+        if ((old + 1u) % (uint32_t)K1_NWG == 0u) {
+            asm volatile("" ::: "memory");
+            sl = (__hip_atomic_load(A.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 2) ? 0 : 1;
+        }
+        *s_last = sl;
     }
     __syncthreads();
     if (!*s_last) return;                                     /* workgroup-uniform */
