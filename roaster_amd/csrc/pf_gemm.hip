@@ -34,6 +34,29 @@
 #include "prefill.h"
 #include "tile.h"
 
+/* Opt-in timing (build with -DROASTER_PF_TS): thread 0 of each of the first
+ * 4096 workgroups of a GEMM launch records the 100 MHz real-time counter at
+ * its entry, after its first barrier, after each K step and at its end, with
+ * its CU / XCD ids; roaster_pf_ts() copies the table out. */
+#ifdef ROASTER_PF_TS
+__device__ unsigned long long g_pf_ts[4096][16];
+extern "C" int roaster_pf_ts(unsigned long long *out)
+{
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_pf_ts), sizeof(g_pf_ts));
+}
+#define PF_TS(i)                                                                              \
+    do {                                                                                      \
+        if (threadIdx.x == 0 && blockIdx.x < 4096) g_pf_ts[blockIdx.x][i] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#define PF_TSV(i, v)                                                                          \
+    do {                                                                                      \
+        if (threadIdx.x == 0 && blockIdx.x < 4096) g_pf_ts[blockIdx.x][i] = (v);              \
+    } while (0)
+#else
+#define PF_TS(i) do { } while (0)
+#define PF_TSV(i, v) do { } while (0)
+#endif
+
 static __device__ __forceinline__ float pf_silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
 /* The exponent s of row_scale(amax): fwd = 2^s, clamped to [-100, 100]. */
 static __device__ __forceinline__ int pf_scale_exp(float amax)
@@ -44,6 +67,11 @@ static __device__ __forceinline__ int pf_scale_exp(float amax)
 /* SiLU(g) * u with the hardware exp and reciprocal (a few ulp in f32; the
  * result is rounded to fp16 for the next GEMM anyway). */
 static __device__ __forceinline__ float pf_silu_mul_fast(float g, float u) { return g * __frcp_rn(1.0f + __expf(-g)) * u; }
+
+/* A workgroup barrier that orders LDS accesses only: every wave's LDS reads
+ * and writes complete, global loads may stay in flight (__syncthreads()
+ * waits for those too). */
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 /* Virtual block id: blocks b < R = ntiles * nblk run; on a grid dispatched
  * round-robin over the 8 XCDs, XCD b % 8 takes the contiguous range of
@@ -502,13 +530,81 @@ __device__ __forceinline__ void v8_mfma(f32x16 (&acc)[MS], const _Float16 *Xs, c
     }
 }
 
+/* Epilogue of a gate/up tile: lane n < 16 holds gate and lane n + 16 up of
+ * column j0 + 16 w + (n & 15).  For the row pair (i, i + 1) one lane swap
+ * (lane ^ 16) gives lanes n < 16 the up value of row i and lanes n >= 16 the
+ * gate value of row i + 1, so all 32 lanes compute act = silu(gate) * up (f32)
+ * for one row each; a 16-lane max gives the row's largest |act| over this
+ * wave's 16 columns (one part), and act is rounded to fp16 scaled by that
+ * part's power of two (row_scale of the part max).  Both are staged in LDS
+ * (the activation buffers are free once every wave's last MFMAs have read
+ * them) and written out as whole rows: the tile's 128 columns of act16 (256
+ * bytes) and its 8 part maxima per row. */
+template <int MS>
+__device__ __forceinline__ void gu_epilogue(const PfGemmArgs &A, const V4Shared &meta, const f32x16 (&acc)[MS], int mlen,
+                                            int j0, uint8_t *lds)
+{
+    const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
+    const bool up = n >= 16;
+    const int npart = A.I / 16;
+    constexpr int AP = V2_GU_J + 8;                          /* fp16 pitch of a staged row */
+    __syncthreads();
+    _Float16 *act_s = (_Float16 *)lds;                       /* [MS * 32][AP] */
+    float *pmx_s = (float *)(lds + (size_t)MS * 32 * AP * 2); /* [MS * 32][8] */
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++) {
+        float fw[8];                                         /* the rows' scales, read together */
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int m = 32 * ms + 8 * (q >> 1) + 4 * h + 2 * (q & 1) + (up ? 1 : 0);
+            fw[q] = meta.fwd[m < mlen ? m : 0];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            const float v0 = acc[ms][i], v1 = acc[ms][i + 1];
+            const float mine = up ? v1 : v0, other = up ? v0 : v1;
+            /* lane ^ 16 (rows 0 <-> 1, 2 <-> 3): a VALU lane swap */
+            const auto sw = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, other),
+                                                             __builtin_bit_cast(uint32_t, other), false, false);
+            const float got = __builtin_bit_cast(float, (uint32_t)(up ? sw[0] : sw[1]));
+            const float gsum = up ? got : mine, usum = up ? mine : got;
+            const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3) + (up ? 1 : 0);
+            float e = 0.0f;
+            if (m < mlen) {
+                const float f = fw[i >> 1];
+                e = pf_silu_mul_fast(gsum * f, usum * f);
+            }
+            float mx = fabsf(e);
+            mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
+            mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
+            mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
+            mx = fmaxf(mx, dpp_f<DPP_MIRROR>(mx));
+            float pinv, pfwd;
+            row_scale(mx, pinv, pfwd);
+            act_s[m * AP + 16 * w + (n & 15)] = (_Float16)(e * pinv);
+            if ((n & 15) == 0) pmx_s[m * 8 + w] = mx;
+        }
+    }
+    __syncthreads();
+    /* rows m < mlen: 16 lanes per row, 16 bytes each */
+    for (int r = t >> 4; r < mlen; r += V2_T / 16) {
+        const int c = t & 15;
+        *(uint4 *)(A.act16 + (size_t)meta.slot[r] * A.I + j0 + 8 * c) = *(const uint4 *)(act_s + r * AP + 8 * c);
+    }
+    for (int r = t >> 1; r < mlen; r += V2_T / 2) {
+        const int c = t & 1;
+        *(float4 *)(A.pmax + (size_t)meta.slot[r] * npart + (j0 >> 4) + 4 * c) = *(const float4 *)(pmx_s + r * 8 + 4 * c);
+    }
+    PF_TS(11);
+}
+
 /* Gate/up tile: lanes n < 16 of wave w take gate row j0 + 16 w + n, lanes
  * n >= 16 the up row of the same column.  QG == QU: one raw type per wave;
  * otherwise the two halves load and dequantise on divergent paths and share
  * the MFMAs (v4_mfma_mixed). */
 template <int MS, bool QG, bool QU>
-__device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G, const V4Shared &meta, int mlen, int j0,
-                                           uint8_t *lds)
+__device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G, V4Shared &meta, const PfTile &tile,
+                                           int mlen, int j0, uint8_t *lds)
 {
     const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
     const int nkb = A.H / GK;
@@ -519,6 +615,23 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
     constexpr int TG = TL_BYTES(QG), TU = TL_BYTES(QU);
     const uint8_t *wt = up ? G.tu + (size_t)(jrow / TL_ROWS) * nkb * TU : G.tg + (size_t)(jrow / TL_ROWS) * nkb * TG;
     const int tb = up ? TU : TG;
+    typename RawOf<QG>::T rg[2];
+    typename RawOf<QU>::T ru[2];
+    auto w_load = [&](int buf, int kb) {
+        if (QG == QU || !up) tile_load(rg[buf], wt + (size_t)kb * tb, tlane);
+        else tile_load(ru[buf], wt + (size_t)kb * tb, tlane);
+    };
+    /* the rows' token ids, then the first step's weights (they depend on
+     * nothing; a wave's loads return in order, so the ids do not wait for
+     * them) */
+    int tok = 0;
+    if (t < mlen) tok = G.tok ? G.tok[tile.m0 + t] : G.tok0 + tile.m0 + t;
+    w_load(0, 0);
+    if (t < mlen) {
+        meta.tok[t] = tok;
+        meta.slot[t] = G.slot0 + tile.m0 + t;
+    }
+    __syncthreads();
     /* activation staging: rows >= mlen read row 0 (their products are never
      * stored), so every load is unconditional and the K loop has no branches
      * around its loads */
@@ -545,12 +658,6 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
     f32x16 acc[MS];
 #pragma unroll
     for (int ms = 0; ms < MS; ms++) acc[ms] = (f32x16){};
-    typename RawOf<QG>::T rg[2];
-    typename RawOf<QU>::T ru[2];
-    auto w_load = [&](int buf, int kb) {
-        if (QG == QU || !up) tile_load(rg[buf], wt + (size_t)kb * tb, tlane);
-        else tile_load(ru[buf], wt + (size_t)kb * tb, tlane);
-    };
     /* a step's MFMA work; the scheduling fences keep the next step's loads
      * ahead of it and the activation store (which waits for those loads)
      * after it */
@@ -561,9 +668,12 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
         __builtin_amdgcn_sched_barrier(0);
     };
     x_load(0);
-    w_load(0, 0);
+    if (t < mlen) meta.fwd[t] = A.xfwd ? A.xfwd[meta.tok[t]] : 1.0f;   /* read in the epilogue */
     x_store(Xb);
     __syncthreads();
+    PF_TS(2);
+    int tsk = 3;
+    (void)tsk;
     int kb = 0;
     if constexpr (QG == QU) {
         /* step kb's MFMA work on raw buffer buf with step kn's loads spread
@@ -578,22 +688,28 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
                 if (j < TL_SLICES(QG)) tile_slice(rg[buf ^ 1], wn, tlane, j);
             });
         };
+        /* bare barriers: __syncthreads()'s release fence would drain the
+         * next step's weight loads, which are only needed after the barrier */
         for (; kb + 2 < nkb; kb += 2) {
             step_ld(0, Xb, kb + 1);
             x_store(Xb + V3_XBUF);
-            __syncthreads();
+            lds_barrier();
+            PF_TS(tsk++);
             step_ld(1, Xb + V3_XBUF, kb + 2);
             x_store(Xb);
-            __syncthreads();
+            lds_barrier();
+            PF_TS(tsk++);
         }
         if (kb + 1 < nkb) {
             step_ld(0, Xb, kb + 1);
             x_store(Xb + V3_XBUF);
-            __syncthreads();
+            lds_barrier();
+            PF_TS(tsk++);
             step(1, Xb + V3_XBUF);
         } else {
             step(0, Xb);
         }
+        PF_TS(tsk++);
     } else {
         /* steady state: steps kb (raw buffer 0, activation buffer 0) and kb +
          * 1 (buffers 1), each issuing the next step's loads first, activations
@@ -624,41 +740,7 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
             step(0, Xb);
         }
     }
-    /* epilogue: lane n < 16 holds gate and lane n + 16 up of column col.  For
-     * the row pair (i, i + 1) one swizzle (lane ^ 16) gives lanes n < 16 the up
-     * value of row i and lanes n >= 16 the gate value of row i + 1, so all 32
-     * lanes compute act = silu(gate) * up (f32) for one row each; a 16-lane max
-     * gives the row's largest |act| over this wave's 16 columns (one part),
-     * stored to pmax[slot][part], and act is stored in fp16 scaled by that
-     * part's power of two (row_scale of the part max). */
-    const int npart = A.I / 16, part = (j0 + 16 * w) >> 4;
-    const int col = j0 + 16 * w + (n & 15);
-#pragma unroll
-    for (int ms = 0; ms < MS; ms++)
-#pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-            const float v0 = acc[ms][i], v1 = acc[ms][i + 1];
-            const float mine = up ? v1 : v0, other = up ? v0 : v1;
-            const float got = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, other), 0x401F));
-            const float gsum = up ? got : mine, usum = up ? mine : got;
-            const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3) + (up ? 1 : 0);
-            float e = 0.0f;
-            if (m < mlen) {
-                const float f = meta.fwd[m];
-                e = pf_silu_mul_fast(gsum * f, usum * f);
-            }
-            float mx = fabsf(e);
-            mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
-            mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
-            mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
-            mx = fmaxf(mx, dpp_f<DPP_MIRROR>(mx));
-            if (m < mlen) {
-                float pinv, pfwd;
-                row_scale(mx, pinv, pfwd);
-                A.act16[(size_t)meta.slot[m] * A.I + col] = __builtin_bit_cast(uint16_t, (_Float16)(e * pinv));
-                if ((n & 15) == 0) A.pmax[(size_t)meta.slot[m] * npart + part] = mx;
-            }
-        }
+    gu_epilogue<MS>(A, meta, acc, mlen, j0, lds);
 }
 
 /* Down tile: wave w takes output rows n0 + 32 w .. + 31 (one tile row group,
@@ -818,32 +900,34 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_gu_kernel(PfGemmArgs A)
     int v;
     PfTile tile;
     if (!v2_tile(A, nblk, v, tile)) return;
+    PF_TS(1);
+#ifdef ROASTER_PF_TS
+    {
+        unsigned hw, xc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xc));
+        PF_TSV(0, ((unsigned long long)xc << 32) | hw);
+        PF_TSV(13, (unsigned long long)v);
+    }
+#endif
     const PfGroup &G = A.groups[tile.grp];
     const int mlen = min(A.chunk, G.n - tile.m0);
-    const int t = threadIdx.x;
-    if (t < mlen) {
-        const int a = tile.m0 + t;
-        const int tok = G.tok ? G.tok[a] : G.tok0 + a;
-        meta.tok[t] = tok;
-        meta.slot[t] = G.slot0 + a;
-        meta.fwd[t] = A.xfwd ? A.xfwd[tok] : 1.0f;
-    }
-    __syncthreads();
+    PF_TSV(12, (unsigned long long)mlen);
     const int j0 = (v % nblk) * V2_GU_J;
     const int ms = (mlen + 31) >> 5;
     const int ty = (G.gq6 ? 2 : 0) | (G.uq6 ? 1 : 0);
     /* three row blocks come with one weight type only (pf_gemm_chunk) */
     if (ms == 3) {
-        if (ty == 3) v5_gu_body<3, true, true>(A, G, meta, mlen, j0, lds4);
-        else if (ty == 0) v5_gu_body<3, false, false>(A, G, meta, mlen, j0, lds4);
+        if (ty == 3) v5_gu_body<3, true, true>(A, G, meta, tile, mlen, j0, lds4);
+        else if (ty == 0) v5_gu_body<3, false, false>(A, G, meta, tile, mlen, j0, lds4);
         return;
     }
 #define GU_CASE(M)                                                                   \
     if (ms == M) {                                                                   \
-        if (ty == 3) v5_gu_body<M, true, true>(A, G, meta, mlen, j0, lds4);          \
-        else if (ty == 2) v5_gu_body<M, true, false>(A, G, meta, mlen, j0, lds4);   \
-        else if (ty == 1) v5_gu_body<M, false, true>(A, G, meta, mlen, j0, lds4);   \
-        else v5_gu_body<M, false, false>(A, G, meta, mlen, j0, lds4);                \
+        if (ty == 3) v5_gu_body<M, true, true>(A, G, meta, tile, mlen, j0, lds4);    \
+        else if (ty == 2) v5_gu_body<M, true, false>(A, G, meta, tile, mlen, j0, lds4);\
+        else if (ty == 1) v5_gu_body<M, false, true>(A, G, meta, tile, mlen, j0, lds4);\
+        else v5_gu_body<M, false, false>(A, G, meta, tile, mlen, j0, lds4);          \
         return;                                                                      \
     }
     GU_CASE(1)
