@@ -399,7 +399,9 @@ def prefill_q6_leg(torch, L, R, dev, stream, reps, with_cpu):
             "metric": "MoE-FFN prefill tok/s (all-Q6_K experts, 2048 tokens x 4 layers, one MI355X)",
             "value": round(tok_s, 1), "unit": "tokens/s", "tokens_per_s": round(tok_s, 1), "tok_s": round(tok_s, 1),
             "higher_is_better": True, "ms_per_pass": round(ms, 4), "layers": NL, "ms_per_layer": round(ms / NL, 4),
-            "dtype": "fp16 MFMA operands (activations row-scaled by powers of two), fp32 accumulation",
+            "dtype": "fp16 MFMA operands (activations row-scaled by powers of two), fp32 accumulation; "
+                     "per-(token, expert) down rows stored in fp16 (row-scaled by a power of two of their bound), "
+                     "combined in fp32",
             "config": {"workload": "all-Q6_K MoE prefill, 2048 tokens x 4 layers, logits ~ N(0,1) given, seed 4",
                        "hidden": H, "inter": I, "experts": E, "top_k": 8, "shared_experts": 1},
             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",

@@ -36,7 +36,8 @@ extern "C" {
 
 /* Prefill arithmetic. */
 /* Prefill GEMM operand precision (fp32 accumulation in every mode). */
-#define ROASTER_PREC_F16   0   /* fp16 operands, activations scaled per row by a power of two (default) */
+#define ROASTER_PREC_F16   0   /* fp16 operands, activations scaled per row by a power of two; the
+                                  per-(token, expert) down rows kept in fp16 until the combine (default) */
 #define ROASTER_PREC_SPLIT 1   /* bf16 hi+lo split of both operands, 3 MFMAs per product block */
 #define ROASTER_PREC_BF16  2   /* bf16 operands: fastest to convert, about 8 significant bits */
 

@@ -743,6 +743,44 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
     gu_epilogue<MS>(A, meta, acc, mlen, j0, lds);
 }
 
+/* A wave's down products of one output tile: lane n of half h holds column
+ * orow (= its tile column + n) of rows 32 ms + 8 (i >> 2) + 4 h + (i & 3).
+ * f32: one store per value.  fp16 (already scaled by each row's 2^-oexp):
+ * lanes n and n ^ 1 swap one value of each row pair (i, i + 1), so the even
+ * lane stores row i's columns (n, n + 1) and the odd lane row i + 1's as one
+ * 4-byte store: half the store instructions. */
+template <int MS>
+__device__ __forceinline__ void dn_store_tile(const PfGemmArgs &A, const V4Shared &meta, const f32x16 (&acc)[MS],
+                                              int mlen, int orow)
+{
+    const int l = threadIdx.x & 63, h = l >> 5;
+    if (!A.out16) {
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3);
+                if (m < mlen) A.out[(size_t)meta.slot[m] * A.H + orow] = acc[ms][i] * meta.fwd[m];
+            }
+        return;
+    }
+    const bool odd = (l & 1) != 0;
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            const int m0 = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3);     /* value i + 1 is row m0 + 1 */
+            const float v0 = acc[ms][i] * meta.fwd[m0], v1 = acc[ms][i + 1] * meta.fwd[m0 + 1];
+            const float got = dpp_f<DPP_XOR1>(odd ? v0 : v1);
+            const float lo = odd ? got : v0, hi = odd ? v1 : got;
+            const int m = odd ? m0 + 1 : m0;
+            if (m < mlen) {
+                const f16x2 pk = { (_Float16)lo, (_Float16)hi };
+                *(uint32_t *)(A.out16 + (size_t)meta.slot[m] * A.H + orow - (odd ? 1 : 0)) = __builtin_bit_cast(uint32_t, pk);
+            }
+        }
+}
+
 /* Down tile: wave w takes output rows n0 + 32 w .. + 31 (one tile row group,
  * its lane records in lane order). */
 template <int MS, bool QD>
@@ -802,13 +840,7 @@ __device__ __forceinline__ void v5_dn_body(const PfGemmArgs &A, const PfGroup &G
         if (kb + 3 < nkb) x_stage(kb + 3, Xb + V3_XBUF);
         __syncthreads();
     }
-#pragma unroll
-    for (int ms = 0; ms < MS; ms++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (m < mlen) A.out[(size_t)meta.slot[m] * A.H + orow] = acc[ms][i] * meta.fwd[m];
-        }
+    dn_store_tile<MS>(A, meta, acc, mlen, orow);
 }
 
 /* Down, K <= 512 (one or two K steps): a workgroup keeps the whole activation
@@ -872,13 +904,7 @@ __device__ __forceinline__ void v6_dn_body(const PfGemmArgs &A, const PfGroup &G
             if (more) tile_load(r[1], wn + TD, l);
         }
         const int orow = n0 + nt * V2_DN_N + 32 * w + n;
-#pragma unroll
-        for (int ms = 0; ms < MS; ms++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3);
-                if (m < mlen) A.out[(size_t)meta.slot[m] * A.H + orow] = acc[ms][i] * meta.fwd[m];
-            }
+        dn_store_tile<MS>(A, meta, acc, mlen, orow);
     }
 }
 
@@ -936,9 +962,14 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_gu_kernel(PfGemmArgs A)
 }
 
 /* Per-row meta of the down GEMM for tile rows [0, mlen): slot, the row's
- * power-of-two scale (from its part maxima) and each part's shift onto it. */
+ * power-of-two scale (from its part maxima) and each part's shift onto it.
+ * With fp16 products (A.out16) the row's products are also scaled by 2^-e,
+ * e the exponent row_scale gives their bound max|act| * G.dbnd (no product
+ * of the row exceeds it, so the scaled products stay below 2^15), and fwd
+ * folds both scales; e goes to A.oexp[slot] (first: the workgroup writing
+ * the row's first output columns). */
 __device__ __forceinline__ void dn_meta(const PfGemmArgs &A, const PfGroup &G, const PfTile &tile, int mlen,
-                                        V4Shared &meta)
+                                        V4Shared &meta, bool first)
 {
     const int t = threadIdx.x;
     if (t < mlen) {
@@ -951,6 +982,11 @@ __device__ __forceinline__ void dn_meta(const PfGemmArgs &A, const PfGroup &G, c
         meta.slot[t] = slot;
         meta.inv[t] = inv;
         meta.fwd[t] = fwd;
+        if (A.out16) {
+            const int sp = pf_scale_exp(mx * G.dbnd), sf = pf_scale_exp(mx) - sp;
+            meta.fwd[t] = __builtin_bit_cast(float, (uint32_t)(127 + max(-126, min(126, sf))) << 23);
+            if (first) A.oexp[slot] = (int8_t)sp;
+        }
         /* shift of part b: exponent of its scale minus the row's (fp16 mode) */
         const int er = pf_scale_exp(mx);
         for (int b = 0; b < nb && b < V5_MAXPART; b++)
@@ -969,9 +1005,9 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
     if (!v2_tile(A, nblk, v, tile)) return;
     const PfGroup &G = A.groups[tile.grp];
     const int mlen = min(A.chunk, G.n - tile.m0);
-    dn_meta(A, G, tile, mlen, meta);
-    __syncthreads();
     const int n0 = (v % nblk) * nt_count * V2_DN_N;
+    dn_meta(A, G, tile, mlen, meta, n0 == 0);
+    __syncthreads();
     const int ms = (mlen + 31) >> 5;
     const bool whole_k = A.I <= 2 * GK;        /* activations for every K step fit in LDS */
 #define DN_CASE(M)                                                                   \
@@ -1014,7 +1050,7 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_bal_kernel(PfGemmArg
         const PfTile tile = A.tiles[ti];
         const PfGroup &G = A.groups[tile.grp];
         const int mlen = min(A.chunk, G.n - tile.m0);
-        dn_meta(A, G, tile, mlen, meta);
+        dn_meta(A, G, tile, mlen, meta, t0 == 0);
         __syncthreads();
         const int ms = (mlen + 31) >> 5, n0 = t0 * V2_DN_N;
         if (ms == 1) {

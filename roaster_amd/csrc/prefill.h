@@ -20,7 +20,7 @@ struct PfGroup {
     int slot0;                      /* first slot */
     int tok0;                       /* rows read X[tok0 + a] when tok is NULL */
     const int *tok;                 /* [n] activation rows, or NULL */
-    int pad;
+    float dbnd;                     /* bound on the L1 norm of any row of d (fp16 products), or 0 */
 };
 
 struct PfTile {
@@ -38,7 +38,9 @@ struct PfGemmArgs {
     uint16_t *act16;                /* [slots x I]: the same in fp16, each 16-column part scaled by the
                                        power of two of its pmax entry (fp16 mode) */
     float *pmax;                    /* [slots][inter / 16] partial max |act| (fp16 mode) */
-    float *out;                     /* [slots x H]: down products */
+    float *out;                     /* [slots x H]: down products (f32), when out16 is NULL */
+    uint16_t *out16;                /* [slots x H]: the same in fp16, row s scaled by 2^-oexp[s], or NULL */
+    int8_t *oexp;                   /* [slots] scale exponents of out16's rows */
     int H, I;
     int chunk;                      /* rows per tile of the tile list (pf_gemm_chunk) */
     int dn_nt;                      /* down GEMM: output tiles per workgroup (set by the launcher) */

@@ -318,6 +318,7 @@ struct PfPlanArgs {
     int *off;                   /* [E] */
     int *counts_out;            /* [E] or NULL */
     PfGroup *groups;            /* [E + 1] */
+    const float *dbound;        /* [E + 1] down-row L1 bounds of the layer */
     PfTile *tiles;
     int *ntiles;
     int T, E;
@@ -348,7 +349,7 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
         G.slot0 = off;
         G.tok0 = 0;
         G.tok = A.list + (size_t)e * A.T;
-        G.pad = 0;
+        G.dbnd = A.dbound[e];
         A.groups[e] = G;
         for (int i = 0; i < nt; i++) A.tiles[toff + i] = PfTile{ e, i * A.chunk };
     }
@@ -362,7 +363,7 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
         G.slot0 = 8 * A.T;
         G.tok0 = 0;
         G.tok = nullptr;
-        G.pad = 0;
+        G.dbnd = A.dbound[A.E];
         A.groups[A.E] = G;
         *A.ntiles = tot_tiles + nsh;
     }
@@ -370,13 +371,14 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
 }
 
 /* ---- combine -------------------------------------------------------------- */
-extern "C" __global__ void __launch_bounds__(256) pf_combine_kernel(const float *ed, const int *ids, const float *w,
-                                                                    const int *rank, const int *off, const float *sg,
-                                                                    float *Y, int T, int H)
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+/* Token t's routed slots and weights in ascending expert id (sl = -1 for an
+ * unrouted pick). */
+__device__ __forceinline__ void pf_token_slots(const int *ids, const float *w, const int *rank, const int *off, int t,
+                                               int (&sl)[8], float (&wt)[8])
 {
-    const int t = blockIdx.x;
-    int id[8], sl[8], rk[8], id0[8];
-    float wt[8];
+    int id[8], rk[8], id0[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) {       /* the token's ids, weights and ranks in one round trip */
         id[k] = ids[(size_t)t * 8 + k];
@@ -406,6 +408,18 @@ extern "C" __global__ void __launch_bounds__(256) pf_combine_kernel(const float 
             sl[k] = off[id[k]] + r;
         }
     }
+}
+
+/* Y[t] = g_t * shared row + sum over the routed rows in ascending expert id of
+ * w * row (f32 rows), one fused multiply-add per term. */
+extern "C" __global__ void __launch_bounds__(256) pf_combine_kernel(const float *ed, const int *ids, const float *w,
+                                                                    const int *rank, const int *off, const float *sg,
+                                                                    float *Y, int T, int H)
+{
+    const int t = blockIdx.x;
+    int sl[8];
+    float wt[8];
+    pf_token_slots(ids, w, rank, off, t, sl, wt);
     const float g = sg[t];
     const float *sh = ed + ((size_t)8 * T + t) * H;
     /* H <= 2048: two float4 columns per thread, all 18 row loads issued
@@ -436,6 +450,47 @@ extern "C" __global__ void __launch_bounds__(256) pf_combine_kernel(const float 
         }
         *(float4 *)(Y + (size_t)t * H + i) = y;
     }
+}
+
+/* The combine on fp16 rows (fp16 mode), row s holding product * 2^-oexp[s]:
+ * each term multiplies by w * 2^oexp[s] instead (exact: a power-of-two
+ * scaling of the weight), so every fused multiply-add equals the f32
+ * combine's on the fp16-rounded product.  8 columns (16 bytes) per thread,
+ * all 9 row loads issued before the first use. */
+extern "C" __global__ void __launch_bounds__(256) pf_combine16_kernel(const uint16_t *ed, const int8_t *oexp,
+                                                                      const int *ids, const float *w, const int *rank,
+                                                                      const int *off, const float *sg, float *Y, int T,
+                                                                      int H)
+{
+    const int t = blockIdx.x;
+    int sl[8];
+    float wt[8];
+    pf_token_slots(ids, w, rank, off, t, sl, wt);
+    const size_t shrow = (size_t)8 * T + t;
+    const float g = __builtin_ldexpf(sg[t], oexp[shrow]);
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        if (sl[k] >= 0) wt[k] = __builtin_ldexpf(wt[k], oexp[sl[k]]);
+    const int i = min((int)threadIdx.x * 8, H - 8);
+    const uint4 s8 = *(const uint4 *)(ed + shrow * H + i);
+    uint4 d8[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) d8[k] = *(const uint4 *)(ed + (sl[k] >= 0 ? (size_t)sl[k] : shrow) * H + i);
+    if ((int)threadIdx.x * 8 >= H) return;
+    const f16x8_t sh = __builtin_bit_cast(f16x8_t, s8);
+    float y[8];
+#pragma unroll
+    for (int c = 0; c < 8; c++) y[c] = g * (float)sh[c];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        if (sl[k] < 0) continue;
+        const f16x8_t d = __builtin_bit_cast(f16x8_t, d8[k]);
+#pragma unroll
+        for (int c = 0; c < 8; c++) y[c] = fmaf(wt[k], (float)d[c], y[c]);
+    }
+    float4 *yo = (float4 *)(Y + (size_t)t * H + i);
+    yo[0] = make_float4(y[0], y[1], y[2], y[3]);
+    yo[1] = make_float4(y[4], y[5], y[6], y[7]);
 }
 
 /* ---- host ---------------------------------------------------------------- */
@@ -471,7 +526,8 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     const size_t o_cnt = take((size_t)E * 4), o_off = take((size_t)E * 4), o_list = take((size_t)E * TT * 4);
     const size_t o_grp = take(sizeof(PfGroup) * (E + 1)), o_tiles = take(sizeof(PfTile) * max_tiles);
     const size_t o_nt = take(4), o_pmax = take(slots * (size_t)(I / 16) * 4);
-    const size_t o_act = take(slots * I * 4), o_ed = take(slots * H * 4);
+    const size_t o_act = take(slots * I * 4), o_ed = take(slots * H * (op == PF_F16 ? 2 : 4));
+    const size_t o_oexp = op == PF_F16 ? take(slots) : 0;
     uint8_t *ws = (uint8_t *)rt_scratch(SCR_PF, sz);
     unsigned *ctrl = rt_ctrl();
     if (!ws || !ctrl) return ROASTER_ENOMEM;
@@ -521,6 +577,7 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     pa.off = (int *)(ws + o_off);
     pa.counts_out = opt.counts_out;
     pa.groups = (PfGroup *)(ws + o_grp);
+    pa.dbound = t->dbound + (size_t)layer * (E + 1);
     pa.tiles = (PfTile *)(ws + o_tiles);
     pa.ntiles = (int *)(ws + o_nt);
     pa.T = T; pa.E = E;
@@ -539,13 +596,23 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     ga.act = (float *)(ws + o_act);
     ga.act16 = (uint16_t *)(ws + o_act);
     ga.pmax = op == PF_F16 ? (float *)(ws + o_pmax) : nullptr;
-    ga.out = (float *)(ws + o_ed);
+    /* fp16 mode: per-(token, expert) products in fp16, each row scaled by a
+     * power of two of its bound (half the bytes of f32 rows, written by the
+     * down GEMM and read back by the combine) */
+    ga.out = op == PF_F16 ? nullptr : (float *)(ws + o_ed);
+    ga.out16 = op == PF_F16 ? (uint16_t *)(ws + o_ed) : nullptr;
+    ga.oexp = op == PF_F16 ? (int8_t *)(ws + o_oexp) : nullptr;
     ga.H = H; ga.I = I;
     ga.chunk = chunk;
     if (int rc = pf_gemm_launch(ga, max_tiles, op)) return rc;
 
-    hipLaunchKernelGGL(pf_combine_kernel, dim3(T), dim3(256), 0, R.stream, (const float *)ga.out,
-                       (const int *)ta.ids, (const float *)ta.w, (const int *)(ws + o_rank), (const int *)pa.off,
-                       (const float *)ta.sg, Y, T, H);
+    if (op == PF_F16)
+        hipLaunchKernelGGL(pf_combine16_kernel, dim3(T), dim3(256), 0, R.stream, (const uint16_t *)ga.out16,
+                           (const int8_t *)ga.oexp, (const int *)ta.ids, (const float *)ta.w, (const int *)(ws + o_rank),
+                           (const int *)pa.off, (const float *)ta.sg, Y, T, H);
+    else
+        hipLaunchKernelGGL(pf_combine_kernel, dim3(T), dim3(256), 0, R.stream, (const float *)ga.out,
+                           (const int *)ta.ids, (const float *)ta.w, (const int *)(ws + o_rank), (const int *)pa.off,
+                           (const float *)ta.sg, Y, T, H);
     return rt_check(hipGetLastError(), "prefill combine launch") ? ROASTER_EDEVICE : 0;
 }

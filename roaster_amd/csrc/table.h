@@ -33,6 +33,7 @@ struct RoasterTable {
     std::vector<DecLayer> layers_h;
     DecLayer *layers_d = nullptr;
     std::vector<TileLayer> tlayers_h;
+    float *dbound = nullptr; /* [n_layers][E + 1]: bound on the L1 norm of any row of each down matrix */
 };
 
 #endif

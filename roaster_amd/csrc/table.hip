@@ -74,12 +74,16 @@ extern "C" RoasterTable *roaster_table_create_layers(const RoasterTableDesc *d, 
     if (hipMalloc((void **)&t->qmem, t->qbytes + RT_TAIL_PAD) != hipSuccess ||
         hipMalloc((void **)&t->tmem, t->tbytes + RT_TAIL_PAD) != hipSuccess ||
         hipMalloc((void **)&t->fmem, t->fbytes) != hipSuccess ||
-        hipMalloc((void **)&t->layers_d, sizeof(DecLayer) * d->n_layers) != hipSuccess) {
+        hipMalloc((void **)&t->layers_d, sizeof(DecLayer) * d->n_layers) != hipSuccess ||
+        hipMalloc((void **)&t->dbound, sizeof(float) * d->n_layers * (E + 1)) != hipSuccess ||
+        hipMemset(t->dbound, 0, sizeof(float) * d->n_layers * (E + 1)) != hipSuccess) {
         (void)hipGetLastError();
         rt_fail(ROASTER_ENOMEM, "expert table of %zu bytes does not fit in HBM", t->qbytes + t->tbytes + t->fbytes);
         if (t->qmem) (void)hipFree(t->qmem);
         if (t->tmem) (void)hipFree(t->tmem);
         if (t->fmem) (void)hipFree(t->fmem);
+        if (t->layers_d) (void)hipFree(t->layers_d);
+        if (t->dbound) (void)hipFree(t->dbound);
         delete t;
         return NULL;
     }
@@ -134,6 +138,7 @@ extern "C" void roaster_table_destroy(RoasterTable *t)
     (void)hipFree(t->tmem);
     (void)hipFree(t->fmem);
     (void)hipFree(t->layers_d);
+    (void)hipFree(t->dbound);
     delete t;
 }
 
@@ -200,8 +205,58 @@ static uint8_t *tmat_ptr(const RoasterTable *t, int layer, int expert, int kind)
     return base + G.toff_exps[kind] + (size_t)expert * G.teb[kind];
 }
 
+/* Bound on the L1 norm of every row of nmat consecutive [rows x cols] down
+ * matrices (one workgroup per matrix), from the block headers alone: a Q6_K
+ * weight is d sc (q - 32) with |q - 32| <= 32, so a 16-weight sub-block sums
+ * to at most 16 * 32 |d| |sc|; a Q4_K weight is d sc q - dmin m with q <= 15,
+ * so a 32-weight sub-block sums to at most 32 (15 |d| sc + |dmin| m).  The
+ * prefill stores its per-row down products in fp16 scaled by this bound times
+ * the row's largest activation, which no product can exceed. */
+__global__ void __launch_bounds__(256) dbound_kernel(const uint8_t *src, size_t src_mat, int rows, int cols, int q6,
+                                                     float *dst)
+{
+    __shared__ float wmax[4];
+    const uint8_t *mat = src + (size_t)blockIdx.x * src_mat;
+    const int nkb = cols / RQK;
+    const size_t bb = q6 ? RQ6K_BYTES : RQ4K_BYTES;
+    float mx = 0.0f;
+    for (int r = threadIdx.x; r < rows; r += blockDim.x) {
+        float s = 0.0f;
+        for (int kb = 0; kb < nkb; kb++) {
+            const uint8_t *blk = mat + ((size_t)r * nkb + kb) * bb;
+            if (q6) {
+                const float d = fabsf((float)__builtin_bit_cast(_Float16, (uint16_t)(blk[208] | (blk[209] << 8))));
+                int sc = 0;
+                for (int j = 0; j < 16; j++) sc += abs((int)(int8_t)blk[192 + j]);
+                s += 512.0f * d * (float)sc;
+            } else {
+                const float d = fabsf((float)__builtin_bit_cast(_Float16, (uint16_t)(blk[0] | (blk[1] << 8))));
+                const float dm = fabsf((float)__builtin_bit_cast(_Float16, (uint16_t)(blk[2] | (blk[3] << 8))));
+                const uint8_t *q = blk + 4;
+                int sc = 0, mn = 0;
+                for (int j = 0; j < 8; j++) {
+                    if (j < 4) {
+                        sc += q[j] & 63;
+                        mn += q[j + 4] & 63;
+                    } else {
+                        sc += (q[j + 4] & 15) | ((q[j - 4] >> 6) << 4);
+                        mn += (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+                    }
+                }
+                s += 32.0f * (15.0f * d * (float)sc + dm * (float)mn);
+            }
+        }
+        mx = fmaxf(mx, s);
+    }
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) dst[blockIdx.x] = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+}
+
 /* Rebuild the tile copy of nmat consecutive matrices of one kind (routed
- * experts e0 .. e0 + nmat - 1, or the shared expert when e0 == E). */
+ * experts e0 .. e0 + nmat - 1, or the shared expert when e0 == E), and for
+ * down matrices their row bounds. */
 static int tile_repack(const RoasterTable *t, int layer, int e0, int nmat, int kind)
 {
     const RoasterTableDesc &d = t->d;
@@ -214,7 +269,14 @@ static int tile_repack(const RoasterTable *t, int layer, int e0, int nmat, int k
     hipLaunchKernelGGL(tile_repack_kernel, dim3(blocks), dim3(256), 0, rt().stream, mat_ptr(t, layer, e0, kind),
                        tmat_ptr(t, layer, e0, kind), mat_bytes(t, layer, e0, kind), sh ? G.tsb[kind] : G.teb[kind], rows,
                        cols, nmat, q6);
-    return rt_check(hipGetLastError(), "tile repack launch") ? ROASTER_EDEVICE : 0;
+    if (rt_check(hipGetLastError(), "tile repack launch")) return ROASTER_EDEVICE;
+    if (kind == 2) {
+        hipLaunchKernelGGL(dbound_kernel, dim3(nmat), dim3(256), 0, rt().stream, mat_ptr(t, layer, e0, kind),
+                           mat_bytes(t, layer, e0, kind), rows, cols, q6,
+                           t->dbound + (size_t)layer * (d.n_experts + 1) + e0);
+        if (rt_check(hipGetLastError(), "down bound launch")) return ROASTER_EDEVICE;
+    }
+    return 0;
 }
 
 extern "C" int roaster_table_set_expert(RoasterTable *t, int layer, int expert, const void *gate, const void *up,
