@@ -11,6 +11,9 @@ task) and on a token sample of the other three; a token's output depends on
 its own input and logits alone (model.c computes every (token, expert) row
 independently), which the permutation tests check bit for bit on the GPU,
 at T = 300 on the Q4_K / Q6_K table and at T = 2048 on the all-Q6_K one.
+The fp16 mode keeps each (token, expert) down row in fp16 scaled by a power
+of two of its bound; a table whose down products reach ~1e7 checks that
+scaling against the oracle.
 """
 import ctypes as C
 import os
@@ -163,6 +166,40 @@ def test_prefill_balanced_down_bit_exact(cfg3, T):
         lib.roaster_prefill_balanced_down(1)
     np.testing.assert_array_equal(ids0, ids1)
     np.testing.assert_array_equal(Y0, Y1)
+
+
+def test_prefill_fp16_products_scaled_by_their_bound():
+    """Down products far outside the fp16 range: expert 3's down matrix with
+    every Q6_K block's d scaled by 2^12 and activations 8x larger, so that its
+    per-(token, expert) rows reach ~1e7 (fp16 ends at 65504).  The fp16 mode
+    stores each row scaled by a power of two of its bound (max activation
+    times the table's bound on the down rows' L1 norm, rebuilt by
+    roaster_table_set_expert), so every output stays finite and within the
+    bar against the oracle."""
+    E, T = 16, 64
+    t = SynthTable(31, n_experts=E)
+    try:
+        g, u, d = t.expert(0, 3)
+        blk = d.copy().reshape(-1, 210)
+        dd = blk[:, 208:210].copy().view(np.float16).astype(np.float32) * 4096.0
+        blk[:, 208:210] = dd.astype(np.float16).view(np.uint8).reshape(-1, 2)
+        d = np.ascontiguousarray(blk.ravel())
+        R.check(R.lib().roaster_table_set_expert(t.t, 0, 3, g.ctypes.data, u.ctypes.data, d.ctypes.data), "set_expert")
+        t._experts[(0, 3)] = (g, u, d)
+        X = (tokens(32, T) * 8.0).astype(np.float32)
+        lg_in = np.stack([R.synth_normal(33, R.synth_stream(0, i, 7), E) for i in range(T)])
+        lg_in[:, 3] = 2.0                            # expert 3 in every token's top 8
+        Y, lg, ids, w, counts = prefill(t, X, logits_in=lg_in)
+        assert (ids == 3).any(axis=1).all()
+        assert np.isfinite(Y).all()
+        rc, Y_ref, _, _, _ = t.oracle_layer(0).prefill(X, logits_in=lg_in)
+        assert rc == 0
+        err = rel_err(Y, Y_ref)
+        log(f"large down products: max|y| = {np.abs(Y_ref).max():.3e}, max|d|/max|y| = {err:.3e}")
+        assert np.abs(Y_ref).max() > 1e6
+        assert err <= TOL
+    finally:
+        t.destroy()
 
 
 def test_prefill_reports_routing_failure(cfg3, cfg3_oracle):
