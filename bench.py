@@ -35,8 +35,11 @@ import sys
 import time
 
 # The prefill CPU baselines run the reference's OpenMP kernels: threads bound
-# close to each other, one per physical core (BASELINE's method).  Set before
-# torch or any OpenMP runtime loads, since the runtime reads them once.
+# close to each other, one per physical core.  Set before torch loads: its
+# bundled libgomp (which the reference build binds to as well, by soname) reads
+# them once, and then binds the initial thread to the first core, so the CPUs
+# this process may use are recorded first.
+_CPUS0 = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
 os.environ.setdefault("OMP_PROC_BIND", "close")
 os.environ.setdefault("OMP_PLACES", "cores")
 
@@ -133,10 +136,7 @@ def socket_cores():
     """Physical cores of one socket among the CPUs this process may run on
     (the socket with the most of them): the prefill CPU baseline's thread
     count."""
-    try:
-        cpus = sorted(os.sched_getaffinity(0))
-    except AttributeError:
-        cpus = list(range(os.cpu_count() or 1))
+    cpus = _CPUS0                    # before the OpenMP runtime bound this thread
     per_pkg = {}
     for c in cpus:
         base = "/sys/devices/system/cpu/cpu%d/topology/" % c
@@ -310,7 +310,7 @@ def cpu_baseline_prefill(table, desc, seed, X, ids, layer=0, with_router=True, r
            "sample": f"one {T}-token {label} layer ({'router + ' if with_router else ''}{len(groups)} expert groups "
                      f"+ shared expert via the reference moe_cpu), best of {reps}: {best:.3f} s",
            "threads": f"{threads} OpenMP threads = physical cores of one socket among the "
-                      f"{len(os.sched_getaffinity(0))} CPUs this process may use; OMP_PROC_BIND="
+                      f"{len(_CPUS0)} CPUs this process may use; OMP_PROC_BIND="
                       f"{os.environ.get('OMP_PROC_BIND')}, OMP_PLACES={os.environ.get('OMP_PLACES')}"}
     out.update(host_cpu())
     return out
