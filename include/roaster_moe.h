@@ -245,6 +245,13 @@ int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, int T, float
  * tiles (0); -1 queries.  Both give bit-identical results.  Returns the mode
  * in force. */
 int roaster_prefill_balanced_down(int enable);
+/* The fp16-mode gate/up GEMM on a persistent grid, one workgroup per CU taking
+ * (tile, 128-column) units from work counters and preparing the next unit
+ * while one runs (1, default; layers whose routed and shared gate and up
+ * matrices share one type and whose hidden size is a multiple of 512, at
+ * least 2048), or one workgroup per unit (0); -1 queries.  Both give
+ * bit-identical results.  Returns the mode in force. */
+int roaster_prefill_persistent_gate_up(int enable);
 
 #ifdef __cplusplus
 }

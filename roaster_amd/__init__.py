@@ -140,6 +140,7 @@ _SIG = {
     "roaster_dense_mfma_min_tokens": (C.c_int, [C.c_int]),
     "roaster_moe_prefill": (C.c_int, [_P, C.c_int, _P, C.c_int, _P, C.POINTER(RoasterPrefillOpts)]),
     "roaster_prefill_balanced_down": (C.c_int, [C.c_int]),
+    "roaster_prefill_persistent_gate_up": (C.c_int, [C.c_int]),
 }
 
 _lib = None

@@ -29,6 +29,8 @@
  * v1 (PF_SPLIT, PF_BF16) -- 64 x 64 output tiles, 256 threads, operands of
  * both sides dequantised / converted into LDS (gemm.h).
  */
+#include <type_traits>
+
 #include "internal.h"
 #include "gemm.h"
 #include "prefill.h"
@@ -52,9 +54,20 @@ extern "C" int roaster_pf_ts(unsigned long long *out)
     do {                                                                                      \
         if (threadIdx.x == 0 && blockIdx.x < 4096) g_pf_ts[blockIdx.x][i] = (v);              \
     } while (0)
+/* the persistent gate/up grid records by unit instead of workgroup */
+#define PF_TSU(u, i)                                                                          \
+    do {                                                                                      \
+        if (threadIdx.x == 0 && (u) >= 0 && (u) < 4096) g_pf_ts[u][i] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#define PF_TSUV(u, i, v)                                                                      \
+    do {                                                                                      \
+        if (threadIdx.x == 0 && (u) >= 0 && (u) < 4096) g_pf_ts[u][i] = (v);                 \
+    } while (0)
 #else
 #define PF_TS(i) do { } while (0)
 #define PF_TSV(i, v) do { } while (0)
+#define PF_TSU(u, i) do { } while (0)
+#define PF_TSUV(u, i, v) do { } while (0)
 #endif
 
 static __device__ __forceinline__ float pf_silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
@@ -540,15 +553,18 @@ __device__ __forceinline__ void v8_mfma(f32x16 (&acc)[MS], const _Float16 *Xs, c
  * (the activation buffers are free once every wave's last MFMAs have read
  * them) and written out as whole rows: the tile's 128 columns of act16 (256
  * bytes) and its 8 part maxima per row. */
-template <int MS>
-__device__ __forceinline__ void gu_epilogue(const PfGemmArgs &A, const V4Shared &meta, const f32x16 (&acc)[MS], int mlen,
+template <int MS, class M = V4Shared, bool LB = false>
+__device__ __forceinline__ void gu_epilogue(const PfGemmArgs &A, const M &meta, const f32x16 (&acc)[MS], int mlen,
                                             int j0, uint8_t *lds)
 {
-    const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
+    int t = threadIdx.x;
+    if constexpr (LB) asm volatile("" : "+v"(t));            /* its addressing is not hoisted into the K loop */
+    const int l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
     const bool up = n >= 16;
     const int npart = A.I / 16;
     constexpr int AP = V2_GU_J + 8;                          /* fp16 pitch of a staged row */
-    __syncthreads();
+    if constexpr (LB) lds_barrier();
+    else __syncthreads();
     _Float16 *act_s = (_Float16 *)lds;                       /* [MS * 32][AP] */
     float *pmx_s = (float *)(lds + (size_t)MS * 32 * AP * 2); /* [MS * 32][8] */
 #pragma unroll
@@ -585,7 +601,8 @@ __device__ __forceinline__ void gu_epilogue(const PfGemmArgs &A, const V4Shared 
             if ((n & 15) == 0) pmx_s[m * 8 + w] = mx;
         }
     }
-    __syncthreads();
+    if constexpr (LB) lds_barrier();
+    else __syncthreads();
     /* rows m < mlen: 16 lanes per row, 16 bytes each */
     for (int r = t >> 4; r < mlen; r += V2_T / 16) {
         const int c = t & 15;
@@ -595,7 +612,7 @@ __device__ __forceinline__ void gu_epilogue(const PfGemmArgs &A, const V4Shared 
         const int c = t & 1;
         *(float4 *)(A.pmax + (size_t)meta.slot[r] * npart + (j0 >> 4) + 4 * c) = *(const float4 *)(pmx_s + r * 8 + 4 * c);
     }
-    PF_TS(11);
+    if constexpr (!LB) PF_TS(11);
 }
 
 /* Gate/up tile: lanes n < 16 of wave w take gate row j0 + 16 w + n, lanes
@@ -961,6 +978,314 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_gu_kernel(PfGemmArgs A)
 #undef GU_CASE
 }
 
+/* ---- gate/up on a persistent grid ------------------------------------------
+ * One workgroup per CU takes (tile, 128-column block) units through work
+ * counters over eight ranges of the unit list (its own XCD's range first,
+ * then the others'), so the units of one XCD share their tiles' activations
+ * in its L2 and no CU sits idle while another still holds several units.
+ * While a unit runs, the next one is prepared in the K steps' shadow: its
+ * index (taken at the unit's start), tile (step 1) and group (step 2), its
+ * rows' tokens (step 3, stored with the slots at step 4) and scales (step 5)
+ * into the second meta buffer; the last K step issues its first step's
+ * activations and weights, so those loads are in flight during this unit's
+ * epilogue.  The epilogue stages its rows above the two activation buffers,
+ * so the next unit's first activations are stored into buffer 0 before the
+ * unit ends.
+ * Each unit's arithmetic is v5_gu_body's (bit-identical results).  Every unit
+ * of a launch has one weight type, and nkb is even and >= 8. */
+#define GP_STAGE (2 * V3_XBUF * 2)                               /* epilogue staging (bytes into LDS) */
+#define GP_LDS (GP_STAGE + V2_MC * (V2_GU_J + 8) * 2 + V2_MC * 8 * 4)
+
+struct GuMeta {
+    int tok[V2_MC];
+    int slot[V2_MC];
+    float fwd[V2_MC];
+};
+
+/* A unit as the workgroup sees it (wave-uniform). */
+struct GuUnit {
+    int u;                          /* unit index, or -1 */
+    int mlen, j0, m0, slot0, tok0;
+    const int *tok;
+    const uint8_t *tg, *tu;
+};
+
+/* A unit's tile and group fields come in by vector loads a K step ahead of
+ * their use (scalar loads would share the LDS wait counter with the MFMA
+ * operand reads, flat loads both counters), one dword per lane: lane k holds
+ * dword k of the record, and the fields are read out by lane.  u < 0 reads
+ * unit 0's (valid addresses, unused). */
+__device__ __forceinline__ uint32_t gp_tile_load(const PfGemmArgs &A, int u, int nblk)
+{
+    return gld_u32((const uint8_t *)(A.tiles + (u >= 0 ? u / nblk : 0)) + 4 * (threadIdx.x & 1));
+}
+
+__device__ __forceinline__ uint32_t gp_group_load(const PfGemmArgs &A, uint32_t tw)
+{
+    constexpr int NW = (int)(sizeof(PfGroup) / 4);
+    const uint8_t *g = (const uint8_t *)(A.groups + __builtin_amdgcn_readlane((int)tw, 0));
+    return gld_u32(g + 4 * min((int)(threadIdx.x & 63), NW - 1));
+}
+
+__device__ __forceinline__ int gp_field(uint32_t gw, size_t off) { return __builtin_amdgcn_readlane((int)gw, (int)(off / 4)); }
+
+__device__ __forceinline__ const void *gp_ptr(uint32_t gw, size_t off)
+{
+    const uint64_t p = ((uint64_t)(uint32_t)gp_field(gw, off + 4) << 32) | (uint32_t)gp_field(gw, off);
+    return (const void *)p;
+}
+
+__device__ __forceinline__ void gp_fill(const PfGemmArgs &A, uint32_t tw, uint32_t gw, int u, int nblk, GuUnit &N)
+{
+    N.u = u;
+    N.m0 = __builtin_amdgcn_readlane((int)tw, 1);
+    N.j0 = (u >= 0 ? u % nblk : 0) * V2_GU_J;
+    N.mlen = min(A.chunk, gp_field(gw, offsetof(PfGroup, n)) - N.m0);
+    N.slot0 = gp_field(gw, offsetof(PfGroup, slot0));
+    N.tok0 = gp_field(gw, offsetof(PfGroup, tok0));
+    N.tok = (const int *)gp_ptr(gw, offsetof(PfGroup, tok));
+    N.tg = (const uint8_t *)gp_ptr(gw, offsetof(PfGroup, tg));
+    N.tu = (const uint8_t *)gp_ptr(gw, offsetof(PfGroup, tu));
+}
+
+/* Row t's token of unit N, clamped to its last row (loads nothing
+ * conditionally: the shared expert's tile reads A.ntiles and ignores it). */
+__device__ __forceinline__ int gp_tok(const PfGemmArgs &A, const GuUnit &N, int t)
+{
+    const int r = min(t, N.mlen - 1);
+    const int *tp = N.tok ? N.tok + N.m0 + r : A.ntiles;
+    const int tv = (int)gld_u32(tp);
+    return N.tok ? tv : N.tok0 + N.m0 + r;
+}
+
+__device__ __forceinline__ float gp_fwd(const PfGemmArgs &A, int tok)
+{
+    return A.xfwd ? __builtin_bit_cast(float, gld_u32(A.xfwd + tok)) : 1.0f;
+}
+
+/* Thread 0: unit index of an issued take (old value of counter x0 + xs);
+ * a range that has run out moves on to the next XCD's. */
+__device__ __forceinline__ int gp_resolve(const PfGemmArgs &A, int old, int &xs, int x0, int U)
+{
+    for (;;) {
+        const int x = (x0 + xs) & 7;
+        const int lo = (int)((long long)x * U / 8), hi = (int)((long long)(x + 1) * U / 8);
+        if (lo + old < hi) return lo + old;
+        if (++xs == 8) return -1;
+        old = __hip_atomic_fetch_add(A.gu_ctr + ((x0 + xs) & 7), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <int MS, bool Q6>
+__device__ __forceinline__ void gp_unit(const PfGemmArgs &A, GuMeta (&meta)[2], int cur, const GuUnit &U, GuUnit &N,
+                                        int *s_unit, typename RawOf<Q6>::T (&rg)[2], uint4 (&xr)[6], uint8_t *lds,
+                                        int &xs, int x0, int Uall, int nblk)
+{
+    const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
+    const int nkb = A.H / GK;
+    _Float16 *Xb = (_Float16 *)lds;
+    const bool up = n >= 16;
+    constexpr int TB = TL_BYTES(Q6), WS = TL_SLICES(Q6), NP = 2 * MS;
+    const int tlane = ((16 * w + (n & 15)) & (TL_ROWS - 1)) + 32 * h;   /* j0 is a multiple of 128 */
+    const int rblk = (16 * w + (n & 15)) / TL_ROWS;
+    const uint8_t *wt = (up ? U.tu : U.tg) + (size_t)(U.j0 / TL_ROWS + rblk) * nkb * TB;
+    GuMeta &mc = meta[cur], &mn = meta[cur ^ 1];
+    const uint8_t *x16 = (const uint8_t *)A.X16;
+    uint32_t xoff[NP];
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const int idx = t + i * V2_T, row = idx >> 5;
+        xoff[i] = 2u * ((uint32_t)mc.tok[row < U.mlen ? row : 0] * (uint32_t)A.H + 8u * (idx & 31));
+    }
+    auto x_load = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < NP; i++) xr[i] = gld_u4(x16 + xoff[i] + 2 * kb * GK);
+    };
+    auto x_store = [&](_Float16 *dst) {
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int idx = t + i * V2_T, row = idx >> 5;
+            *(uint4 *)(dst + row * V2_LD + 8 * (idx & 31)) = xr[i];
+        }
+    };
+    PF_TSU(U.u, 1);
+#ifdef ROASTER_PF_TS
+    {
+        unsigned hw, xc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xc));
+        PF_TSUV(U.u, 0, ((unsigned long long)xc << 32) | hw);
+        PF_TSUV(U.u, 12, (unsigned long long)U.mlen);
+        PF_TSUV(U.u, 13, (unsigned long long)blockIdx.x);
+    }
+#endif
+    int tk = 0;
+    if (t == 0) tk = __hip_atomic_fetch_add(A.gu_ctr + ((x0 + xs) & 7), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    f32x16 acc[MS];
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++) acc[ms] = (f32x16){};
+    /* step kb on raw and activation buffer buf, loading step kb + 1 into
+     * buffer buf ^ 1 */
+    auto step = [&](auto bc, int kb) {
+        constexpr int buf = decltype(bc)::value;
+        const uint8_t *wn = wt + (size_t)(kb + 1) * TB;
+        __builtin_amdgcn_sched_barrier(0);
+        v8_mfma<MS, Q6>(acc, Xb + buf * V3_XBUF, rg[buf], h, [&](int j) {
+            if (j == 0) x_load(kb + 1);
+            if (j < WS) tile_slice(rg[buf ^ 1], wn, tlane, j);
+        });
+        __builtin_amdgcn_sched_barrier(0);
+        x_store(Xb + (buf ^ 1) * V3_XBUF);
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    step(B0(), 0);
+    if (t == 0) s_unit[cur ^ 1] = gp_resolve(A, tk, xs, x0, Uall);
+    lds_barrier();
+    PF_TSU(U.u, 2);
+    const int nu = __builtin_amdgcn_readfirstlane(s_unit[cur ^ 1]);
+    const uint32_t ntl = gp_tile_load(A, nu, nblk); /* step 1: the next unit's tile */
+    step(B1(), 1);
+    lds_barrier();
+    PF_TSU(U.u, 3);
+    const uint32_t ngr = gp_group_load(A, ntl);    /* step 2: its group */
+    step(B0(), 2);
+    lds_barrier();
+    PF_TSU(U.u, 4);
+    gp_fill(A, ntl, ngr, nu, nblk, N);
+    const int ntok = gp_tok(A, N, t);              /* step 3: its rows' tokens */
+    step(B1(), 3);
+    lds_barrier();
+    PF_TSU(U.u, 5);
+    if (t < V2_MC) {                                /* step 4: stored, their scales loaded */
+        mn.tok[t] = ntok;
+        mn.slot[t] = N.slot0 + N.m0 + t;
+    }
+    const float nfwd = gp_fwd(A, ntok);
+    step(B0(), 4);
+    lds_barrier();
+    PF_TSU(U.u, 6);
+    if (t < V2_MC) mn.fwd[t] = nfwd;                /* step 5 */
+    step(B1(), 5);
+    lds_barrier();
+    PF_TSU(U.u, 7);
+    int kb = 6;
+    for (; kb + 2 <= nkb - 2; kb += 2) {
+        step(B0(), kb);
+        lds_barrier();
+        step(B1(), kb + 1);
+        lds_barrier();
+    }
+    step(B0(), kb);                           /* kb = nkb - 2 */
+    lds_barrier();
+    PF_TSU(U.u, 8);
+    /* the last step (raw and activation buffer 1), with the next unit's
+     * first activations (all 96 rows; rows >= mlen read row 0) and step 0
+     * weights into buffer 0 */
+    {
+        uint32_t nxo[6];
+#pragma unroll
+        for (int i = 0; i < 6; i++) {
+            const int idx = t + i * V2_T, row = idx >> 5;
+            nxo[i] = 2u * ((uint32_t)mn.tok[row < N.mlen ? row : 0] * (uint32_t)A.H + 8u * (idx & 31));
+        }
+        const uint8_t *nwt = (up ? N.tu : N.tg) + (size_t)(N.j0 / TL_ROWS + rblk) * nkb * TB;
+        __builtin_amdgcn_sched_barrier(0);
+        v8_mfma<MS, Q6>(acc, Xb + V3_XBUF, rg[1], h, [&](int j) {
+            if (j == 0) {
+#pragma unroll
+                for (int i = 0; i < 6; i++) xr[i] = gld_u4(x16 + nxo[i]);
+            }
+            if (j < WS) tile_slice(rg[0], nwt, tlane, j);
+        });
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    PF_TSU(U.u, 9);
+    gu_epilogue<MS, GuMeta, true>(A, mc, acc, U.mlen, U.j0, lds + GP_STAGE);
+    PF_TSU(U.u, 10);
+#pragma unroll
+    for (int i = 0; i < 6; i++) {                   /* the next unit's step 0 activations */
+        const int idx = t + i * V2_T, row = idx >> 5;
+        *(uint4 *)(Xb + row * V2_LD + 8 * (idx & 31)) = xr[i];
+    }
+    lds_barrier();
+    PF_TSU(U.u, 11);
+}
+
+template <bool Q6>
+__device__ __forceinline__ void gp_body(const PfGemmArgs &A, uint8_t *lds, GuMeta (&meta)[2], int *s_unit)
+{
+    const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
+    const int nkb = A.H / GK, nblk = A.I / V2_GU_J;
+    const int Uall = *A.ntiles * nblk;
+    const bool up = n >= 16;
+    constexpr int TB = TL_BYTES(Q6);
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    const int x0 = (int)(xcc & 7);
+    int xs = 0;
+    if (t == 0) {
+        const int old = __hip_atomic_fetch_add(A.gu_ctr + x0, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_unit[0] = gp_resolve(A, old, xs, x0, Uall);
+    }
+    __syncthreads();
+    GuUnit U;
+    {
+        const int u0 = __builtin_amdgcn_readfirstlane(s_unit[0]);
+        if (u0 < 0) return;                         /* workgroup-uniform */
+        const uint32_t tl = gp_tile_load(A, u0, nblk);
+        gp_fill(A, tl, gp_group_load(A, tl), u0, nblk, U);
+    }
+    /* the first unit's meta, step 0 weights and step 0 activations */
+    typename RawOf<Q6>::T rg[2];
+    uint4 xr[6];
+    {
+        const int tv = gp_tok(A, U, t);
+        if (t < V2_MC) {
+            meta[0].tok[t] = tv;
+            meta[0].slot[t] = U.slot0 + U.m0 + t;
+            meta[0].fwd[t] = gp_fwd(A, tv);
+        }
+        const int tlane = ((16 * w + (n & 15)) & (TL_ROWS - 1)) + 32 * h;
+        const uint8_t *wt = (up ? U.tu : U.tg) + (size_t)(U.j0 / TL_ROWS + (16 * w + (n & 15)) / TL_ROWS) * nkb * TB;
+        tile_load(rg[0], wt, tlane);
+        __syncthreads();
+        const uint8_t *x16 = (const uint8_t *)A.X16;
+#pragma unroll
+        for (int i = 0; i < 6; i++) {
+            const int idx = t + i * V2_T, row = idx >> 5;
+            xr[i] = gld_u4(x16 + 2u * ((uint32_t)meta[0].tok[row < U.mlen ? row : 0] * (uint32_t)A.H + 8u * (idx & 31)));
+        }
+        _Float16 *Xb = (_Float16 *)lds;
+#pragma unroll
+        for (int i = 0; i < 6; i++) {
+            const int idx = t + i * V2_T, row = idx >> 5;
+            *(uint4 *)(Xb + row * V2_LD + 8 * (idx & 31)) = xr[i];
+        }
+        lds_barrier();
+    }
+    int cur = 0;
+    for (;;) {
+        GuUnit N;
+        const int ms = (U.mlen + 31) >> 5;
+        if (ms == 1) gp_unit<1, Q6>(A, meta, cur, U, N, s_unit, rg, xr, lds, xs, x0, Uall, nblk);
+        else if (ms == 2) gp_unit<2, Q6>(A, meta, cur, U, N, s_unit, rg, xr, lds, xs, x0, Uall, nblk);
+        else gp_unit<3, Q6>(A, meta, cur, U, N, s_unit, rg, xr, lds, xs, x0, Uall, nblk);
+        if (N.u < 0) break;                         /* workgroup-uniform */
+        U = N;
+        cur ^= 1;
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(V2_T) pf2_gu_pers_kernel(PfGemmArgs A)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds4[];
+    __shared__ GuMeta meta[2];
+    __shared__ int s_unit[2];
+    if (A.gu_pers == 2) gp_body<true>(A, lds4, meta, s_unit);
+    else gp_body<false>(A, lds4, meta, s_unit);
+}
+
 /* Per-row meta of the down GEMM for tile rows [0, mlen): slot, the row's
  * power-of-two scale (from its part maxima) and each part's shift onto it.
  * With fp16 products (A.out16) the row's products are also scaled by 2^-e,
@@ -1070,12 +1395,20 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_bal_kernel(PfGemmArg
 
 /* ---- host ----------------------------------------------------------------- */
 static int g_pf_dn_bal = 1;             /* roaster_prefill_balanced_down */
+static int g_pf_gu_pers = 1;            /* roaster_prefill_persistent_gate_up */
 
 extern "C" int roaster_prefill_balanced_down(int enable)
 {
     std::lock_guard<std::recursive_mutex> g(rt_lock());
     if (enable == 0 || enable == 1) g_pf_dn_bal = enable;
     return g_pf_dn_bal;
+}
+
+extern "C" int roaster_prefill_persistent_gate_up(int enable)
+{
+    std::lock_guard<std::recursive_mutex> g(rt_lock());
+    if (enable == 0 || enable == 1) g_pf_gu_pers = enable;
+    return g_pf_gu_pers;
 }
 
 template <int OP>
@@ -1110,7 +1443,10 @@ int pf_gemm_launch(const PfGemmArgs &A, int max_tiles, int op)
     if (op == PF_BF16) return launch_v1<PF_BF16>(A, max_tiles);
     RtState &R = rt();
     const size_t lds_gu = 2 * (size_t)V3_XBUF * 2, lds_dn = lds_gu;
-    hipLaunchKernelGGL(pf2_gu_kernel, dim3(max_tiles * (A.I / V2_GU_J)), dim3(V2_T), lds_gu, R.stream, A);
+    if (A.gu_pers && g_pf_gu_pers)
+        hipLaunchKernelGGL(pf2_gu_pers_kernel, dim3(R.n_cu), dim3(V2_T), (size_t)GP_LDS, R.stream, A);
+    else
+        hipLaunchKernelGGL(pf2_gu_kernel, dim3(max_tiles * (A.I / V2_GU_J)), dim3(V2_T), lds_gu, R.stream, A);
     if (rt_check(hipGetLastError(), "prefill gate/up launch")) return ROASTER_EDEVICE;
     PfGemmArgs D = A;
     if (A.I <= 2 * GK && g_pf_dn_bal) {

@@ -44,6 +44,9 @@ struct PfGemmArgs {
     int H, I;
     int chunk;                      /* rows per tile of the tile list (pf_gemm_chunk) */
     int dn_nt;                      /* down GEMM: output tiles per workgroup (set by the launcher) */
+    int gu_pers;                    /* fp16 gate/up on the persistent grid: 0 no, 1 every unit Q4_K,
+                                       2 every unit Q6_K (one type for all, H / 256 even and >= 8) */
+    int *gu_ctr;                    /* [8] its work counters, zeroed by the plan kernel */
 };
 
 /* Rows per tile the GEMMs of operand mode op expect in the tile list;

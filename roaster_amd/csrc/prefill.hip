@@ -321,6 +321,7 @@ struct PfPlanArgs {
     const float *dbound;        /* [E + 1] down-row L1 bounds of the layer */
     PfTile *tiles;
     int *ntiles;
+    int *gu_ctr;                /* [8] zeroed for the persistent gate/up GEMM */
     int T, E;
     int chunk;                  /* rows per tile */
 };
@@ -329,6 +330,7 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
 {
     __shared__ int wsum[4];
     const int e = threadIdx.x;
+    if (e < 8) A.gu_ctr[e] = 0;
     const int c = e < A.E ? A.cnt[e] : 0;
     const int nt = (c + A.chunk - 1) / A.chunk;
     int tot_rows, tot_tiles;
@@ -580,6 +582,7 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     pa.dbound = t->dbound + (size_t)layer * (E + 1);
     pa.tiles = (PfTile *)(ws + o_tiles);
     pa.ntiles = (int *)(ws + o_nt);
+    pa.gu_ctr = (int *)(ws + o_nt) + 32;            /* its own cache line of the 256-byte slot */
     pa.T = T; pa.E = E;
     pa.chunk = chunk;
     hipLaunchKernelGGL(pf_plan_kernel, dim3(1), dim3(256), 0, R.stream, pa);
@@ -604,6 +607,16 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     ga.oexp = op == PF_F16 ? (int8_t *)(ws + o_oexp) : nullptr;
     ga.H = H; ga.I = I;
     ga.chunk = chunk;
+    ga.dn_nt = 0;
+    {
+        /* the persistent gate/up grid takes layers whose routed and shared
+         * gate and up matrices share one type and whose K loop has an even
+         * number (>= 8) of super-block steps */
+        const int q = LG.q6[0];
+        const bool one = LG.q6[1] == q && LG.sh_q6[0] == q && LG.sh_q6[1] == q;
+        ga.gu_pers = op == PF_F16 && one && (H / 256) % 2 == 0 && H / 256 >= 8 ? 1 + q : 0;
+        ga.gu_ctr = pa.gu_ctr;
+    }
     if (int rc = pf_gemm_launch(ga, max_tiles, op)) return rc;
 
     if (op == PF_F16)

@@ -57,6 +57,14 @@ def cfg3_oracle(cfg3):
     return cfg3.oracle_layer(0)
 
 
+@pytest.fixture(scope="module")
+def q6tab():
+    log("building the all-Q6_K table (seed 4)")
+    t = SynthTable(4, n_layers=1, q6=(1, 1, 1), sh_q6=(1, 1, 1))
+    yield t
+    t.destroy()
+
+
 def test_prefill_config3_zipf(cfg3, cfg3_oracle):
     """T = 512, Zipf-biased routing (expert lists 0 .. ~200 rows), F16 operands."""
     T = 512
@@ -164,6 +172,27 @@ def test_prefill_balanced_down_bit_exact(cfg3, T):
         Y0, _, ids0, _, _ = prefill(cfg3, X, bias=b)
     finally:
         lib.roaster_prefill_balanced_down(1)
+    np.testing.assert_array_equal(ids0, ids1)
+    np.testing.assert_array_equal(Y0, Y1)
+
+
+@pytest.mark.parametrize("which,T", [("cfg3", 512), ("cfg3", 37), ("q6", 2048)])
+def test_prefill_persistent_gate_up_bit_exact(request, which, T):
+    """The gate/up GEMM on its persistent grid (work counters, the next unit
+    prepared during the current one) gives the bits of one workgroup per
+    unit: Zipf routing on the Q4_K table (tiles of 1..96 rows; T = 37: fewer
+    units than CUs) and the all-Q6_K table at 2048 tokens."""
+    tab = request.getfixturevalue("cfg3" if which == "cfg3" else "q6tab")
+    X = tokens(14, T, start=7000)
+    b = zipf_bias(256, 2) if which == "cfg3" else None
+    lib = R.lib()
+    assert lib.roaster_prefill_persistent_gate_up(-1) == 1
+    Y1, _, ids1, _, _ = prefill(tab, X, bias=b)
+    try:
+        assert lib.roaster_prefill_persistent_gate_up(0) == 0
+        Y0, _, ids0, _, _ = prefill(tab, X, bias=b)
+    finally:
+        lib.roaster_prefill_persistent_gate_up(1)
     np.testing.assert_array_equal(ids0, ids1)
     np.testing.assert_array_equal(Y0, Y1)
 
