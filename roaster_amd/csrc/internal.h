@@ -64,6 +64,8 @@ void rt_unregister_device_range(const void *dev);
 size_t wt_page_size();
 int wt_available();                                   /* 1 if writes can be tracked here */
 int wt_register(uintptr_t start, size_t n);           /* 0: pages of the range now tracked */
+void wt_unregister(uintptr_t start, size_t n);        /* its pages no longer tracked */
+void wt_unregister_all();
 /* Written page runs of the pages overlapping [start, start+n), re-protected
  * in the same walk; 0 ok, -1 if the range cannot be scanned. */
 int wt_scan(uintptr_t start, size_t n, std::vector<std::pair<uintptr_t, uintptr_t>> &runs);

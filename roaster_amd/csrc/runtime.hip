@@ -10,6 +10,8 @@
  */
 #include "internal.h"
 
+#include <algorithm>
+
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -404,7 +406,11 @@ static int twin_sync(Twin &T, uintptr_t h, uintptr_t a, size_t bytes)
     std::vector<std::pair<uintptr_t, uintptr_t>> runs;
     if (wt_scan(p_lo, p_hi - p_lo, runs)) {
         /* The range is no longer tracked (remapped behind the library's back):
-         * copy on every use from now on. */
+         * copy on every use from now on.  The scan may have re-protected
+         * written pages before it failed, so every page of the range counts
+         * as written: every other twin holding one copies it again. */
+        ++g_epoch;
+        for (uintptr_t pg = p_lo; pg < p_hi; pg += P) set_page_ver(pg / P, g_epoch);
         T.tracked = false;
         T.synced.clear();
         return stage_upload(T.dev + (a - h), (const uint8_t *)a, bytes);
@@ -484,6 +490,7 @@ static void free_twin(Twin &T)
 void rt_registry_clear()
 {
     (void)hipDeviceSynchronize();
+    wt_unregister_all();
     for (auto &kv : g_imports) free_twin(kv.second);
     g_imports.clear();
     for (auto &kv : g_regions) free_twin(kv.second);
@@ -567,6 +574,33 @@ extern "C" int kernel_vk_register_region(const void *ptr, size_t size)
  * caller is about to free that memory; weights.c:333-339).  Imports that lie
  * inside a dropped region go with it.  Arena memory is the library's own and
  * is released at shutdown only. */
+/* Pages of the dropped ranges that no remaining twin covers stop being
+ * tracked, so that memory mapped there later is registered afresh. */
+static void untrack_dropped(std::vector<std::pair<uintptr_t, uintptr_t>> &dropped)
+{
+    if (dropped.empty() || !wt_available()) return;
+    const size_t P = wt_page_size();
+    std::vector<std::pair<uintptr_t, uintptr_t>> live;
+    auto add_live = [&](uintptr_t s, size_t n) {
+        if (n) live.push_back(std::make_pair(s & ~(uintptr_t)(P - 1), (s + n + P - 1) & ~(uintptr_t)(P - 1)));
+    };
+    for (auto &ar : g_arenas) add_live((uintptr_t)ar.host, ar.size);
+    for (auto &kv : g_regions) add_live(kv.first, kv.second.size);
+    for (auto &kv : g_imports) add_live(kv.first.first, kv.second.size);
+    std::sort(live.begin(), live.end());
+    for (auto &d : dropped) {
+        uintptr_t at = d.first & ~(uintptr_t)(P - 1);
+        const uintptr_t end = (d.second + P - 1) & ~(uintptr_t)(P - 1);
+        for (auto &lv : live) {
+            if (lv.second <= at) continue;
+            if (lv.first >= end) break;
+            if (lv.first > at) wt_unregister(at, lv.first - at);
+            at = lv.second > at ? lv.second : at;
+        }
+        if (at < end) wt_unregister(at, end - at);
+    }
+}
+
 extern "C" void kernel_vk_release_host_ptr(const void *ptr)
 {
     std::lock_guard<std::recursive_mutex> g(g_lock);
@@ -576,10 +610,12 @@ extern "C" void kernel_vk_release_host_ptr(const void *ptr)
     auto rg = g_regions.find(a);
     if (rg != g_regions.end()) hi = a + rg->second.size;
     bool synced = false;
+    std::vector<std::pair<uintptr_t, uintptr_t>> dropped;
     for (auto it = g_imports.begin(); it != g_imports.end();) {
         const uintptr_t s = it->first.first;
         if (s == a || (s >= lo && s + it->first.second <= hi)) {
             if (!synced) { (void)hipStreamSynchronize(g_rt.stream); synced = true; }
+            dropped.push_back(std::make_pair(s, s + it->first.second));
             free_twin(it->second);
             it = g_imports.erase(it);
         } else {
@@ -588,9 +624,11 @@ extern "C" void kernel_vk_release_host_ptr(const void *ptr)
     }
     if (rg != g_regions.end()) {
         if (!synced) (void)hipStreamSynchronize(g_rt.stream);
+        dropped.push_back(std::make_pair(a, hi));
         free_twin(rg->second);
         g_regions.erase(rg);
     }
+    untrack_dropped(dropped);
 }
 
 /* Bytes copied host -> HBM by the registry since load, and whether writes are

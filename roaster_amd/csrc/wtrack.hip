@@ -226,6 +226,42 @@ int wt_register(uintptr_t start, size_t n)
     return 0;
 }
 
+/* Stop tracking the pages of [start, start + n): they leave the span set, so
+ * a later registration of the same addresses (a new mapping there) is
+ * registered and protected again, and are unregistered from the descriptor
+ * (which fails harmlessly for memory that is no longer mapped). */
+void wt_unregister(uintptr_t start, size_t n)
+{
+    if (g_state <= 0 || !n) return;
+    const size_t P = wt_page_size();
+    const uintptr_t p0 = start & ~(uintptr_t)(P - 1), p1 = (start + n + P - 1) & ~(uintptr_t)(P - 1);
+    auto it = g_spans.upper_bound(p0);
+    if (it != g_spans.begin()) {
+        auto pv = std::prev(it);
+        if (pv->second > p0) it = pv;
+    }
+    std::vector<std::pair<uintptr_t, uintptr_t>> keep;
+    while (it != g_spans.end() && it->first < p1) {
+        if (it->first < p0) keep.push_back(std::make_pair(it->first, p0));
+        if (it->second > p1) keep.push_back(std::make_pair(p1, it->second));
+        it = g_spans.erase(it);
+    }
+    for (auto &k : keep) g_spans[k.first] = k.second;
+    struct uffdio_range r;
+    r.start = p0;
+    r.len = p1 - p0;
+    (void)ioctl(g_uffd, UFFDIO_UNREGISTER, &r);
+}
+
+/* Every span (at shutdown, before the library's own mappings go away). */
+void wt_unregister_all()
+{
+    while (!g_spans.empty()) {
+        const auto sp = *g_spans.begin();
+        wt_unregister(sp.first, sp.second - sp.first);
+    }
+}
+
 int wt_scan(uintptr_t start, size_t n, std::vector<std::pair<uintptr_t, uintptr_t>> &runs)
 {
     if (!wt_available()) return -1;

@@ -6,10 +6,11 @@ on every cache miss reads a new expert into a slot at the same address
 (weights.c:615-645) -- by pread(2), i.e. a write made by the kernel.  In the
 reference the GPU reads that host memory in place (kernels.c:1445-1475), so
 the next kernel_ffn_fused (model.c:1103) or kernel_moe_prefill (model.c:1771)
-computes on the new bytes.  These tests rewrite slots in place, by stores and
-by pread, and require every result to match the oracle run on the bytes the
-host memory holds at the time of the call; both sync modes (write tracking,
-and copy-on-every-use) are exercised.  Tolerances: the reference test's 2e-4
+computes on the new bytes.  These tests rewrite slots in place, by stores, by
+pread and by O_DIRECT pread (weights.c's default), and require every result to
+match the oracle run on the bytes the host memory holds at the time of the
+call; both sync modes (write tracking, and copy-on-every-use) are exercised,
+and a region mapped again at a released region's address is tracked again.  Tolerances: the reference test's 2e-4
 (test_kernels.c:31) for kernel_moe_prefill, 2e-5 for the f32 decode path."""
 import ctypes as C
 import os
@@ -205,3 +206,113 @@ def test_imports_sharing_a_page_see_rewrites(sync_mode):
     buf[A.nbytes - 288:A.nbytes + 144] = new
     run()
     run()
+
+
+def test_region_at_a_reused_address_is_tracked_again():
+    """A region released by kernel_vk_release_host_ptr and unmapped, then a new
+    mapping at the same address registered as a region: its writes are still
+    tracked (a call with no write in between copies nothing, a store copies
+    its page), and every call computes on the bytes the memory holds."""
+    L = R.lib()
+    if not L.roaster_weight_tracking(-1):
+        pytest.skip("write tracking unavailable on this kernel")
+    libc = C.CDLL(None, use_errno=True)
+    libc.mmap.restype = C.c_void_p
+    libc.mmap.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_int, C.c_long]
+    libc.munmap.argtypes = [C.c_void_p, C.c_size_t]
+    PROT_RW, MAP_PRIV_ANON, MAP_FIXED_NOREPLACE = 0x3, 0x02 | 0x20, 0x100000
+    rows = 64
+    A = R.synth_q4k(11, 1, rows * 8)
+    B = R.synth_q4k(11, 2, rows * 8)
+    N = (A.nbytes + 4095) & ~4095
+    x = R.synth_normal(11, 3, 2048)
+    y = np.empty(rows, np.float32)
+
+    def check(p, data):
+        L.kernel_matvec_q4_k(p, x.ctypes.data, y.ctypes.data, rows, 2048)
+        ref = O.matvec(0, np.ascontiguousarray(data), x, rows, 2048)
+        assert rel_err(y, ref) <= 2e-5, rel_err(y, ref)
+
+    p1 = libc.mmap(None, N, PROT_RW, MAP_PRIV_ANON, -1, 0)
+    assert p1 and p1 != C.c_void_p(-1).value
+    _store(p1, A)
+    assert L.kernel_vk_register_region(p1, N) == 1
+    check(p1, A)
+    L.kernel_vk_release_host_ptr(p1)
+    assert libc.munmap(p1, N) == 0
+    p2 = libc.mmap(p1, N, PROT_RW, MAP_PRIV_ANON | MAP_FIXED_NOREPLACE, -1, 0)
+    if p2 != p1:
+        if p2 and p2 != C.c_void_p(-1).value:
+            libc.munmap(p2, N)
+        pytest.skip("the address could not be mapped again")
+    try:
+        _store(p2, B)
+        assert L.kernel_vk_register_region(p2, N) == 1
+        check(p2, B)
+        c0 = _copied()
+        check(p2, B)
+        assert _copied() == c0, "an unwritten region was copied again: its pages are not tracked"
+        C2 = B.copy()
+        C2[144:288] = R.synth_q4k(11, 4, 1)             # one block of row 0
+        _store(p2 + 144, C2[144:288])
+        check(p2, C2)
+        assert 0 < _copied() - c0 <= 4096
+    finally:
+        L.kernel_vk_release_host_ptr(p2)
+        libc.munmap(p2, N)
+
+
+def _pread_direct(p, arr):
+    """Write arr's bytes at the page-aligned host address p with an O_DIRECT
+    pread(2), as weights.c reads experts by default (weights.c:69-74, 686):
+    the kernel writes through the pages it pinned.  False where no
+    directory's filesystem accepts O_DIRECT (tmpfs refuses it)."""
+    n = arr.nbytes
+    assert p % 4096 == 0 and n % 4096 == 0
+    for d in (os.path.dirname(os.path.abspath(__file__)), "/var/tmp", tempfile.gettempdir()):
+        try:
+            fdw, path = tempfile.mkstemp(dir=d)
+        except OSError:
+            continue
+        try:
+            os.write(fdw, np.ascontiguousarray(arr).tobytes())
+            os.fsync(fdw)
+            os.close(fdw)
+            try:
+                fd = os.open(path, os.O_RDONLY | os.O_DIRECT)
+            except OSError:
+                continue
+            try:
+                view = memoryview((C.c_char * n).from_address(p)).cast("B")
+                got = os.preadv(fd, [view], 0)
+            except OSError:
+                continue
+            finally:
+                os.close(fd)
+            if got == n:
+                return True
+        finally:
+            os.unlink(path)
+    return False
+
+
+def test_arena_rewritten_by_o_direct_pread(sync_mode):
+    """Arena memory rewritten by an O_DIRECT pread between two matvec calls:
+    the second call computes on the new bytes."""
+    L = R.lib()
+    rows = 64                                       # 64 x 8 Q4_K blocks: 18 pages
+    A = R.synth_q4k(12, 1, rows * 8)
+    B = R.synth_q4k(12, 2, rows * 8)
+    p = alloc_w(A)
+    x = R.synth_normal(12, 3, 2048)
+    y = np.empty(rows, np.float32)
+
+    def check(data):
+        L.kernel_matvec_q4_k(p, x.ctypes.data, y.ctypes.data, rows, 2048)
+        ref = O.matvec(0, np.ascontiguousarray(data), x, rows, 2048)
+        assert rel_err(y, ref) <= 2e-5, rel_err(y, ref)
+
+    check(A)
+    if not _pread_direct(p, B):
+        pytest.skip("O_DIRECT refused by every candidate directory's filesystem")
+    check(B)
