@@ -77,9 +77,12 @@ static __device__ __forceinline__ int pf_scale_exp(float amax)
     const int s = (int)((__builtin_bit_cast(uint32_t, amax) >> 23) & 255u) - 127 - 14;
     return s < -100 ? -100 : (s > 100 ? 100 : s);
 }
-/* SiLU(g) * u with the hardware exp and reciprocal (a few ulp in f32; the
- * result is rounded to fp16 for the next GEMM anyway). */
-static __device__ __forceinline__ float pf_silu_mul_fast(float g, float u) { return g * __frcp_rn(1.0f + __expf(-g)) * u; }
+/* SiLU(g) * u with the hardware exp and reciprocal (v_exp_f32, v_rcp_f32: a
+ * few ulp in f32; the result is rounded to fp16 for the next GEMM anyway). */
+static __device__ __forceinline__ float pf_silu_mul_fast(float g, float u)
+{
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
 
 /* A workgroup barrier that orders LDS accesses only: every wave's LDS reads
  * and writes complete, global loads may stay in flight (__syncthreads()
@@ -569,12 +572,11 @@ __device__ __forceinline__ void gu_epilogue(const PfGemmArgs &A, const M &meta, 
     float *pmx_s = (float *)(lds + (size_t)MS * 32 * AP * 2); /* [MS * 32][8] */
 #pragma unroll
     for (int ms = 0; ms < MS; ms++) {
-        float fw[8];                                         /* the rows' scales, read together */
+        /* the rows' scales, read together; a row >= mlen reads whatever its
+         * slot holds and its value is replaced by 0 below */
+        float fw[8];
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const int m = 32 * ms + 8 * (q >> 1) + 4 * h + 2 * (q & 1) + (up ? 1 : 0);
-            fw[q] = meta.fwd[m < mlen ? m : 0];
-        }
+        for (int q = 0; q < 8; q++) fw[q] = meta.fwd[32 * ms + 8 * (q >> 1) + 4 * h + 2 * (q & 1) + (up ? 1 : 0)];
 #pragma unroll
         for (int i = 0; i < 16; i += 2) {
             const float v0 = acc[ms][i], v1 = acc[ms][i + 1];
@@ -585,16 +587,17 @@ __device__ __forceinline__ void gu_epilogue(const PfGemmArgs &A, const M &meta, 
             const float got = __builtin_bit_cast(float, (uint32_t)(up ? sw[0] : sw[1]));
             const float gsum = up ? got : mine, usum = up ? mine : got;
             const int m = 32 * ms + 8 * (i >> 2) + 4 * h + (i & 3) + (up ? 1 : 0);
-            float e = 0.0f;
-            if (m < mlen) {
-                const float f = fw[i >> 1];
-                e = pf_silu_mul_fast(gsum * f, usum * f);
-            }
-            float mx = fabsf(e);
-            mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
-            mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
-            mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
-            mx = fmaxf(mx, dpp_f<DPP_MIRROR>(mx));
+            const float f = fw[i >> 1];
+            float e = pf_silu_mul_fast(gsum * f, usum * f);
+            e = m < mlen ? e : 0.0f;                         /* a select: no branch */
+            /* the 16-lane maximum of |e| on the bit patterns (non-negative
+             * floats order as unsigned integers): one DPP max per step */
+            uint32_t mb = __builtin_bit_cast(uint32_t, e) & 0x7FFFFFFFu;
+            mb = max(mb, (uint32_t)dpp_i<DPP_XOR1>((int)mb));
+            mb = max(mb, (uint32_t)dpp_i<DPP_XOR2>((int)mb));
+            mb = max(mb, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)mb));
+            mb = max(mb, (uint32_t)dpp_i<DPP_MIRROR>((int)mb));
+            const float mx = __builtin_bit_cast(float, mb);
             float pinv, pfwd;
             row_scale(mx, pinv, pfwd);
             act_s[m * AP + 16 * w + (n & 15)] = (_Float16)(e * pinv);
