@@ -55,6 +55,18 @@ extern "C" int roaster_pf_ts(unsigned long long *out)
         if (threadIdx.x == 0 && blockIdx.x < 4096) g_pf_ts[blockIdx.x][i] = (v);              \
     } while (0)
 /* the persistent gate/up grid records by unit instead of workgroup */
+/* the balanced down GEMM: [workgroup][event] */
+__device__ unsigned long long g_pf_ts2[256][40];
+extern "C" int roaster_pf_ts2(unsigned long long *out)
+{
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_pf_ts2), sizeof(g_pf_ts2));
+}
+#define PF_TSD(i)                                                                             \
+    do {                                                                                      \
+        const int pf_i_ = (i);                                                                \
+        if (threadIdx.x == 0 && blockIdx.x < 256 && pf_i_ < 40)                               \
+            g_pf_ts2[blockIdx.x][pf_i_] = __builtin_amdgcn_s_memrealtime();                   \
+    } while (0)
 #define PF_TSU(u, i)                                                                          \
     do {                                                                                      \
         if (threadIdx.x == 0 && (u) >= 0 && (u) < 4096) g_pf_ts[u][i] = __builtin_amdgcn_s_memrealtime(); \
@@ -67,6 +79,7 @@ extern "C" int roaster_pf_ts(unsigned long long *out)
 #define PF_TS(i) do { } while (0)
 #define PF_TSV(i, v) do { } while (0)
 #define PF_TSU(u, i) do { } while (0)
+#define PF_TSD(i) do { } while (0)
 #define PF_TSUV(u, i, v) do { } while (0)
 #endif
 
@@ -869,44 +882,61 @@ __device__ __forceinline__ void v5_dn_body(const PfGemmArgs &A, const PfGroup &G
  * current tile computes, with no workgroup barrier after the staging. */
 template <int MS, bool QD>
 __device__ __forceinline__ void v6_dn_body(const PfGemmArgs &A, const PfGroup &G, const V4Shared &meta, int mlen, int n0,
-                                           int nt_count, uint8_t *lds)
+                                           int nt_count, uint8_t *lds, int &ev)
 {
-    const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
+    (void)ev;
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));                 /* addressing computed per unit, not held across units */
+    const int l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
     const int nkb = A.I / GK;                  /* 1 or 2 */
     _Float16 *Xb = (_Float16 *)lds;
     constexpr int TD = TL_BYTES(QD);
-    constexpr int NP = MS * 32 * 64 / V2_T;
+    constexpr int NP = MS * 32 * 32 / V2_T;   /* 16-byte pieces (8 columns) per thread per K step */
     const uint8_t *a16 = (const uint8_t *)A.act16;
-    auto x_stage = [&](int kb, _Float16 *dst) {
-        uint2 xr[NP];
+    uint4 xr[NP];
+    auto x_load = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < NP; i++) {
-            const int idx = t + i * V2_T, row = idx >> 6;
+            const int idx = t + i * V2_T, row = idx >> 5;
             const int slot = meta.slot[row < mlen ? row : 0];
-            xr[i] = gld_u2(a16 + 2 * ((size_t)slot * A.I + kb * GK + 4 * (idx & 63)));
+            xr[i] = gld_u4(a16 + 2 * ((size_t)slot * A.I + kb * GK + 8 * (idx & 31)));
         }
+    };
+    /* each piece onto its part's scale (8 columns lie in one 16-column part),
+     * stored as two 4-column groups at their permuted K positions */
+    auto x_store = [&](int kb, _Float16 *dst) {
 #pragma unroll
         for (int i = 0; i < NP; i++) {
-            const int idx = t + i * V2_T, row = idx >> 6, c4 = 4 * (idx & 63);
-            const int sh = row < mlen ? (int)meta.psh[row][(kb * GK + c4) >> 4] : -200;
-            const f16x4 hv = __builtin_bit_cast(f16x4, xr[i]);
-            const f32x8 e = { __builtin_ldexpf((float)hv[0], sh), __builtin_ldexpf((float)hv[1], sh),
-                              __builtin_ldexpf((float)hv[2], sh), __builtin_ldexpf((float)hv[3], sh),
-                              0.f, 0.f, 0.f, 0.f };
+            const int idx = t + i * V2_T, row = idx >> 5, c8 = 8 * (idx & 31);
+            const int sh = row < mlen ? (int)meta.psh[row][(kb * GK + c8) >> 4] : -200;
+            const f16x8 hv = __builtin_bit_cast(f16x8, xr[i]);
+            f32x8 e;
+#pragma unroll
+            for (int k = 0; k < 8; k++) e[k] = __builtin_ldexpf((float)hv[k], sh);
             const uint4 cu = __builtin_bit_cast(uint4, __builtin_convertvector(e, f16x8));
-            *(uint2 *)(dst + row * V2_LD + perm_slot4(c4)) = make_uint2(cu.x, cu.y);
+            *(uint2 *)(dst + row * V2_LD + perm_slot4(c8)) = make_uint2(cu.x, cu.y);
+            *(uint2 *)(dst + row * V2_LD + perm_slot4(c8 + 4)) = make_uint2(cu.z, cu.w);
         }
     };
     auto tile_base = [&](int nt) {
         return G.td + (size_t)((n0 + nt * V2_DN_N + 32 * w) / TL_ROWS) * nkb * TD;
     };
+    /* each K step's activations are fetched before its weights (a wave's
+     * loads complete in order, so the staging stores wait for the
+     * activations only), and the barrier orders LDS only: the weights stay in
+     * flight */
     typename RawOf<QD>::T r[2];
     const uint8_t *wt = tile_base(0);
+    x_load(0);
     tile_load(r[0], wt, l);
-    if (nkb > 1) tile_load(r[1], wt + TD, l);
-    x_stage(0, Xb);
-    if (nkb > 1) x_stage(1, Xb + V3_XBUF);
-    __syncthreads();
+    x_store(0, Xb);
+    if (nkb > 1) {
+        x_load(1);
+        tile_load(r[1], wt + TD, l);
+        x_store(1, Xb + V3_XBUF);
+    }
+    lds_barrier();
+    PF_TSD(ev++);
     for (int nt = 0; nt < nt_count; nt++) {
         const bool more = nt + 1 < nt_count;
         const uint8_t *wn = tile_base(more ? nt + 1 : nt);
@@ -925,6 +955,7 @@ __device__ __forceinline__ void v6_dn_body(const PfGemmArgs &A, const PfGroup &G
         }
         const int orow = n0 + nt * V2_DN_N + 32 * w + n;
         dn_store_tile<MS>(A, meta, acc, mlen, orow);
+        PF_TSD(ev++);
     }
 }
 
@@ -1303,8 +1334,19 @@ __device__ __forceinline__ void dn_meta(const PfGemmArgs &A, const PfGroup &G, c
     if (t < mlen) {
         const int slot = G.slot0 + tile.m0 + t;
         const int nb = A.I / 16;
+        const float *pr = A.pmax + (size_t)slot * nb;
         float mx = 0.0f;
-        for (int b = 0; b < nb; b++) mx = fmaxf(mx, A.pmax[(size_t)slot * nb + b]);
+        float4 v[8];
+        if (nb <= 32) {
+            /* the row's part maxima in one batch of 16-byte loads (a row is
+             * 16-byte aligned: nb is a multiple of 16) */
+#pragma unroll
+            for (int q = 0; q < 8; q++) v[q] = 4 * q < nb ? gld_f4(pr + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int q = 0; q < 8; q++) mx = fmaxf(fmaxf(fmaxf(mx, v[q].x), fmaxf(v[q].y, v[q].z)), v[q].w);
+        } else {
+            for (int b = 0; b < nb; b++) mx = fmaxf(mx, pr[b]);
+        }
         float inv, fwd;
         row_scale(mx, inv, fwd);
         meta.slot[t] = slot;
@@ -1315,10 +1357,18 @@ __device__ __forceinline__ void dn_meta(const PfGemmArgs &A, const PfGroup &G, c
             meta.fwd[t] = __builtin_bit_cast(float, (uint32_t)(127 + max(-126, min(126, sf))) << 23);
             if (first) A.oexp[slot] = (int8_t)sp;
         }
-        /* shift of part b: exponent of its scale minus the row's (fp16 mode) */
+        /* shift of part b: exponent of its scale minus the row's (fp16 mode);
+         * 2^-64 is 0 in fp16 */
         const int er = pf_scale_exp(mx);
-        for (int b = 0; b < nb && b < V5_MAXPART; b++)
-            meta.psh[t][b] = (int8_t)max(pf_scale_exp(A.pmax[(size_t)slot * nb + b]) - er, -64);   /* 2^-64: 0 in fp16 */
+        auto sh = [&](float pmx) { return (uint32_t)(uint8_t)(int8_t)max(pf_scale_exp(pmx) - er, -64); };
+        if (nb <= 32) {
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (4 * q < nb)
+                    *(uint32_t *)&meta.psh[t][4 * q] = sh(v[q].x) | sh(v[q].y) << 8 | sh(v[q].z) << 16 | sh(v[q].w) << 24;
+        } else {
+            for (int b = 0; b < nb && b < V5_MAXPART; b++) meta.psh[t][b] = (int8_t)sh(pr[b]);
+        }
     }
 }
 
@@ -1338,11 +1388,12 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
     __syncthreads();
     const int ms = (mlen + 31) >> 5;
     const bool whole_k = A.I <= 2 * GK;        /* activations for every K step fit in LDS */
+    int ev = 0;                                /* timestamp build: event index of this workgroup */
 #define DN_CASE(M)                                                                   \
     if (ms == M) {                                                                   \
         if (whole_k) {                                                               \
-            if (G.dq6) v6_dn_body<M, true>(A, G, meta, mlen, n0, nt_count, lds4);   \
-            else v6_dn_body<M, false>(A, G, meta, mlen, n0, nt_count, lds4);        \
+            if (G.dq6) v6_dn_body<M, true>(A, G, meta, mlen, n0, nt_count, lds4, ev); \
+            else v6_dn_body<M, false>(A, G, meta, mlen, n0, nt_count, lds4, ev);    \
         } else {                                                                     \
             if (G.dq6) v5_dn_body<M, true>(A, G, meta, mlen, n0, lds4);             \
             else v5_dn_body<M, false>(A, G, meta, mlen, n0, lds4);                  \
@@ -1372,6 +1423,8 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_bal_kernel(PfGemmArg
     const int U = *A.ntiles * NT;
     const int vb = (Gd & 7) ? b : (b & 7) * (Gd >> 3) + (b >> 3);
     int u = (int)((long long)vb * U / Gd);
+    int ev = 0;
+    PF_TSD(ev++);
     const int u1 = (int)((long long)(vb + 1) * U / Gd);
     while (u < u1) {
         const int ti = u / NT, t0 = u % NT, cnt = min(NT - t0, u1 - u);
@@ -1380,16 +1433,17 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_bal_kernel(PfGemmArg
         const int mlen = min(A.chunk, G.n - tile.m0);
         dn_meta(A, G, tile, mlen, meta, t0 == 0);
         __syncthreads();
+        PF_TSD(ev++);
         const int ms = (mlen + 31) >> 5, n0 = t0 * V2_DN_N;
         if (ms == 1) {
-            if (G.dq6) v6_dn_body<1, true>(A, G, meta, mlen, n0, cnt, lds4);
-            else v6_dn_body<1, false>(A, G, meta, mlen, n0, cnt, lds4);
+            if (G.dq6) v6_dn_body<1, true>(A, G, meta, mlen, n0, cnt, lds4, ev);
+            else v6_dn_body<1, false>(A, G, meta, mlen, n0, cnt, lds4, ev);
         } else if (ms == 2) {
-            if (G.dq6) v6_dn_body<2, true>(A, G, meta, mlen, n0, cnt, lds4);
-            else v6_dn_body<2, false>(A, G, meta, mlen, n0, cnt, lds4);
+            if (G.dq6) v6_dn_body<2, true>(A, G, meta, mlen, n0, cnt, lds4, ev);
+            else v6_dn_body<2, false>(A, G, meta, mlen, n0, cnt, lds4, ev);
         } else {
-            if (G.dq6) v6_dn_body<3, true>(A, G, meta, mlen, n0, cnt, lds4);
-            else v6_dn_body<3, false>(A, G, meta, mlen, n0, cnt, lds4);
+            if (G.dq6) v6_dn_body<3, true>(A, G, meta, mlen, n0, cnt, lds4, ev);
+            else v6_dn_body<3, false>(A, G, meta, mlen, n0, cnt, lds4, ev);
         }
         u += cnt;
         __syncthreads();                        /* meta and the staged activations are rewritten next */
