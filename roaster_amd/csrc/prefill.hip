@@ -179,12 +179,12 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + wv;
     if (t >= A.T) return;
-    /* X row: max |x| and the shared-expert gate dot.  The row (H <= 2048: at
-     * most 8 float4 per lane) and the gate vector are loaded at once, indices
-     * clamped, and the row stays in registers for the fp16 conversion. */
-    /* the token's logits (or router partial sums) are loaded first, so that
-     * they arrive with the X row instead of after its conversion */
-    float v4[4];
+    /* The token's logits (or router partial sums) and biases are loaded
+     * first, then its X row (H <= 2048: at most 8 float4 per lane) and the
+     * gate vector, indices clamped.  A wave's loads complete in order, so
+     * the top 8 runs on the logits while the X row is still arriving; the
+     * row then stays in registers for the fp16 conversion. */
+    float v4[4], b4[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int e = min(lane + 64 * i, A.E - 1);
@@ -195,6 +195,7 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
             const size_t TE = (size_t)A.T * A.E;
             v4[i] = ((A.part[o] + A.part[TE + o]) + A.part[2 * TE + o]) + A.part[3 * TE + o];
         }
+        b4[i] = A.bias ? A.bias[e] : 0.0f;
     }
     const float *x = A.X + (size_t)t * A.H;
     float4 xv[8], gv[8];
@@ -204,6 +205,22 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
         xv[i] = *(const float4 *)(x + k);
         gv[i] = *(const float4 *)(A.gate_inp + k);
     }
+    /* logits (+ bias) and the top 8 */
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int e = lane + 64 * i;
+        float l = -INFINITY;
+        if (e < A.E) {
+            l = v4[i];
+            if (A.bias) l = l + b4[i];
+            if (A.logits_out) A.logits_out[(size_t)t * A.E + e] = l;
+        }
+        v4[i] = l;
+    }
+    if (lane == 0) bad[wv] = 0;
+    __builtin_amdgcn_wave_barrier();
+    topk8_fast(v4, A.E, A.ids + (size_t)t * 8, A.w + (size_t)t * 8, &bad[wv], &ts[wv]);
+    /* X row: max |x|, the shared-expert gate dot, the fp16 copy */
     float mx = 0.0f, dot = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -238,21 +255,6 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
         }
     }
     if (lane == 0) A.sg[t] = 1.0f / (1.0f + expf(-dot));
-    /* logits (+ bias) */
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int e = lane + 64 * i;
-        float l = -INFINITY;
-        if (e < A.E) {
-            l = v4[i];
-            if (A.bias) l = l + A.bias[e];
-            if (A.logits_out) A.logits_out[(size_t)t * A.E + e] = l;
-        }
-        v4[i] = l;
-    }
-    if (lane == 0) bad[wv] = 0;
-    __builtin_amdgcn_wave_barrier();
-    topk8_fast(v4, A.E, A.ids + (size_t)t * 8, A.w + (size_t)t * 8, &bad[wv], &ts[wv]);
     if (lane < 8) {
         if (A.ids_out) A.ids_out[(size_t)t * 8 + lane] = A.ids[(size_t)t * 8 + lane];
         if (A.w_out) A.w_out[(size_t)t * 8 + lane] = A.w[(size_t)t * 8 + lane];
