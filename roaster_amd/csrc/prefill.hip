@@ -2,7 +2,7 @@
  * prefill.hip -- the MoE block over T tokens (model.c:1671-1791) on the GPU.
  *
  *   pf_router_mfma_kernel  logits = X . W_r^T in f32 on v_mfma_f32_32x32x2_f32,
- *                      split over K into 4 partial sums added in fixed order
+ *                      split over K into 8 partial sums added in fixed order
  *                      by the token kernel (model.c:1679)
  *   pf_token_kernel    one wave per token: logits (+ bias), top-8 and
  *                      renormalised weights (model.c:1681-1692), the shared
@@ -32,7 +32,7 @@
 #include <string.h>
 
 #define PF_MAX_T (1 << 16)
-#define RT_KSPLIT 4               /* router K split */
+#define RT_KSPLIT 8               /* router K split */
 
 /* Natural position p (multiple of 4) inside a super-block -> the slot of its
  * first element in the fp16 GEMM's permuted K order (pf_gemm.hip). */
@@ -193,7 +193,13 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
             v4[i] = A.logits_in[o];
         } else {
             const size_t TE = (size_t)A.T * A.E;
-            v4[i] = ((A.part[o] + A.part[TE + o]) + A.part[2 * TE + o]) + A.part[3 * TE + o];
+            float p[RT_KSPLIT];
+#pragma unroll
+            for (int s = 0; s < RT_KSPLIT; s++) p[s] = A.part[s * TE + o];
+            float sum = p[0];
+#pragma unroll
+            for (int s = 1; s < RT_KSPLIT; s++) sum += p[s];
+            v4[i] = sum;
         }
         b4[i] = A.bias ? A.bias[e] : 0.0f;
     }
