@@ -256,6 +256,7 @@ __global__ void __launch_bounds__(GT) pf_down_kernel(PfGemmArgs A)
 #define V2_W 8                    /* waves */
 #define V2_GU_J (16 * V2_W)       /* gate/up j columns per workgroup */
 #define V2_DN_N (32 * V2_W)       /* down output rows per workgroup */
+static_assert(V2_DN_N == PF_DN_ROWS, "the down GEMM's unit is the plan kernel's");
 #define V2_MC 96                  /* rows per tile */
 #define V2_LD (GK + 8)            /* LDS row stride (fp16 elements) */
 #ifndef PF_DN_NT
@@ -782,12 +783,15 @@ __device__ __forceinline__ void v5_gu_body(const PfGemmArgs &A, const PfGroup &G
  * lanes n and n ^ 1 swap one value of each row pair (i, i + 1), so the even
  * lane stores row i's columns (n, n + 1) and the odd lane row i + 1's as one
  * 4-byte store: half the store instructions. */
-template <int MS>
+template <int MS, bool ALL = false>
 __device__ __forceinline__ void dn_store_tile(const PfGemmArgs &A, const V4Shared &meta, const f32x16 (&acc)[MS],
                                               int mlen, int orow)
 {
+    /* ALL: fp16 products, every row stored (rows past the tile's end carry
+     * the spare slot), no branches */
+    if constexpr (ALL) mlen = MS * 32;
     const int l = threadIdx.x & 63, h = l >> 5;
-    if (!A.out16) {
+    if (!ALL && !A.out16) {
 #pragma unroll
         for (int ms = 0; ms < MS; ms++)
 #pragma unroll
@@ -1372,6 +1376,139 @@ __device__ __forceinline__ void dn_meta(const PfGemmArgs &A, const PfGroup &G, c
     }
 }
 
+/* Tile ti's down record spread over the wave: lane k holds its dword k (k < 8). */
+__device__ __forceinline__ uint32_t dn_rec_load(const PfGemmArgs &A, int ti)
+{
+    return gld_u32((const uint32_t *)(A.dn_tiles + ti) + (threadIdx.x & 7));
+}
+
+/* One tile range of the balanced down GEMM (inter <= 512): dn_meta's row
+ * meta, the activation staging and the output tiles of v6_dn_body, with the
+ * range's loads issued as one batch in the order their data is needed — the
+ * rows' part maxima, both K steps' activations, then the first output tile's
+ * weights — so that the maxima and the activations (L2) return without
+ * waiting behind the weights (HBM): a wave's loads complete in order.  The
+ * part maxima are spread over the workgroup, four parts (one 16-byte load)
+ * per thread and up to two pieces each: piece p holds parts 4 (p % ppr) ..
+ * + 3 of row p / ppr, ppr = inter / 64, and the row maximum is taken over the
+ * row's ppr neighbouring lanes by DPP (fmaxf, so the order does not change
+ * it).  An activation row's slot is the tile's first slot plus the row. */
+template <int MS, bool QD, int NKB>
+__device__ __forceinline__ void v7_dn_range(const PfGemmArgs &A, const uint8_t *td, int sbase, int mlen, float dbnd,
+                                            V4Shared &meta, int n0, int nt_count, bool first, int nti, uint32_t &rec,
+                                            uint8_t *lds, int &ev)
+{
+    (void)ev;
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));                 /* addressing computed per range, not held across ranges */
+    const int l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
+    constexpr int nkb = NKB;                   /* K steps: inter / 256, 1 or 2 */
+    constexpr int nb = 16 * NKB, lp = NKB == 2 ? 3 : 2, ppr = 1 << lp;
+    _Float16 *Xb = (_Float16 *)lds;
+    constexpr int TD = TL_BYTES(QD);
+    constexpr int NP = MS * 32 * 32 / V2_T;   /* 16-byte pieces (8 columns) per thread per K step */
+    const uint8_t *a16 = (const uint8_t *)A.act16;
+    float4 pm[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int p = t + V2_T * i, row = p >> lp;
+        pm[i] = gld_f4(A.pmax + (size_t)(sbase + (row < mlen ? row : 0)) * nb + 4 * (p & (ppr - 1)));
+    }
+    uint4 xr[2][NP];
+    auto x_load = [&](int kb, uint4 (&dst)[NP]) {
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int idx = t + i * V2_T, row = idx >> 5;
+            dst[i] = gld_u4(a16 + 2 * ((size_t)(sbase + (row < mlen ? row : 0)) * A.I + kb * GK + 8 * (idx & 31)));
+        }
+    };
+    auto x_store = [&](int kb, const uint4 (&src)[NP], _Float16 *dst) {
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int idx = t + i * V2_T, row = idx >> 5, c8 = 8 * (idx & 31);
+            const int sh = row < mlen ? (int)meta.psh[row][(kb * GK + c8) >> 4] : -200;
+            const f16x8 hv = __builtin_bit_cast(f16x8, src[i]);
+            f32x8 e;
+#pragma unroll
+            for (int k = 0; k < 8; k++) e[k] = __builtin_ldexpf((float)hv[k], sh);
+            const uint4 cu = __builtin_bit_cast(uint4, __builtin_convertvector(e, f16x8));
+            *(uint2 *)(dst + row * V2_LD + perm_slot4(c8)) = make_uint2(cu.x, cu.y);
+            *(uint2 *)(dst + row * V2_LD + perm_slot4(c8 + 4)) = make_uint2(cu.z, cu.w);
+        }
+    };
+    auto tile_base = [&](int nt) {
+        return td + (size_t)((n0 + nt * V2_DN_N + 32 * w) / TL_ROWS) * nkb * TD;
+    };
+    x_load(0, xr[0]);
+    if constexpr (NKB > 1) x_load(1, xr[1]);
+    typename RawOf<QD>::T r[2];
+    const uint8_t *wt = tile_base(0);
+    tile_load(r[0], wt, l);
+    if constexpr (NKB > 1) tile_load(r[1], wt + TD, l);
+    rec = dn_rec_load(A, nti);                  /* the next range's record, read at its start */
+    /* the rows' meta (dn_meta's values) */
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int p = t + V2_T * i, row = p >> lp, q = p & (ppr - 1);
+        const float4 v = pm[i];
+        float mx = fmaxf(fmaxf(fmaxf(0.0f, v.x), fmaxf(v.y, v.z)), v.w);
+        mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
+        mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
+        if constexpr (ppr == 8) mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
+        if (row < mlen) {
+            const int er = pf_scale_exp(mx);
+            auto sh = [&](float pmx) { return (uint32_t)(uint8_t)(int8_t)max(pf_scale_exp(pmx) - er, -64); };
+            *(uint32_t *)&meta.psh[row][4 * q] = sh(v.x) | sh(v.y) << 8 | sh(v.z) << 16 | sh(v.w) << 24;
+            if (q == 0) {
+                const int slot = sbase + row;
+                float inv, fwd;
+                row_scale(mx, inv, fwd);
+                meta.slot[row] = slot;
+                meta.inv[row] = inv;
+                meta.fwd[row] = fwd;
+                if (A.out16) {
+                    const int sp = pf_scale_exp(mx * dbnd), sf = er - sp;
+                    meta.fwd[row] = __builtin_bit_cast(float, (uint32_t)(127 + max(-126, min(126, sf))) << 23);
+                    if (first) A.oexp[slot] = (int8_t)sp;
+                }
+            }
+        } else if (row < MS * 32 && q == 0) {
+            meta.slot[row] = A.dn_spare;
+            meta.fwd[row] = 0.0f;
+        }
+    }
+    lds_barrier();                              /* the meta, for the staging and the stores */
+    PF_TSD(ev++);
+    x_store(0, xr[0], Xb);
+    if constexpr (NKB > 1) x_store(1, xr[1], Xb + V3_XBUF);
+    lds_barrier();                              /* the weights stay in flight */
+    PF_TSD(ev++);
+    /* the next output tile's weights are loaded unconditionally (the last
+     * tile reloads its own, from L2) and every row is stored (rows past the
+     * tile's end to the spare slot): with a fixed set of loads and stores per
+     * tile the compiler's waits count exactly, and each K step waits for its
+     * own weights only, not for the next step's or the last tile's stores */
+    for (int nt = 0; nt < nt_count; nt++) {
+        const uint8_t *wn = tile_base(nt + 1 < nt_count ? nt + 1 : nt);
+        f32x16 acc[MS];
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++) acc[ms] = (f32x16){};
+        __builtin_amdgcn_sched_barrier(0);
+        v4_mfma<MS, QD>(acc, Xb, r[0], h);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_load(r[0], wn, l);
+        if constexpr (NKB > 1) {
+            __builtin_amdgcn_sched_barrier(0);
+            v4_mfma<MS, QD>(acc, Xb + V3_XBUF, r[1], h);
+            __builtin_amdgcn_sched_barrier(0);
+            tile_load(r[1], wn + TD, l);
+        }
+        const int orow = n0 + nt * V2_DN_N + 32 * w + n;
+        dn_store_tile<MS, true>(A, meta, acc, mlen, orow);
+        PF_TSD(ev++);
+    }
+}
+
 extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds4[];
@@ -1408,45 +1545,64 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_kernel(PfGemmArgs A)
 
 /* The down GEMM for inter <= 512 on a fixed grid (one workgroup per CU): the
  * (tile, 256-row output tile) units, tile-major, are split into gridDim.x
- * contiguous ranges of equal length, so every workgroup does the same number
- * of output tiles and no last wave of workgroups runs on a few CUs while the
- * rest idle.  A range crosses at most a few tiles; each piece is walked like
- * pf2_down_kernel's nt_count tiles (activations staged once, the next output
- * tile's weights loaded during the current one's MFMA work).  Workgroups of
- * one XCD (grid dealt round-robin over the 8 XCDs) take neighbouring ranges,
- * so the activation rows of a tile are fetched into one L2. */
+ * contiguous ranges of about equal cost (the plan kernel's bounds, from a
+ * cost per unit that grows with the tile's 32-row blocks plus one per tile
+ * range started), so no last wave of workgroups runs on a few CUs while the
+ * rest idle.  A range crosses at most a few tiles; each piece is one
+ * v7_dn_range (meta and activations staged once, the next output tile's
+ * weights loaded during the current one's MFMA work), its tile record loaded
+ * during the piece before.  Workgroups of one XCD (grid dealt round-robin
+ * over the 8 XCDs) take neighbouring ranges, so the activation rows of a
+ * tile are fetched into one L2. */
 extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_bal_kernel(PfGemmArgs A)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds4[];
     __shared__ V4Shared meta;
     const int NT = A.H / V2_DN_N, Gd = (int)gridDim.x, b = blockIdx.x;
-    const int U = *A.ntiles * NT;
     const int vb = (Gd & 7) ? b : (b & 7) * (Gd >> 3) + (b >> 3);
-    int u = (int)((long long)vb * U / Gd);
+    int u, u1;
+    if (A.dn_bnd) {
+        u = A.dn_bnd[vb];
+        u1 = A.dn_bnd[vb + 1];
+    } else {
+        const int U = *A.ntiles * NT;
+        u = (int)((long long)vb * U / Gd);
+        u1 = (int)((long long)(vb + 1) * U / Gd);
+    }
     int ev = 0;
     PF_TSD(ev++);
-    const int u1 = (int)((long long)(vb + 1) * U / Gd);
+    /* each range's record is loaded during the range before it (the first
+     * here), so a range starts with its loads, not a chain of lookups */
+    uint32_t rec = dn_rec_load(A, u < u1 ? u / NT : 0);
     while (u < u1) {
         const int ti = u / NT, t0 = u % NT, cnt = min(NT - t0, u1 - u);
-        const PfTile tile = A.tiles[ti];
-        const PfGroup &G = A.groups[tile.grp];
-        const int mlen = min(A.chunk, G.n - tile.m0);
-        dn_meta(A, G, tile, mlen, meta, t0 == 0);
-        __syncthreads();
-        PF_TSD(ev++);
+        const int nti = u + cnt < u1 ? (u + cnt) / NT : ti;
+        auto field = [&](size_t off) { return __builtin_amdgcn_readlane((int)rec, (int)(off / 4)); };
+        const uint8_t *td = (const uint8_t *)(((uint64_t)(uint32_t)field(offsetof(PfDnTile, td) + 4) << 32) |
+                                              (uint32_t)field(offsetof(PfDnTile, td)));
+        const int sbase = field(offsetof(PfDnTile, slot)), mlen = field(offsetof(PfDnTile, mlen));
+        const bool dq6 = field(offsetof(PfDnTile, dq6)) != 0;
+        const float dbnd = __builtin_bit_cast(float, field(offsetof(PfDnTile, dbnd)));
         const int ms = (mlen + 31) >> 5, n0 = t0 * V2_DN_N;
+        const bool first = t0 == 0;
+#define DN_RANGE(M, Q)                                                                          \
+    do {                                                                                        \
+        if (A.I > GK) v7_dn_range<M, Q, 2>(A, td, sbase, mlen, dbnd, meta, n0, cnt, first, nti, rec, lds4, ev); \
+        else v7_dn_range<M, Q, 1>(A, td, sbase, mlen, dbnd, meta, n0, cnt, first, nti, rec, lds4, ev);          \
+    } while (0)
         if (ms == 1) {
-            if (G.dq6) v6_dn_body<1, true>(A, G, meta, mlen, n0, cnt, lds4, ev);
-            else v6_dn_body<1, false>(A, G, meta, mlen, n0, cnt, lds4, ev);
+            if (dq6) DN_RANGE(1, true);
+            else DN_RANGE(1, false);
         } else if (ms == 2) {
-            if (G.dq6) v6_dn_body<2, true>(A, G, meta, mlen, n0, cnt, lds4, ev);
-            else v6_dn_body<2, false>(A, G, meta, mlen, n0, cnt, lds4, ev);
+            if (dq6) DN_RANGE(2, true);
+            else DN_RANGE(2, false);
         } else {
-            if (G.dq6) v6_dn_body<3, true>(A, G, meta, mlen, n0, cnt, lds4, ev);
-            else v6_dn_body<3, false>(A, G, meta, mlen, n0, cnt, lds4, ev);
+            if (dq6) DN_RANGE(3, true);
+            else DN_RANGE(3, false);
         }
+#undef DN_RANGE
         u += cnt;
-        __syncthreads();                        /* meta and the staged activations are rewritten next */
+        lds_barrier();                          /* meta and the staged activations are rewritten next */
     }
 }
 
@@ -1506,7 +1662,7 @@ int pf_gemm_launch(const PfGemmArgs &A, int max_tiles, int op)
         hipLaunchKernelGGL(pf2_gu_kernel, dim3(max_tiles * (A.I / V2_GU_J)), dim3(V2_T), lds_gu, R.stream, A);
     if (rt_check(hipGetLastError(), "prefill gate/up launch")) return ROASTER_EDEVICE;
     PfGemmArgs D = A;
-    if (A.I <= 2 * GK && g_pf_dn_bal) {
+    if (A.I <= 2 * GK && g_pf_dn_bal && A.dn_bnd && A.dn_tiles && A.out16) {
         /* every K step's activations fit in LDS: one workgroup per CU over an
          * even split of the output tiles */
         D.dn_nt = 0;

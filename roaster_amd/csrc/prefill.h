@@ -27,6 +27,16 @@ struct PfTile {
     int grp, m0;
 };
 
+/* A tile as the balanced down GEMM reads it (one record, no group lookup). */
+struct PfDnTile {
+    const uint8_t *td;              /* the group's down matrix in the tile layout */
+    int slot;                       /* slot of the tile's first row */
+    int mlen;                       /* rows */
+    int dq6;                        /* down type Q6_K */
+    float dbnd;                     /* the group's dbnd */
+    int pad[2];
+};
+
 struct PfGemmArgs {
     const PfGroup *groups;
     const PfTile *tiles;
@@ -47,7 +57,22 @@ struct PfGemmArgs {
     int gu_pers;                    /* fp16 gate/up on the persistent grid: 0 no, 1 every unit Q4_K,
                                        2 every unit Q6_K (one type for all, H / 256 even and >= 8) */
     int *gu_ctr;                    /* [8] its work counters, zeroed by the plan kernel */
+    const int *dn_bnd;              /* [n_cu + 1] first unit of each workgroup of the balanced down
+                                       GEMM, written by the plan kernel (with dn_tiles), or NULL */
+    const PfDnTile *dn_tiles;       /* [max_tiles] the tile list as down records, or NULL */
+    int dn_spare;                   /* with dn_tiles: a slot past the last, which takes the balanced down
+                                       GEMM's products of rows past a tile's end (never read) */
 };
+
+/* The balanced down GEMM's units are (tile, PF_DN_ROWS output rows); the plan
+ * kernel splits them over the workgroups by a cost model measured on the
+ * all-Q6_K and Zipf 2048-wide layers (units of about 0.5 us): a unit of a tile
+ * with ms 32-row blocks costs PF_DN_CA + PF_DN_CB * ms, a tile range's start
+ * (row scales and activation staging) PF_DN_CP more. */
+#define PF_DN_ROWS 256
+#define PF_DN_CA 4
+#define PF_DN_CB 3
+#define PF_DN_CP 24
 
 /* Rows per tile the GEMMs of operand mode op expect in the tile list;
  * mixed_gate_up: the gate and up matrices of some group differ in type. */

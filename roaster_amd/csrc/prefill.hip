@@ -330,20 +330,76 @@ struct PfPlanArgs {
     PfTile *tiles;
     int *ntiles;
     int *gu_ctr;                /* [8] zeroed for the persistent gate/up GEMM */
+    int *dn_bnd;                /* [n_wg + 1] the balanced down GEMM's split, or NULL */
+    PfDnTile *dn_tiles;         /* the tile list as down records (with dn_bnd) */
+    int n_wg;                   /* its workgroups */
+    int nt_out;                 /* its units per tile: H / PF_DN_ROWS */
     int T, E;
     int chunk;                  /* rows per tile */
 };
 
+/* Cost of the down-GEMM units of a group of c rows cut into tiles of chunk
+ * rows (the start of each tile counted as a range start). */
+__device__ __forceinline__ int pf_dn_tile_cost(int rows, int nt_out)
+{
+    return PF_DN_CP + nt_out * (PF_DN_CA + PF_DN_CB * ((rows + 31) >> 5));
+}
+__device__ __forceinline__ int pf_dn_group_cost(int c, int chunk, int nt_out)
+{
+    if (c <= 0) return 0;
+    const int nt = (c + chunk - 1) / chunk;
+    return (nt - 1) * pf_dn_tile_cost(chunk, nt_out) + pf_dn_tile_cost(c - (nt - 1) * chunk, nt_out);
+}
+
+/* Three exclusive prefix sums over a 256-thread workgroup in one pass (one
+ * LDS exchange); *total gets the sums. */
+__device__ int3 block_scan3_256(int3 v, int *lds, int3 *total)
+{
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int3 inc = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int ox = __shfl_up(inc.x, d), oy = __shfl_up(inc.y, d), oz = __shfl_up(inc.z, d);
+        if (lane >= d) { inc.x += ox; inc.y += oy; inc.z += oz; }
+    }
+    if (lane == 63) { lds[w] = inc.x; lds[4 + w] = inc.y; lds[8 + w] = inc.z; }
+    __syncthreads();
+    int3 before = make_int3(0, 0, 0), all = make_int3(0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int cx = lds[i], cy = lds[4 + i], cz = lds[8 + i];
+        if (i < w) { before.x += cx; before.y += cy; before.z += cz; }
+        all.x += cx; all.y += cy; all.z += cz;
+    }
+    __syncthreads();
+    *total = all;
+    return make_int3(before.x + inc.x - v.x, before.y + inc.y - v.y, before.z + inc.z - v.z);
+}
+
 extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
 {
-    __shared__ int wsum[4];
+    __shared__ int wsum[12];
+    __shared__ int s_gc[258], s_toff[257], s_c[257];
     const int e = threadIdx.x;
     if (e < 8) A.gu_ctr[e] = 0;
+    /* every global read first (their latencies overlap) */
     const int c = e < A.E ? A.cnt[e] : 0;
+    const float dbnd = e < A.E ? A.dbound[e] : 0.0f, sdbnd = A.dbound[A.E];
     const int nt = (c + A.chunk - 1) / A.chunk;
-    int tot_rows, tot_tiles;
-    const int off = block_scan_256(c, wsum, &tot_rows);
-    const int toff = block_scan_256(nt, wsum, &tot_tiles);
+    const int cost = A.dn_bnd && e < A.E ? pf_dn_group_cost(c, A.chunk, A.nt_out) : 0;
+    int3 tot;
+    const int3 pre = block_scan3_256(make_int3(c, nt, cost), wsum, &tot);
+    const int off = pre.x, toff = pre.y, tot_tiles = tot.y;
+    const int nsh = (A.T + A.chunk - 1) / A.chunk;
+    if (A.dn_bnd) {
+        /* the balanced down GEMM's cost prefix over groups 0..E-1 (routed)
+         * and E (shared), each tile a range start plus its units */
+        if (e < A.E) { s_gc[e] = pre.z; s_toff[e] = toff; s_c[e] = c; }
+        if (e == 0) {
+            s_gc[A.E] = tot.z; s_toff[A.E] = tot_tiles; s_c[A.E] = A.T;
+            s_gc[A.E + 1] = tot.z + pf_dn_group_cost(A.T, A.chunk, A.nt_out);
+        }
+    }
     if (e < A.E) {
         A.off[e] = off;
         if (A.counts_out) A.counts_out[e] = c;
@@ -359,11 +415,13 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
         G.slot0 = off;
         G.tok0 = 0;
         G.tok = A.list + (size_t)e * A.T;
-        G.dbnd = A.dbound[e];
+        G.dbnd = dbnd;
         A.groups[e] = G;
         for (int i = 0; i < nt; i++) A.tiles[toff + i] = PfTile{ e, i * A.chunk };
+        if (A.dn_bnd)
+            for (int i = 0; i < nt; i++)
+                A.dn_tiles[toff + i] = PfDnTile{ G.td, off + i * A.chunk, min(A.chunk, c - i * A.chunk), G.dq6, dbnd, { 0, 0 } };
     }
-    const int nsh = (A.T + A.chunk - 1) / A.chunk;
     if (e == 0) {
         PfGroup G;
         G.g = A.L.sgate; G.u = A.L.sup; G.d = A.L.sdown;
@@ -373,11 +431,43 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
         G.slot0 = 8 * A.T;
         G.tok0 = 0;
         G.tok = nullptr;
-        G.dbnd = A.dbound[A.E];
+        G.dbnd = sdbnd;
         A.groups[A.E] = G;
         *A.ntiles = tot_tiles + nsh;
     }
-    for (int i = e; i < nsh; i += 256) A.tiles[tot_tiles + i] = PfTile{ A.E, i * A.chunk };
+    for (int i = e; i < nsh; i += 256) {
+        A.tiles[tot_tiles + i] = PfTile{ A.E, i * A.chunk };
+        if (A.dn_bnd)
+            A.dn_tiles[tot_tiles + i] = PfDnTile{ A.TL.sdown, 8 * A.T + i * A.chunk, min(A.chunk, A.T - i * A.chunk),
+                                                  A.sq6d, sdbnd, { 0, 0 } };
+    }
+    if (A.dn_bnd) {
+        /* the balanced down GEMM's split: workgroup b starts at the unit
+         * where the cost prefix reaches b / n_wg of the total; the bounds are
+         * non-decreasing in b, so the ranges cover every unit once */
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   /* LDS only: the stores stay in flight */
+        const int ctot = s_gc[A.E + 1];
+        const bool narrow = (unsigned long long)ctot * (unsigned)A.n_wg < (1ull << 32);
+        const int full = pf_dn_tile_cost(A.chunk, A.nt_out);
+        for (int b = e; b <= A.n_wg; b += 256) {
+            int u = (tot_tiles + nsh) * A.nt_out;
+            if (b < A.n_wg) {
+                const int cpos = narrow ? (int)((unsigned)b * (unsigned)ctot / (unsigned)A.n_wg)
+                                        : (int)((long long)b * ctot / A.n_wg);
+                int lo = 0, hi = A.E;              /* the last group g <= E with s_gc[g] <= cpos */
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (s_gc[mid] <= cpos) lo = mid; else hi = mid - 1;
+                }
+                const int g = lo, cg = s_c[g], ntg = (cg + A.chunk - 1) / A.chunk, go = cpos - s_gc[g];
+                const int i = min(go / full, ntg - 1);
+                const int rows = i < ntg - 1 ? A.chunk : cg - i * A.chunk;
+                const int uc = PF_DN_CA + PF_DN_CB * ((rows + 31) >> 5), rem = go - i * full - PF_DN_CP;
+                u = (s_toff[g] + i) * A.nt_out + (rem <= 0 ? 0 : min(A.nt_out, (rem + uc - 1) / uc));
+            }
+            A.dn_bnd[b] = u;
+        }
+    }
 }
 
 /* ---- combine -------------------------------------------------------------- */
@@ -536,12 +626,14 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     const size_t o_cnt = take((size_t)E * 4), o_off = take((size_t)E * 4), o_list = take((size_t)E * TT * 4);
     const size_t o_grp = take(sizeof(PfGroup) * (E + 1)), o_tiles = take(sizeof(PfTile) * max_tiles);
     const size_t o_nt = take(4), o_pmax = take(slots * (size_t)(I / 16) * 4);
-    const size_t o_act = take(slots * I * 4), o_ed = take(slots * H * (op == PF_F16 ? 2 : 4));
+    const size_t o_act = take(slots * I * 4), o_ed = take((slots + 1) * H * (op == PF_F16 ? 2 : 4));
     const size_t o_oexp = op == PF_F16 ? take(slots) : 0;
+    RtState &R = rt();
+    const size_t o_bnd = op == PF_F16 ? take((size_t)(R.n_cu + 1) * 4) : 0;
+    const size_t o_dnt = op == PF_F16 ? take(sizeof(PfDnTile) * max_tiles) : 0;
     uint8_t *ws = (uint8_t *)rt_scratch(SCR_PF, sz);
     unsigned *ctrl = rt_ctrl();
     if (!ws || !ctrl) return ROASTER_ENOMEM;
-    RtState &R = rt();
     const DecLayer &L = t->layers_h[layer];
 
     if (!opt.logits_in) {
@@ -591,6 +683,10 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     pa.tiles = (PfTile *)(ws + o_tiles);
     pa.ntiles = (int *)(ws + o_nt);
     pa.gu_ctr = (int *)(ws + o_nt) + 32;            /* its own cache line of the 256-byte slot */
+    pa.dn_bnd = op == PF_F16 ? (int *)(ws + o_bnd) : nullptr;
+    pa.dn_tiles = op == PF_F16 ? (PfDnTile *)(ws + o_dnt) : nullptr;
+    pa.n_wg = R.n_cu;
+    pa.nt_out = H / PF_DN_ROWS;
     pa.T = T; pa.E = E;
     pa.chunk = chunk;
     hipLaunchKernelGGL(pf_plan_kernel, dim3(1), dim3(256), 0, R.stream, pa);
@@ -616,6 +712,9 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     ga.H = H; ga.I = I;
     ga.chunk = chunk;
     ga.dn_nt = 0;
+    ga.dn_bnd = pa.dn_bnd;
+    ga.dn_tiles = pa.dn_tiles;
+    ga.dn_spare = (int)slots;                    /* o_ed holds one row past the slots */
     {
         /* the persistent gate/up grid takes layers whose routed and shared
          * gate and up matrices share one type and whose K loop has an even
