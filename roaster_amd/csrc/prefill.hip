@@ -474,39 +474,33 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 
 /* Token t's routed slots and weights in ascending expert id (sl = -1 for an
- * unrouted pick). */
+ * unrouted pick).  Lane k of each wave (k < 8) holds pick k: its id, weight
+ * and slot (off[id] + its rank, rank indexed by (t, k)); its place in the
+ * ascending order of (id, k) — ids of one token are distinct, -1 marks an
+ * unrouted pick — is the count of picks before it, and entry p is read out
+ * of the lane whose place is p.  All loads are issued unconditionally, in
+ * two round trips (picks, then offsets). */
 __device__ __forceinline__ void pf_token_slots(const int *ids, const float *w, const int *rank, const int *off, int t,
                                                int (&sl)[8], float (&wt)[8])
 {
-    int id[8], rk[8], id0[8];
+    const int lane = (int)threadIdx.x & 63, k = lane & 7;
+    const int id = ids[(size_t)t * 8 + k];
+    const float wk = w[(size_t)t * 8 + k];
+    const int rk = rank[(size_t)t * 8 + k];
+    const int of = off[id >= 0 ? id : 0];
+    const int s = id >= 0 ? of + rk : -1;
+    int pos = 0;
 #pragma unroll
-    for (int k = 0; k < 8; k++) {       /* the token's ids, weights and ranks in one round trip */
-        id[k] = ids[(size_t)t * 8 + k];
-        wt[k] = w[(size_t)t * 8 + k];
-        rk[k] = rank[(size_t)t * 8 + k];
+    for (int j = 0; j < 8; j++) {
+        const int ij = __builtin_amdgcn_readlane(id, j);
+        pos += ij < id || (ij == id && j < k) ? 1 : 0;
     }
 #pragma unroll
-    for (int k = 0; k < 8; k++) id0[k] = id[k];
-    /* ascending expert id (ids of one token are distinct; -1 = unrouted) */
-#pragma unroll
-    for (int i = 1; i < 8; i++)
-#pragma unroll
-        for (int j = i; j > 0; j--)
-            if (id[j] < id[j - 1]) {
-                const int ti = id[j]; id[j] = id[j - 1]; id[j - 1] = ti;
-                const float tw = wt[j]; wt[j] = wt[j - 1]; wt[j - 1] = tw;
-            }
-    /* slots need the original k of each id: rank is indexed by (t, k) */
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        sl[k] = -1;
-        if (id[k] >= 0) {
-            int r = 0;
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                if (id0[j] == id[k]) r = rk[j];
-            sl[k] = off[id[k]] + r;
-        }
+    for (int p = 0; p < 8; p++) {
+        const unsigned long long m = __ballot(pos == p && lane < 8);
+        const int src = (int)__builtin_ctzll(m);
+        sl[p] = __builtin_amdgcn_readlane(s, src);
+        wt[p] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), src));
     }
 }
 
@@ -567,15 +561,21 @@ extern "C" __global__ void __launch_bounds__(256) pf_combine16_kernel(const uint
     float wt[8];
     pf_token_slots(ids, w, rank, off, t, sl, wt);
     const size_t shrow = (size_t)8 * T + t;
-    const float g = __builtin_ldexpf(sg[t], oexp[shrow]);
+    /* the rows' scale exponents and the rows themselves in one round trip
+     * (unrouted picks read the shared row, unused) */
+    int ex[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++)
-        if (sl[k] >= 0) wt[k] = __builtin_ldexpf(wt[k], oexp[sl[k]]);
+    for (int k = 0; k < 8; k++) ex[k] = oexp[sl[k] >= 0 ? (size_t)sl[k] : shrow];
+    const int exs = oexp[shrow];
     const int i = min((int)threadIdx.x * 8, H - 8);
     const uint4 s8 = *(const uint4 *)(ed + shrow * H + i);
     uint4 d8[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) d8[k] = *(const uint4 *)(ed + (sl[k] >= 0 ? (size_t)sl[k] : shrow) * H + i);
+    const float g = __builtin_ldexpf(sg[t], exs);
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        if (sl[k] >= 0) wt[k] = __builtin_ldexpf(wt[k], ex[k]);
     if ((int)threadIdx.x * 8 >= H) return;
     const f16x8_t sh = __builtin_bit_cast(f16x8_t, s8);
     float y[8];
