@@ -184,24 +184,23 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
      * gate vector, indices clamped.  A wave's loads complete in order, so
      * the top 8 runs on the logits while the X row is still arriving; the
      * row then stays in registers for the fp16 conversion. */
-    float v4[4], b4[4];
+    float v4[4], b4[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+    /* the router's 4 x RT_KSPLIT partial sums (or the 4 logits) in one
+     * batch, summed in split order once the X row is on its way */
+    const size_t TE = (size_t)A.T * A.E;
+    float p[4][RT_KSPLIT];
+    if (A.logits_in) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int e = min(lane + 64 * i, A.E - 1);
-        const size_t o = (size_t)t * A.E + e;
-        if (A.logits_in) {
-            v4[i] = A.logits_in[o];
-        } else {
-            const size_t TE = (size_t)A.T * A.E;
-            float p[RT_KSPLIT];
+        for (int i = 0; i < 4; i++) v4[i] = A.logits_in[(size_t)t * A.E + min(lane + 64 * i, A.E - 1)];
+    } else {
 #pragma unroll
-            for (int s = 0; s < RT_KSPLIT; s++) p[s] = A.part[s * TE + o];
-            float sum = p[0];
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int s = 1; s < RT_KSPLIT; s++) sum += p[s];
-            v4[i] = sum;
-        }
-        b4[i] = A.bias ? A.bias[e] : 0.0f;
+            for (int s = 0; s < RT_KSPLIT; s++) p[i][s] = A.part[s * TE + (size_t)t * A.E + min(lane + 64 * i, A.E - 1)];
+    }
+    if (A.bias) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) b4[i] = A.bias[min(lane + 64 * i, A.E - 1)];
     }
     const float *x = A.X + (size_t)t * A.H;
     float4 xv[8], gv[8];
@@ -210,6 +209,15 @@ extern "C" __global__ void __launch_bounds__(256) pf_token_kernel(PfTokArgs A)
         const int k = min(4 * lane + 256 * i, A.H - 4);
         xv[i] = *(const float4 *)(x + k);
         gv[i] = *(const float4 *)(A.gate_inp + k);
+    }
+    if (!A.logits_in) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float sum = p[i][0];
+#pragma unroll
+            for (int s = 1; s < RT_KSPLIT; s++) sum += p[i][s];
+            v4[i] = sum;
+        }
     }
     /* logits (+ bias) and the top 8 */
 #pragma unroll
