@@ -66,13 +66,17 @@ struct PfGemmArgs {
 
 /* The balanced down GEMM's units are (tile, PF_DN_ROWS output rows); the plan
  * kernel splits them over the workgroups by a cost model measured on the
- * all-Q6_K and Zipf 2048-wide layers (units of about 0.5 us): a unit of a tile
- * with ms 32-row blocks costs PF_DN_CA + PF_DN_CB * ms, a tile range's start
- * (row scales and activation staging) PF_DN_CP more. */
+ * all-Q6_K and Zipf 2048-wide layers (units of about 0.25 us): a unit of a
+ * tile with ms 32-row blocks costs PF_DN_CA + PF_DN_CB * ms, a tile range's
+ * start (row scales and activation staging) PF_DN_CP more.  PF_DN_CP is below
+ * the measured ~10 us per range start: a range that starts on a tile's first
+ * unit is charged its own start, the others are not, and the lower charge
+ * measured fastest (kernel trace, 8 / 5 / 28 against 8 / 5 / 40 and 4 / 3 / 16
+ * in these units: -1.6 and -2.9 us on the two layers). */
 #define PF_DN_ROWS 256
-#define PF_DN_CA 4
-#define PF_DN_CB 3
-#define PF_DN_CP 24
+#define PF_DN_CA 8
+#define PF_DN_CB 5
+#define PF_DN_CP 28
 
 /* Rows per tile the GEMMs of operand mode op expect in the tile list;
  * mixed_gate_up: the gate and up matrices of some group differ in type. */
