@@ -252,6 +252,14 @@ int roaster_prefill_balanced_down(int enable);
  * least 2048), or one workgroup per unit (0); -1 queries.  Both give
  * bit-identical results.  Returns the mode in force. */
 int roaster_prefill_persistent_gate_up(int enable);
+/* Both fp16-mode GEMMs in one persistent kernel (1, where the persistent
+ * gate/up grid and the balanced down GEMM both apply and the GPU has 8
+ * XCDs): each XCD's workgroups take its share of the tiles' gate/up units,
+ * then their down chunks once a chunk's tile is complete, so the down work
+ * fills the gate/up tail; or two kernels (0, default: the one kernel
+ * measured 1-3% faster, within the spread between boxes); -1 queries.  Both
+ * give bit-identical results.  Returns the mode in force. */
+int roaster_prefill_fused_gemm(int enable);
 
 #ifdef __cplusplus
 }

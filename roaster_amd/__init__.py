@@ -141,6 +141,7 @@ _SIG = {
     "roaster_moe_prefill": (C.c_int, [_P, C.c_int, _P, C.c_int, _P, C.POINTER(RoasterPrefillOpts)]),
     "roaster_prefill_balanced_down": (C.c_int, [C.c_int]),
     "roaster_prefill_persistent_gate_up": (C.c_int, [C.c_int]),
+    "roaster_prefill_fused_gemm": (C.c_int, [C.c_int]),
 }
 
 _lib = None

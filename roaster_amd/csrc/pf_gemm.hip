@@ -1103,8 +1103,16 @@ __device__ __forceinline__ float gp_fwd(const PfGemmArgs &A, int tok)
 
 /* Thread 0: unit index of an issued take (old value of counter x0 + xs);
  * a range that has run out moves on to the next XCD's. */
+template <bool FUSED = false>
 __device__ __forceinline__ int gp_resolve(const PfGemmArgs &A, int old, int &xs, int x0, int U)
 {
+    if constexpr (FUSED) {
+        /* this XCD's tiles only: their SiLU*up rows stay in its L2 for its
+         * own down chunks */
+        const int nblk = A.I / V2_GU_J, lo = A.xcd_tb[x0] * nblk, hi = A.xcd_tb[x0 + 1] * nblk;
+        (void)xs; (void)U;
+        return lo + old < hi ? lo + old : -1;
+    }
     for (;;) {
         const int x = (x0 + xs) & 7;
         const int lo = (int)((long long)x * U / 8), hi = (int)((long long)(x + 1) * U / 8);
@@ -1114,10 +1122,10 @@ __device__ __forceinline__ int gp_resolve(const PfGemmArgs &A, int old, int &xs,
     }
 }
 
-template <int MS, bool Q6>
+template <int MS, bool Q6, bool FUSED = false>
 __device__ __forceinline__ void gp_unit(const PfGemmArgs &A, GuMeta (&meta)[2], int cur, const GuUnit &U, GuUnit &N,
                                         int *s_unit, typename RawOf<Q6>::T (&rg)[2], uint4 (&xr)[6], uint8_t *lds,
-                                        int &xs, int x0, int Uall, int nblk)
+                                        int &xs, int x0, int Uall, int nblk, int sig = -1)
 {
     const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
     const int nkb = A.H / GK;
@@ -1178,8 +1186,14 @@ __device__ __forceinline__ void gp_unit(const PfGemmArgs &A, GuMeta (&meta)[2], 
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
     step(B0(), 0);
-    if (t == 0) s_unit[cur ^ 1] = gp_resolve(A, tk, xs, x0, Uall);
+    if (t == 0) s_unit[cur ^ 1] = gp_resolve<FUSED>(A, tk, xs, x0, Uall);
     lds_barrier();
+    if constexpr (FUSED) {
+        /* the previous unit's rows are stored: every thread has waited for
+         * step 0's activation loads, issued after them (a wave's memory
+         * operations complete in order), before the barrier */
+        if (t == 0 && sig >= 0) __hip_atomic_fetch_add(A.tile_done + sig, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     PF_TSU(U.u, 2);
     const int nu = __builtin_amdgcn_readfirstlane(s_unit[cur ^ 1]);
     const uint32_t ntl = gp_tile_load(A, nu, nblk); /* step 1: the next unit's tile */
@@ -1250,7 +1264,7 @@ __device__ __forceinline__ void gp_unit(const PfGemmArgs &A, GuMeta (&meta)[2], 
     PF_TSU(U.u, 11);
 }
 
-template <bool Q6>
+template <bool Q6, bool FUSED = false>
 __device__ __forceinline__ void gp_body(const PfGemmArgs &A, uint8_t *lds, GuMeta (&meta)[2], int *s_unit)
 {
     const int t = threadIdx.x, l = t & 63, h = l >> 5, w = t >> 6, n = l & 31;
@@ -1264,7 +1278,7 @@ __device__ __forceinline__ void gp_body(const PfGemmArgs &A, uint8_t *lds, GuMet
     int xs = 0;
     if (t == 0) {
         const int old = __hip_atomic_fetch_add(A.gu_ctr + x0, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_unit[0] = gp_resolve(A, old, xs, x0, Uall);
+        s_unit[0] = gp_resolve<FUSED>(A, old, xs, x0, Uall);
     }
     __syncthreads();
     GuUnit U;
@@ -1302,16 +1316,23 @@ __device__ __forceinline__ void gp_body(const PfGemmArgs &A, uint8_t *lds, GuMet
         }
         lds_barrier();
     }
-    int cur = 0;
+    int cur = 0, sig = -1;
     for (;;) {
         GuUnit N;
         const int ms = (U.mlen + 31) >> 5;
-        if (ms == 1) gp_unit<1, Q6>(A, meta, cur, U, N, s_unit, rg, xr, lds, xs, x0, Uall, nblk);
-        else if (ms == 2) gp_unit<2, Q6>(A, meta, cur, U, N, s_unit, rg, xr, lds, xs, x0, Uall, nblk);
-        else gp_unit<3, Q6>(A, meta, cur, U, N, s_unit, rg, xr, lds, xs, x0, Uall, nblk);
+        if (ms == 1) gp_unit<1, Q6, FUSED>(A, meta, cur, U, N, s_unit, rg, xr, lds, xs, x0, Uall, nblk, sig);
+        else if (ms == 2) gp_unit<2, Q6, FUSED>(A, meta, cur, U, N, s_unit, rg, xr, lds, xs, x0, Uall, nblk, sig);
+        else gp_unit<3, Q6, FUSED>(A, meta, cur, U, N, s_unit, rg, xr, lds, xs, x0, Uall, nblk, sig);
+        sig = U.u / nblk;
         if (N.u < 0) break;                         /* workgroup-uniform */
         U = N;
         cur ^= 1;
+    }
+    if constexpr (FUSED) {
+        /* the last unit's rows: its stores complete, then counted */
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        lds_barrier();
+        if (t == 0) __hip_atomic_fetch_add(A.tile_done + sig, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -1606,9 +1627,106 @@ extern "C" __global__ void __launch_bounds__(V2_T) pf2_down_bal_kernel(PfGemmArg
     }
 }
 
+/* The fused kernel's down phase: chunks of PF_FX_CH output tiles of this
+ * XCD's tiles, taken in tile order from the XCD's counter (whole tiles as
+ * the first three quarters' chunks, or chunks of 2 or 3, measured slower:
+ * coarser ends, or more activation stagings).  A chunk starts
+ * once its tile's gate/up units are all counted (thread 0 polls the counter,
+ * at most PF_FX_SPIN times, then reports bit 8 and goes on); the next chunk
+ * is claimed while the current one runs.  The SiLU*up rows it reads were
+ * written by workgroups of the same XCD, so they are in its L2 (and in no
+ * CU's L1: nothing reads them before this). */
+#define PF_FX_CH 4
+#define PF_FX_SPIN (1 << 22)
+__device__ __forceinline__ void dn_fused(const PfGemmArgs &A, uint8_t *lds, V4Shared &meta, int *s_unit)
+{
+    const int t = threadIdx.x;
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    const int x0 = (int)(xcc & 7);
+    const int NT = A.H / V2_DN_N, cps = (NT + PF_FX_CH - 1) / PF_FX_CH, nblk = A.I / V2_GU_J;
+    const int tb0 = A.xcd_tb[x0], ntx = A.xcd_tb[x0 + 1] - tb0;
+    const int nch = ntx * cps;
+    int ev = 0;
+    uint32_t rec = 0;
+    if (t == 0) s_unit[0] = __hip_atomic_fetch_add(A.dn_ctr + x0, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lds_barrier();
+    for (;;) {
+        const int c = __builtin_amdgcn_readfirstlane(s_unit[0]);
+        if (c >= nch) break;                        /* workgroup-uniform */
+        const int ti = tb0 + c / cps, j0 = (c % cps) * PF_FX_CH, cnt = min(PF_FX_CH, NT - j0);
+        rec = dn_rec_load(A, ti);
+        int nextc = 0;
+        if (t == 0) {
+            nextc = __hip_atomic_fetch_add(A.dn_ctr + x0, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            int it = 0;
+            while (__hip_atomic_load(A.tile_done + ti, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < nblk) {
+                if (++it == PF_FX_SPIN) {
+                    __hip_atomic_fetch_or(A.err, 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        lds_barrier();                              /* LDS only: the last chunk's stores stay in flight */
+        auto field = [&](size_t off) { return __builtin_amdgcn_readlane((int)rec, (int)(off / 4)); };
+        const uint8_t *td = (const uint8_t *)(((uint64_t)(uint32_t)field(offsetof(PfDnTile, td) + 4) << 32) |
+                                              (uint32_t)field(offsetof(PfDnTile, td)));
+        const int sbase = field(offsetof(PfDnTile, slot)), mlen = field(offsetof(PfDnTile, mlen));
+        const bool dq6 = field(offsetof(PfDnTile, dq6)) != 0;
+        const float dbnd = __builtin_bit_cast(float, field(offsetof(PfDnTile, dbnd)));
+        const int ms = (mlen + 31) >> 5, n0 = j0 * V2_DN_N;
+        const bool first = j0 == 0;
+#define DN_RANGE(M, Q)                                                                          \
+    do {                                                                                        \
+        if (A.I > GK) v7_dn_range<M, Q, 2>(A, td, sbase, mlen, dbnd, meta, n0, cnt, first, ti, rec, lds, ev); \
+        else v7_dn_range<M, Q, 1>(A, td, sbase, mlen, dbnd, meta, n0, cnt, first, ti, rec, lds, ev);          \
+    } while (0)
+        if (ms == 1) {
+            if (dq6) DN_RANGE(1, true);
+            else DN_RANGE(1, false);
+        } else if (ms == 2) {
+            if (dq6) DN_RANGE(2, true);
+            else DN_RANGE(2, false);
+        } else {
+            if (dq6) DN_RANGE(3, true);
+            else DN_RANGE(3, false);
+        }
+#undef DN_RANGE
+        if (t == 0) s_unit[0] = nextc;
+        lds_barrier();                              /* meta, the staged activations and the claim */
+    }
+}
+
+/* Both fp16 GEMMs in one persistent grid (one workgroup per CU): each XCD's
+ * workgroups take its tiles' gate/up units, then its tiles' down chunks, so
+ * the CUs that run out of gate/up units work on down chunks while the last
+ * units finish, and the down GEMM's start overlaps the gate/up tail. */
+extern "C" __global__ void __launch_bounds__(V2_T) pf2_fused_kernel(PfGemmArgs A)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds4[];
+    __shared__ GuMeta meta[2];
+    __shared__ int s_unit[2];
+    __shared__ V4Shared dmeta;
+    if (A.gu_pers == 2) gp_body<true, true>(A, lds4, meta, s_unit);
+    else gp_body<false, true>(A, lds4, meta, s_unit);
+    __syncthreads();
+    dn_fused(A, lds4, dmeta, s_unit);
+}
+
 /* ---- host ----------------------------------------------------------------- */
 static int g_pf_dn_bal = 1;             /* roaster_prefill_balanced_down */
 static int g_pf_gu_pers = 1;            /* roaster_prefill_persistent_gate_up */
+static int g_pf_fused = 0;              /* roaster_prefill_fused_gemm */
+
+bool pf_fused_enabled() { return g_pf_fused && g_pf_gu_pers && g_pf_dn_bal; }
+
+extern "C" int roaster_prefill_fused_gemm(int enable)
+{
+    std::lock_guard<std::recursive_mutex> g(rt_lock());
+    if (enable == 0 || enable == 1) g_pf_fused = enable;
+    return g_pf_fused;
+}
 
 extern "C" int roaster_prefill_balanced_down(int enable)
 {
@@ -1656,6 +1774,11 @@ int pf_gemm_launch(const PfGemmArgs &A, int max_tiles, int op)
     if (op == PF_BF16) return launch_v1<PF_BF16>(A, max_tiles);
     RtState &R = rt();
     const size_t lds_gu = 2 * (size_t)V3_XBUF * 2, lds_dn = lds_gu;
+    if (A.fused && A.gu_pers && A.dn_tiles && A.out16 && A.xcd_tb) {
+        /* the plan kernel set up the fused kernel's split and counters */
+        hipLaunchKernelGGL(pf2_fused_kernel, dim3(R.n_cu), dim3(V2_T), (size_t)GP_LDS, R.stream, A);
+        return rt_check(hipGetLastError(), "prefill fused GEMM launch") ? ROASTER_EDEVICE : 0;
+    }
     if (A.gu_pers && g_pf_gu_pers)
         hipLaunchKernelGGL(pf2_gu_pers_kernel, dim3(R.n_cu), dim3(V2_T), (size_t)GP_LDS, R.stream, A);
     else

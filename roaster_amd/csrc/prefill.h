@@ -62,7 +62,22 @@ struct PfGemmArgs {
     const PfDnTile *dn_tiles;       /* [max_tiles] the tile list as down records, or NULL */
     int dn_spare;                   /* with dn_tiles: a slot past the last, which takes the balanced down
                                        GEMM's products of rows past a tile's end (never read) */
+    /* both GEMMs in one persistent kernel (with gu_pers and dn_tiles): each
+     * XCD owns tiles [xcd_tb[x], xcd_tb[x + 1]) for both, its workgroups
+     * taking gate/up units, then down chunks whose tile's gate/up units are
+     * done (tile_done[tile] == inter / 128); the plan kernel writes the
+     * bounds and zeroes the counters */
+    int fused;
+    const int *xcd_tb;              /* [9] */
+    int *dn_ctr;                    /* [8] down chunks taken, per XCD */
+    int *tile_done;                 /* [max_tiles] gate/up units done, per tile */
+    int *err;                       /* device error word: bit 8 = a tile wait gave up */
 };
+
+/* Tile weight of the fused kernel's split of the tiles over the XCDs (both
+ * GEMMs' cost of a tile of ms 32-row blocks, in relative units). */
+#define PF_FX_CA 10
+#define PF_FX_CB 3
 
 /* The balanced down GEMM's units are (tile, PF_DN_ROWS output rows); the plan
  * kernel splits them over the workgroups by a cost model measured on the
@@ -77,6 +92,10 @@ struct PfGemmArgs {
 #define PF_DN_CA 8
 #define PF_DN_CB 5
 #define PF_DN_CP 28
+
+/* Whether prefill runs both fp16 GEMMs as one persistent kernel where it can
+ * (roaster_prefill_fused_gemm). */
+bool pf_fused_enabled();
 
 /* Rows per tile the GEMMs of operand mode op expect in the tile list;
  * mixed_gate_up: the gate and up matrices of some group differ in type. */

@@ -340,6 +340,8 @@ struct PfPlanArgs {
     int *gu_ctr;                /* [8] zeroed for the persistent gate/up GEMM */
     int *dn_bnd;                /* [n_wg + 1] the balanced down GEMM's split, or NULL */
     PfDnTile *dn_tiles;         /* the tile list as down records (with dn_bnd) */
+    int *fx;                    /* fused GEMMs: [0, 9) XCD tile bounds, [16, 24) down chunk
+                                   counters, [32, 32 + max tiles) tile counters; or NULL */
     int n_wg;                   /* its workgroups */
     int nt_out;                 /* its units per tile: H / PF_DN_ROWS */
     int T, E;
@@ -399,12 +401,15 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
     const int3 pre = block_scan3_256(make_int3(c, nt, cost), wsum, &tot);
     const int off = pre.x, toff = pre.y, tot_tiles = tot.y;
     const int nsh = (A.T + A.chunk - 1) / A.chunk;
+    /* per group: tile offset and rows (group E: the shared expert); with the
+     * balanced down GEMM, its cost prefix (each tile a range start plus its
+     * units) */
+    if (e < A.E) { s_toff[e] = toff; s_c[e] = c; }
+    if (e == 0) { s_toff[A.E] = tot_tiles; s_c[A.E] = A.T; }
     if (A.dn_bnd) {
-        /* the balanced down GEMM's cost prefix over groups 0..E-1 (routed)
-         * and E (shared), each tile a range start plus its units */
-        if (e < A.E) { s_gc[e] = pre.z; s_toff[e] = toff; s_c[e] = c; }
+        if (e < A.E) s_gc[e] = pre.z;
         if (e == 0) {
-            s_gc[A.E] = tot.z; s_toff[A.E] = tot_tiles; s_c[A.E] = A.T;
+            s_gc[A.E] = tot.z;
             s_gc[A.E + 1] = tot.z + pf_dn_group_cost(A.T, A.chunk, A.nt_out);
         }
     }
@@ -448,6 +453,42 @@ extern "C" __global__ void __launch_bounds__(256) pf_plan_kernel(PfPlanArgs A)
         if (A.dn_bnd)
             A.dn_tiles[tot_tiles + i] = PfDnTile{ A.TL.sdown, 8 * A.T + i * A.chunk, min(A.chunk, A.T - i * A.chunk),
                                                   A.sq6d, sdbnd, { 0, 0 } };
+    }
+    if (A.fx) {
+        /* the fused GEMMs: counters zeroed, and the tiles split over the 8
+         * XCDs by a prefix of tile weights (routed groups, then the shared
+         * one), each bound rounded to a tile */
+        const int ntot = tot_tiles + nsh;
+        for (int i = e; i < ntot; i += 256) A.fx[32 + i] = 0;
+        if (e < 8) A.fx[16 + e] = 0;
+        auto tw = [&](int rows) { return PF_FX_CA + PF_FX_CB * ((rows + 31) >> 5); };
+        auto gw = [&](int cnt) {
+            if (cnt <= 0) return 0;
+            const int ntg = (cnt + A.chunk - 1) / A.chunk;
+            return (ntg - 1) * tw(A.chunk) + tw(cnt - (ntg - 1) * A.chunk);
+        };
+        __shared__ int s_fw[258];
+        int wall;
+        const int wpre = block_scan_256(e < A.E ? gw(c) : 0, wsum, &wall);
+        if (e < A.E) s_fw[e] = wpre;
+        if (e == 0) { s_fw[A.E] = wall; s_fw[A.E + 1] = wall + gw(A.T); }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (e <= 8) {
+            int tb = e == 0 ? 0 : ntot;
+            if (e > 0 && e < 8) {
+                const int target = (int)((long long)e * s_fw[A.E + 1] / 8);
+                int lo = 0, hi = A.E;              /* the last group g <= E with s_fw[g] <= target */
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (s_fw[mid] <= target) lo = mid; else hi = mid - 1;
+                }
+                const int g = lo, cg = s_c[g];
+                const int ntg = (cg + A.chunk - 1) / A.chunk, off = target - s_fw[g];
+                const int i = min((off + tw(A.chunk) / 2) / tw(A.chunk), ntg);
+                tb = s_toff[g] + i;
+            }
+            A.fx[e] = tb;
+        }
     }
     if (A.dn_bnd) {
         /* the balanced down GEMM's split: workgroup b starts at the unit
@@ -639,6 +680,7 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     RtState &R = rt();
     const size_t o_bnd = op == PF_F16 ? take((size_t)(R.n_cu + 1) * 4) : 0;
     const size_t o_dnt = op == PF_F16 ? take(sizeof(PfDnTile) * max_tiles) : 0;
+    const size_t o_fx = op == PF_F16 ? take((size_t)(32 + max_tiles) * 4) : 0;
     uint8_t *ws = (uint8_t *)rt_scratch(SCR_PF, sz);
     unsigned *ctrl = rt_ctrl();
     if (!ws || !ctrl) return ROASTER_ENOMEM;
@@ -693,6 +735,13 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     pa.gu_ctr = (int *)(ws + o_nt) + 32;            /* its own cache line of the 256-byte slot */
     pa.dn_bnd = op == PF_F16 ? (int *)(ws + o_bnd) : nullptr;
     pa.dn_tiles = op == PF_F16 ? (PfDnTile *)(ws + o_dnt) : nullptr;
+    /* both GEMMs in one persistent kernel: fp16 mode on the persistent gate/up
+     * grid and the balanced down GEMM, 8 XCDs of equal CU counts */
+    const int q6 = LG.q6[0];
+    const bool gu_one = LG.q6[1] == q6 && LG.sh_q6[0] == q6 && LG.sh_q6[1] == q6;
+    const int gu_pers = op == PF_F16 && gu_one && (H / 256) % 2 == 0 && H / 256 >= 8 ? 1 + q6 : 0;
+    const bool fused = gu_pers && I <= 2 * GK && R.n_xcd == 8 && R.n_cu % 8 == 0 && pf_fused_enabled();
+    pa.fx = fused ? (int *)(ws + o_fx) : nullptr;
     pa.n_wg = R.n_cu;
     pa.nt_out = H / PF_DN_ROWS;
     pa.T = T; pa.E = E;
@@ -723,15 +772,16 @@ extern "C" int roaster_moe_prefill(RoasterTable *t, int layer, const float *X, i
     ga.dn_bnd = pa.dn_bnd;
     ga.dn_tiles = pa.dn_tiles;
     ga.dn_spare = (int)slots;                    /* o_ed holds one row past the slots */
-    {
-        /* the persistent gate/up grid takes layers whose routed and shared
-         * gate and up matrices share one type and whose K loop has an even
-         * number (>= 8) of super-block steps */
-        const int q = LG.q6[0];
-        const bool one = LG.q6[1] == q && LG.sh_q6[0] == q && LG.sh_q6[1] == q;
-        ga.gu_pers = op == PF_F16 && one && (H / 256) % 2 == 0 && H / 256 >= 8 ? 1 + q : 0;
-        ga.gu_ctr = pa.gu_ctr;
-    }
+    /* the persistent gate/up grid takes layers whose routed and shared gate
+     * and up matrices share one type and whose K loop has an even number
+     * (>= 8) of super-block steps */
+    ga.gu_pers = gu_pers;
+    ga.gu_ctr = pa.gu_ctr;
+    ga.fused = fused ? 1 : 0;
+    ga.xcd_tb = fused ? pa.fx : nullptr;
+    ga.dn_ctr = fused ? pa.fx + 16 : nullptr;
+    ga.tile_done = fused ? pa.fx + 32 : nullptr;
+    ga.err = (int *)(ctrl + 16);
     if (int rc = pf_gemm_launch(ga, max_tiles, op)) return rc;
 
     if (op == PF_F16)

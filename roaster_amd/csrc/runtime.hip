@@ -140,6 +140,7 @@ int rt_take_err()
     if (e & 4) dec_placement_failed();   /* later launches exchange through memory, groups fixed by index */
     if (e & 4) return rt_fail(ROASTER_EDEVICE, "a decode stack workgroup read an XCC_ID out of range");
     if (e & 2) return rt_fail(ROASTER_EDEVICE, "a decode layer's exchange wait timed out (workgroups not all resident?)");
+    if (e & 8) return rt_fail(ROASTER_EDEVICE, "a fused prefill GEMM's tile wait timed out");
     return rt_fail(ROASTER_EROUTE, "router produced fewer than 8 finite logits for some token");
 }
 

@@ -197,6 +197,32 @@ def test_prefill_persistent_gate_up_bit_exact(request, which, T):
     np.testing.assert_array_equal(Y0, Y1)
 
 
+@pytest.mark.parametrize("which,T", [("cfg3", 512), ("cfg3", 37), ("q6", 2048), ("q6", 300)])
+def test_prefill_fused_gemm_bit_exact(request, which, T):
+    """Both GEMMs in one persistent kernel (each XCD's workgroups take its
+    tiles' gate/up units, then their down chunks once a tile's units are all
+    counted) gives the bits of the two-kernel path: Zipf routing on the Q4_K
+    table (T = 37: some XCDs with one tile or none) and the all-Q6_K table,
+    twice in a row (the counters are re-zeroed by each call's plan kernel);
+    no tile wait gives up (the call reports no error)."""
+    tab = request.getfixturevalue("cfg3" if which == "cfg3" else "q6tab")
+    X = tokens(15, T, start=9000)
+    b = zipf_bias(256, 2) if which == "cfg3" else None
+    lib = R.lib()
+    assert lib.roaster_prefill_fused_gemm(-1) == 0
+    Y0, _, ids0, _, _ = prefill(tab, X, bias=b)
+    try:
+        assert lib.roaster_prefill_fused_gemm(1) == 1
+        Y1, _, ids1, _, _ = prefill(tab, X, bias=b)
+        Y2, _, _, _, _ = prefill(tab, X, bias=b)
+        R.check(lib.roaster_sync(), "sync after the fused calls")
+    finally:
+        lib.roaster_prefill_fused_gemm(0)
+    np.testing.assert_array_equal(ids0, ids1)
+    np.testing.assert_array_equal(Y0, Y1)
+    np.testing.assert_array_equal(Y0, Y2)
+
+
 def test_prefill_fp16_products_scaled_by_their_bound():
     """Down products far outside the fp16 range: expert 3's down matrix with
     every Q6_K block's d scaled by 2^12 and activations 8x larger, so that its
