@@ -369,3 +369,41 @@ def test_prefill_all_q6k_2048_every_token():
         np.testing.assert_array_equal(Yp.view(np.uint32), Y[perm].view(np.uint32))
     finally:
         tab.destroy()
+
+
+@pytest.mark.parametrize("E,H,I", [(64, 1024, 256), (64, 2048, 256), (32, 1536, 1024)])
+def test_prefill_other_shapes(E, H, I):
+    """Shapes beside the model's: inter 256 (the down GEMM's one-K-step
+    tile ranges, four part maxima per row) at hidden 1024 (four output tiles
+    per tile; the gate/up GEMM one workgroup per unit) and 2048 (the
+    persistent gate/up grid, two units per tile), and inter 1024 at hidden
+    1536 (the down GEMM's per-tile grid over four K steps).  fp16 mode
+    against the oracle at the prefill bar, and the down GEMM's balanced
+    split, its per-tile grid and the one-kernel GEMMs bit for bit against
+    each other where they apply."""
+    T = 150
+    tab = SynthTable(41, n_experts=E, hidden=H, inter=I)
+    lib = R.lib()
+    try:
+        X = tokens(16, T, H=H, start=500)
+        lg_in = np.stack([R.synth_normal(17, R.synth_stream(0, t, 7), E) for t in range(T)]).astype(np.float32)
+        Y, lg, ids, w, counts = prefill(tab, X, logits_in=lg_in)
+        rc, Y_ref, ids_ref, _, _ = tab.oracle_layer(0).prefill(X, logits_in=lg_in)
+        assert rc == 0 and np.array_equal(ids_ref, ids)
+        err = rel_err(Y, Y_ref)
+        log(f"prefill E {E} hidden {H} inter {I}: max|d|/max|y| = {err:.3e}")
+        assert err <= TOL
+        try:
+            assert lib.roaster_prefill_balanced_down(0) == 0
+            Y0, _, _, _, _ = prefill(tab, X, logits_in=lg_in)
+        finally:
+            lib.roaster_prefill_balanced_down(1)
+        np.testing.assert_array_equal(Y0, Y)
+        try:
+            assert lib.roaster_prefill_fused_gemm(1) == 1
+            Y1, _, _, _, _ = prefill(tab, X, logits_in=lg_in)
+        finally:
+            lib.roaster_prefill_fused_gemm(0)
+        np.testing.assert_array_equal(Y1, Y)
+    finally:
+        tab.destroy()
