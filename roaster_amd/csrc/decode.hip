@@ -2651,7 +2651,7 @@ __device__ __forceinline__ void stackB_body(const DecArgs &A)
 #pragma unroll
             for (int i = 0; i < 4; i++)
                 if (lane + 64 * i >= E) v4[i] = -INFINITY;
-            topk8_fast(v4, E, ids_s[b], w_s[b], &s_err, &tks[b], &s_ids_rdy[b], li + 1);
+            topk8_fast<true>(v4, E, ids_s[b], w_s[b], &s_err, &tks[b], &s_ids_rdy[b], li + 1);
             if (gw == 0) {
                 if (lane < RTOPK) {
                     const size_t o = ((size_t)li * B + b) * RTOPK + lane;

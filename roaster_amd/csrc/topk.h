@@ -155,10 +155,16 @@ __device__ __forceinline__ unsigned long long topk_ck(uint32_t key, int e)
  * fills slot r.  The rounds of topk8_wave run instead when more than 64 keys
  * qualify (many ties at the threshold, or a group without a selectable
  * logit).  All 64 lanes must be active; S is this wave's scratch. */
+template <bool OPAQUE = false>
 static __device__ void topk8_fast(const float v4in[4], int E, int *ids, float *w, int *bad, TopkScratch *S,
                                   int *ready = nullptr, int ready_val = 0)
 {
-    const int lane = threadIdx.x & 63;
+    /* OPAQUE: the scratch addresses are computed at each call, not hoisted
+     * out of a caller's loop (where, held across its other work, they were
+     * spilled to scratch memory in the batched decode stack) */
+    int lane_v = (int)threadIdx.x & 63;
+    if constexpr (OPAQUE) asm volatile("" : "+v"(lane_v));
+    const int lane = lane_v;
     uint32_t key[4];
     topk_keys(v4in, E, key);
     uint32_t g = max(max(key[0], key[1]), max(key[2], key[3]));
