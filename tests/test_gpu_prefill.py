@@ -197,12 +197,12 @@ def test_prefill_persistent_gate_up_bit_exact(request, which, T):
     np.testing.assert_array_equal(Y0, Y1)
 
 
-@pytest.mark.parametrize("which,T", [("cfg3", 512), ("cfg3", 37), ("q6", 2048), ("q6", 300)])
+@pytest.mark.parametrize("which,T", [("cfg3", 512), ("cfg3", 37), ("cfg3", 3), ("cfg3", 1), ("q6", 2048), ("q6", 300)])
 def test_prefill_fused_gemm_bit_exact(request, which, T):
     """Both GEMMs in one persistent kernel (each XCD's workgroups take its
     tiles' gate/up units, then their down chunks once a tile's units are all
     counted) gives the bits of the two-kernel path: Zipf routing on the Q4_K
-    table (T = 37: some XCDs with one tile or none) and the all-Q6_K table,
+    table (T = 37, 3, 1: XCDs with one tile or none) and the all-Q6_K table,
     twice in a row (the counters are re-zeroed by each call's plan kernel);
     no tile wait gives up (the call reports no error)."""
     tab = request.getfixturevalue("cfg3" if which == "cfg3" else "q6tab")
